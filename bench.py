@@ -1,0 +1,232 @@
+"""Benchmark of the KDA BT=16 forward on one MI355X.
+
+Workload: BASELINE configs[2], B=1 T=8192 H=32 K=V=128, bf16 q/k/v/g/beta,
+A_log = log U(1,16), dt_bias ~N(0, 0.1), zero initial state, final state
+returned, all in-kernel flags on (lower_bound -5, scale 128^-0.5).  A step is
+one kda_bt16_fwd over that batch with inputs already resident in HBM.
+
+Prints ONE JSON line with the throughput (tokens/s), the roofline of the
+dominant kernel measured with HIP events on the launch stream, and the CPU
+restatement of the reference chunked path timed on this host.
+
+  python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "kda-ascendc_amd"))
+
+from kda_bt16 import kda_bt16_fwd, kda_bt16_stage_launchers  # noqa: E402
+
+METRIC = "KDA fwd tokens/sec and ms at B=1 T=8192 H=32 bf16; % HBM/MFMA roofline"
+B, T, H, D = 1, 8192, 32, 128
+LOWER_BOUND = -5.0
+SCALE = D ** -0.5
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+# Published reference latency for this shape (Ascend 910B3, README.md:53): 20.5 ms.
+REF_MS = 20.5
+
+
+def make_inputs(seed: int = 42):
+    """BASELINE.json generators on the CPU: seed 42, order q, k, v, g_raw,
+    beta_raw (N(0,1), stored bf16), A_log = log U(1,16), dt_bias ~N(0,0.1)."""
+    gen = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, T, H, D, generator=gen).to(torch.bfloat16)
+    k = torch.randn(B, T, H, D, generator=gen).to(torch.bfloat16)
+    v = torch.randn(B, T, H, D, generator=gen).to(torch.bfloat16)
+    g = torch.randn(B, T, H, D, generator=gen).to(torch.bfloat16)
+    beta = torch.randn(B, T, H, generator=gen).to(torch.bfloat16)
+    A_log = torch.log(torch.rand(H, generator=gen) * 15.0 + 1.0)
+    dt_bias = torch.randn(H * D, generator=gen) * 0.1
+    return q, k, v, g, beta, A_log, dt_bias
+
+
+def algorithmic_bytes():
+    """Algorithmic HBM bytes of one forward, split by the kernel that moves
+    them: stage 1 reads q, k, v (2 B), g (2 B), beta (2 B) per token-head
+    element plus A_log/dt_bias; stage 2 writes o (2 B) and the fp32 final
+    state.  Total = 1282 B per token-head + states."""
+    nth = B * T * H
+    k1 = nth * (3 * D * 2 + D * 2 + 2) + H * (4 + 4 * D)
+    k2 = nth * D * 2 + B * H * D * D * 4
+    return k1, k2
+
+
+def matmul_flops():
+    nch = B * H * math.ceil(T / 16)
+    k1 = nch * 4 * (2 * 16 * 16 * D)
+    k2 = nch * (3 * (2 * 16 * D * D) + 2 * 16 * 16 * D)
+    return k1, k2
+
+
+def time_events(fn, reps: int) -> float:
+    """Average ms per call over ``reps`` calls, HIP events on the current stream."""
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def cpu_baseline(inputs) -> dict:
+    """The CPU restatement of the reference chunked path (oracle/kda_oracle.py),
+    timed on this host over the full workload once (about 10 s on 8 cores)."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    from kda_oracle import chunked_reference  # checker/baseline only, never the product
+
+    q, k, v, g, beta, A_log, dt_bias = inputs
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    # warm up on a small slice
+    chunked_reference(q[:, :64, :2], k[:, :64, :2], v[:, :64, :2], g[:, :64, :2].float(),
+                      beta[:, :64, :2].float(), SCALE, A_log=A_log[:2], dt_bias=dt_bias[:2 * D],
+                      lower_bound=LOWER_BOUND)
+    t0 = time.perf_counter()
+    chunked_reference(q, k, v, g.float(), beta.float(), SCALE, A_log=A_log, dt_bias=dt_bias,
+                      lower_bound=LOWER_BOUND)
+    dt = time.perf_counter() - t0
+    cpu_model = platform.processor() or ""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": B * T / dt,
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"full workload B={B} T={T} H={H}, 1 rep after a small warmup, "
+                  f"{dt:.2f} s, torch CPU fp32 with bf16 rounding points, {cpu_model}",
+    }
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the forward shards over (batch, head) with no "
+              "communication, so every GPU runs this same single-GPU workload on its share; "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(2)
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    inputs_cpu = make_inputs()
+    q, k, v, g, beta, A_log, dt_bias = (x.to(dev) for x in inputs_cpu)
+    kw = dict(scale=SCALE, output_final_state=True, use_qk_l2norm_in_kernel=True,
+              use_gate_in_kernel=True, use_beta_sigmoid_in_kernel=True,
+              lower_bound=LOWER_BOUND, A_log=A_log, dt_bias=dt_bias)
+
+    def step():
+        return kda_bt16_fwd(q, k, v, g, beta, **kw)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    # timed region: synchronize on both sides, exactly `steps` forwards
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    # per-call latency distribution with HIP events
+    lat = []
+    for _ in range(max(args.steps, 5)):
+        lat.append(time_events(step, 1))
+    lat.sort()
+
+    # per-kernel durations with HIP events on the launch stream
+    k1, k2, _, _ = kda_bt16_stage_launchers(q, k, v, g, beta, output_final_state=True,
+                                            A_log=A_log, dt_bias=dt_bias, lower_bound=LOWER_BOUND)
+    k1(); k2()
+    reps = max(args.steps, 10)
+    k1_ms = time_events(k1, reps)
+    k2_ms = time_events(k2, reps)
+    by1, by2 = algorithmic_bytes()
+    fl1, fl2 = matmul_flops()
+    kern = {
+        "k1": {"ms": k1_ms, "alg_bytes": by1, "alg_gbs": by1 / k1_ms / 1e6,
+               "tflops": fl1 / k1_ms / 1e9},
+        "k2": {"ms": k2_ms, "alg_bytes": by2, "alg_gbs": by2 / k2_ms / 1e6,
+               "tflops": fl2 / k2_ms / 1e9},
+    }
+    dom = "k1" if k1_ms >= k2_ms else "k2"
+    achieved = kern[dom]["alg_gbs"]
+    tot_bytes = by1 + by2
+    roofline = {
+        "bound": "hbm",
+        "kernel": dom,
+        "achieved": round(achieved, 2),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 5),
+        "traffic": None,
+        "forward_alg_bytes": tot_bytes,
+        "forward_alg_gbs": round(tot_bytes / wall_ms / 1e6, 2),
+        "forward_mfma_frac": round((fl1 + fl2) / wall_ms / 1e9 / BF16_PEAK_TFLOPS, 6),
+        "kernels": {n: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
+                        for kk, vv in d.items()} for n, d in kern.items()},
+    }
+
+    result = {
+        "metric": METRIC,
+        "value": round(B * T / (wall_ms / 1e3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round((B * T / (wall_ms / 1e3)) / (B * T / (REF_MS / 1e3)), 2),
+        "baseline_ref": "reference kda_bt16_fwd 20.5 ms at this shape on Ascend 910B3 (README.md:53)",
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"kda_bt16_fwd B={B} T={T} H={H} K=V={D} (BASELINE configs[2]), "
+                        "zero h0, final state out, all in-kernel flags",
+            "global_batch": B,
+            "seq_len": T,
+            "heads": H,
+            "parallelism": "none (1 GPU)",
+        },
+        "latency_ms": {"p20": round(lat[len(lat) // 5], 4),
+                       "median": round(statistics.median(lat), 4),
+                       "p80": round(lat[(4 * len(lat)) // 5], 4)},
+        "roofline": roofline,
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(inputs_cpu)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

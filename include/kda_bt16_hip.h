@@ -1,0 +1,123 @@
+/*
+ * kda_bt16_hip.h -- C ABI of libkda_bt16_hip.so, the MI355X (gfx950) KDA
+ * BT=16 chunked forward.
+ *
+ * The reference exposes this path only as Python/Triton:
+ *   kda_bt16_fwd    /root/reference/src/kda_bt16/kernels.py:752-810
+ *   kda_bt16_debug  /root/reference/src/kda_bt16/kernels.py:813-850
+ *   _run (host driver, two launches)  kernels.py:475-606
+ *   kda_bt16_kernel_k1 (intra-chunk)  kernels.py:53-184
+ *   kda_bt16_kernel_k2 (state/output) kernels.py:187-302
+ * The entry points below are what a binding of that path calls: device
+ * pointers, sizes and flags only, no framework types.  Every call is
+ * asynchronous on the caller's HIP stream and returns 0 or a negative
+ * KDA_BT16_E* code; nothing is allocated inside the library.
+ *
+ * Tensor layouts (all row-major, contiguous, on one device):
+ *   q, k      [B, T, H, 128]  bf16
+ *   v         [B, T, H, 128]  bf16            (HV == H)
+ *   g         [B, T, H, 128]  fp32 or bf16    raw gate, or the precomputed
+ *                                             chunk-local log2 cumsum
+ *   beta      [B, T, H]       fp32 or bf16
+ *   A_log     [H]             fp32
+ *   dt_bias   [H * 128]       fp32 (optional)
+ *   h0, ht    [B, H, 128, 128] fp32, [V, K] if KDA_BT16_STATE_V_FIRST is
+ *                             set, else [K, V] (optional)
+ *   o         [B, T, H, 128]  bf16
+ * Debug outputs (optional, reference layouts, kernels.py:572-579):
+ *   dbg_Aqk, dbg_A_inv [B, T, H, 16] bf16; dbg_w, dbg_u [B, T, H, 128] bf16;
+ *   dbg_g [B, T, H, 128] fp32.
+ */
+#ifndef KDA_BT16_HIP_H
+#define KDA_BT16_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KDA_BT16_ABI_VERSION 1
+
+/* Flags: the reference's tl.constexpr switches (kernels.py:78-82, 208-212).
+ * USE_INITIAL_STATE / STORE_FINAL_STATE / HAS_BIAS / STORE_A_INV follow from
+ * which pointers are non-NULL and need no flag. */
+#define KDA_BT16_USE_GATE          (1u << 0) /* USE_GATE          kernels.py:115 */
+#define KDA_BT16_USE_QK_L2NORM     (1u << 1) /* USE_QK_L2NORM     kernels.py:108 */
+#define KDA_BT16_USE_BETA_SIGMOID  (1u << 2) /* USE_BETA_SIGMOID  kernels.py:98  */
+#define KDA_BT16_STATE_V_FIRST     (1u << 3) /* STATE_V_FIRST     kernels.py:218 */
+
+/* Element types of g and beta. */
+#define KDA_BT16_DTYPE_F32  0
+#define KDA_BT16_DTYPE_BF16 1
+
+/* Error codes. */
+#define KDA_BT16_OK                 0
+#define KDA_BT16_EINVAL            -1 /* null pointer, non-positive size, bad dtype tag,
+                                         misaligned tensor (16 B; beta its element size;
+                                         Aqk/A_inv 8 B) */
+#define KDA_BT16_EUNSUPPORTED      -2 /* K != 128, V != 128 or HV != H (kernels.py:727-730) */
+#define KDA_BT16_EWORKSPACE        -3 /* workspace missing or smaller than kda_bt16_workspace_bytes */
+#define KDA_BT16_ELAUNCH           -4 /* HIP launch error */
+#define KDA_BT16_EABI              -5 /* args->abi_version != KDA_BT16_ABI_VERSION */
+#define KDA_BT16_ERANGE            -6 /* lower_bound outside (-11, 0) with USE_GATE (kernels.py:733-744) */
+
+typedef struct KdaBt16Args {
+    int32_t abi_version; /* KDA_BT16_ABI_VERSION */
+    int32_t B, T, H, HV, K, V;
+    uint32_t flags;      /* KDA_BT16_* flag bits */
+    float scale;         /* already resolved: the API substitutes K**-0.5 for None */
+    float lower_bound;
+    int32_t g_dtype;     /* KDA_BT16_DTYPE_* */
+    int32_t beta_dtype;  /* KDA_BT16_DTYPE_* */
+    const void* q;
+    const void* k;
+    const void* v;
+    const void* g;
+    const void* beta;
+    const float* A_log;   /* required with USE_GATE */
+    const float* dt_bias; /* optional */
+    const float* h0;      /* optional initial state */
+    void* o;              /* required */
+    float* ht;            /* optional final state */
+    void* workspace;      /* kda_bt16_workspace_bytes() bytes, 256-byte aligned */
+    size_t workspace_bytes;
+    void* dbg_Aqk;        /* optional debug outputs, all or none */
+    void* dbg_A_inv;
+    void* dbg_w;
+    void* dbg_u;
+    float* dbg_g;
+} KdaBt16Args;
+
+/* Bytes of scratch the two stages exchange for this geometry (one 17 KiB
+ * record per (batch, head, 16-token chunk)).  Replaces the reference's
+ * intermediate allocations Aqk / Akk_scratch / w / u / g_cumsum,
+ * kernels.py:572-579.  Returns 0 for an unsupported geometry. */
+size_t kda_bt16_workspace_bytes(int32_t B, int32_t T, int32_t H, int32_t K, int32_t V);
+
+/* Full forward: stage 1 then stage 2 on `stream` (a hipStream_t; NULL is the
+ * legacy default stream).  Replaces _run's two launches, kernels.py:581-602. */
+int kda_bt16_fwd_hip(const KdaBt16Args* args, void* stream);
+
+/* Stage 1 only: per-chunk gates, grams, (I+L)^-1 solve and W/U into the
+ * workspace, plus the debug outputs when given.  Replaces the
+ * kda_bt16_kernel_k1 launch, kernels.py:581-592. */
+int kda_bt16_k1_hip(const KdaBt16Args* args, void* stream);
+
+/* Stage 2 only: the serial state recurrence over the records stage 1 wrote;
+ * writes o and ht.  Replaces the kda_bt16_kernel_k2 launch,
+ * kernels.py:593-602. */
+int kda_bt16_k2_hip(const KdaBt16Args* args, void* stream);
+
+/* Static message for an error code. */
+const char* kda_bt16_strerror(int code);
+
+/* KDA_BT16_ABI_VERSION of the built library. */
+int kda_bt16_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KDA_BT16_HIP_H */

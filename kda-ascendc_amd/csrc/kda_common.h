@@ -1,0 +1,133 @@
+// Shared device helpers and the chunk-record layout exchanged by the two
+// stages of the KDA BT=16 forward on gfx950.
+//
+// Record layout.  Stage 1 writes one record per (batch*head, chunk) and
+// stage 2 reads them head by head, chunk after chunk.  Records of one head
+// are contiguous: record index = (b*H + h) * NT + chunk.  Every operand is
+// stored in the register order in which stage 2 feeds it to the matrix
+// cores, so each lane reads its slice with 16-byte loads and no shuffles.
+//
+// Notation: lane l of a 64-wide wave, r = l & 15 (row inside a 16-lane DPP
+// row), q4 = l >> 4 (which of the four 16-lane rows).  A 16-wide column tile
+// index is kt (over K) or vt (over V).  "F order" for a 16x128 matrix M
+// means lane l holds M[r][16*kt + 4*q4 + i] at item 4*kt + i (kt 0..7,
+// i 0..3); "T order" means lane l holds M[4*q4 + i][16*kt + r] at item
+// 4*kt + i.
+//
+//   offset  bytes  content
+//   0       4096   w      bf16, F order               (A operand of w @ h)
+//   4096    4096   qg     bf16, F order  = bf16(q^ * 2^G)
+//   8192    4096   kg     bf16, T order  = bf16(k^ * 2^(G_last - G))
+//   12288   4096   u      bf16, [vt][lane][i] = u[4*q4+i][16*vt+r]
+//   16384    512   Aqk    bf16, [lane][i] = Aqk[r][4*q4+i]
+//   16896    512   decay  fp32, [q4][kt][i] = 2^G_last[16*kt+4*q4+i]
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kda {
+
+constexpr int BT = 16;    // chunk length (kernels.py:40)
+constexpr int DK = 128;   // K == V == 128 (kernels.py:727-728)
+
+constexpr int REC_W = 0;
+constexpr int REC_QG = 4096;
+constexpr int REC_KG = 8192;
+constexpr int REC_U = 12288;
+constexpr int REC_AQK = 16384;
+constexpr int REC_DECAY = 16896;
+constexpr int REC_BYTES = 17408;
+
+// RCP_LN2 and the l2norm epsilon, kernels.py:38-39.
+constexpr float RCP_LN2 = 1.4426950216f;
+constexpr float L2_EPS = 1e-6f;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+struct Params {
+    const uint16_t* q;
+    const uint16_t* k;
+    const uint16_t* v;
+    const void* g;
+    const void* beta;
+    const float* A_log;
+    const float* dt_bias;
+    const float* h0;
+    uint16_t* o;
+    float* ht;
+    uint8_t* ws;
+    uint16_t* dbg_Aqk;
+    uint16_t* dbg_A_inv;
+    uint16_t* dbg_w;
+    uint16_t* dbg_u;
+    float* dbg_g;
+    int B, T, H, NT;
+    float scale, lower_bound;
+    int g_bf16, beta_bf16;
+    int use_gate, use_l2norm, use_beta_sigmoid, state_v_first;
+};
+
+// bf16 <-> fp32.  fp32 -> bf16 rounds to nearest even (the hardware
+// conversion on gfx950), matching torch's .to(torch.bfloat16).
+__device__ __forceinline__ float bf2f(uint16_t h) {
+    return __builtin_bit_cast(float, (uint32_t)h << 16);
+}
+__device__ __forceinline__ uint16_t f2bf(float x) {
+    return __builtin_bit_cast(uint16_t, (__bf16)x);
+}
+// Round a float to the nearest bf16 value and return it as float.
+__device__ __forceinline__ float round_bf(float x) { return bf2f(f2bf(x)); }
+
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+    return (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
+}
+
+// Inclusive prefix sum over the 16 lanes of a DPP row (row_shr:1,2,4,8).
+// Lanes shifted in from outside the row contribute 0.
+__device__ __forceinline__ float row_scan16(float x) {
+#define KDA_SCAN_STEP(n)                                                      \
+    x += __builtin_bit_cast(                                                  \
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x),     \
+                                           0x110 + (n), 0xf, 0xf, false));
+    KDA_SCAN_STEP(1)
+    KDA_SCAN_STEP(2)
+    KDA_SCAN_STEP(4)
+    KDA_SCAN_STEP(8)
+#undef KDA_SCAN_STEP
+    return x;
+}
+
+__device__ __forceinline__ float shfl(float x, int src_lane) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_ds_bpermute(src_lane << 2, __builtin_bit_cast(int, x)));
+}
+
+// Matrix-core wrappers (gfx950).  Operand/result layouts for the 16x16
+// shapes: A[m][k] comes from lane m + 16*(k / kpl) item k % kpl, B[k][n]
+// from lane n + 16*(k / kpl) item k % kpl, and D[m][n] lands in lane
+// n + 16*(m / 4) item m % 4, with kpl = 1, 4, 8 for K = 4, 16, 32.
+__device__ __forceinline__ f32x4 mfma_f32_16x16x4(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_bf16_16x16x16(i16x4 a, i16x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_bf16_16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ i16x4 as_i16x4(u32x2 v) { return __builtin_bit_cast(i16x4, v); }
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+}  // namespace kda
+
+// Host-side launchers (defined next to each kernel).
+namespace kda {
+hipError_t launch_k1(const Params& p, hipStream_t stream);
+hipError_t launch_k2(const Params& p, hipStream_t stream);
+}  // namespace kda

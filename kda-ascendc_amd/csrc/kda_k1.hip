@@ -1,0 +1,334 @@
+// Stage 1 of the KDA BT=16 forward: everything that does not depend on the
+// recurrent state, one 64-lane wave per (batch, head, 16-token chunk).
+//
+// Follows kda_bt16_kernel_k1 (/root/reference/src/kda_bt16/kernels.py:53-184)
+// for the math and its bf16 rounding points, and additionally produces the
+// per-chunk operands the reference recomputes inside its serial state loop
+// (kernels.py:253-291): bf16(q^ * 2^G), bf16(k^ * 2^(G_last - G)) and
+// 2^G_last.  Moving them here takes the l2norm and every exp2 off the
+// serial chain of stage 2.
+//
+// Lane l owns row r = l & 15 of the chunk and the 32 columns
+// {16*kt + 4*q4 + i} (q4 = l >> 4), so that
+//   * row reductions (l2norm) are two cross-row shuffles,
+//   * the column cumsum over the 16 rows is a DPP row scan,
+//   * the fp32 grams run on 16x16x4 f32 matrix cores straight from
+//     registers (any fixed assignment of columns to k-slots is a valid
+//     reduction order), landing as Aqk[r][4*q4 + i] in lane (r, q4),
+//   * w comes out of the matrix cores directly in stage 2's operand order.
+#include "kda_common.h"
+
+namespace kda {
+
+namespace {
+
+constexpr int LROW = DK + 8;  // bf16 elements per LDS row (padding spreads banks)
+
+__device__ __forceinline__ void load_bf16x32(const uint16_t* __restrict__ src, bool valid,
+                                             int colbase, float out[32]) {
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) {
+        u32x2 a = {0u, 0u};
+        if (valid) a = *reinterpret_cast<const u32x2*>(src + 16 * kt + colbase);
+        out[4 * kt + 0] = __builtin_bit_cast(float, a.x << 16);
+        out[4 * kt + 1] = __builtin_bit_cast(float, a.x & 0xffff0000u);
+        out[4 * kt + 2] = __builtin_bit_cast(float, a.y << 16);
+        out[4 * kt + 3] = __builtin_bit_cast(float, a.y & 0xffff0000u);
+    }
+}
+
+__device__ __forceinline__ void store_lds_row(uint16_t* lds, int r, int colbase, const float x[32]) {
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) {
+        u32x2 pk = {pack2(x[4 * kt + 0], x[4 * kt + 1]), pack2(x[4 * kt + 2], x[4 * kt + 3])};
+        *reinterpret_cast<u32x2*>(lds + r * LROW + 16 * kt + colbase) = pk;
+    }
+}
+
+// T order read: item 4*kt + i = M[4*q4 + i][16*kt + r], packed for the
+// 16x16x16 bf16 operand of tile kt.
+__device__ __forceinline__ void load_lds_T(const uint16_t* lds, int r, int q4, i16x4 out[8]) {
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) {
+        i16x4 v;
+        v.x = (short)lds[(4 * q4 + 0) * LROW + 16 * kt + r];
+        v.y = (short)lds[(4 * q4 + 1) * LROW + 16 * kt + r];
+        v.z = (short)lds[(4 * q4 + 2) * LROW + 16 * kt + r];
+        v.w = (short)lds[(4 * q4 + 3) * LROW + 16 * kt + r];
+        out[kt] = v;
+    }
+}
+
+__device__ __forceinline__ u32x2 pack4(f32x4 v) {
+    return u32x2{pack2(v.x, v.y), pack2(v.z, v.w)};
+}
+
+__global__ __launch_bounds__(64) void k1_kernel(Params p) {
+    __shared__ __attribute__((aligned(16))) uint16_t s_kb[BT * LROW];
+    __shared__ __attribute__((aligned(16))) uint16_t s_vb[BT * LROW];
+    __shared__ __attribute__((aligned(16))) uint16_t s_kg[BT * LROW];
+    __shared__ __attribute__((aligned(16))) float s_L[BT * BT];
+    __shared__ float s_X[BT * (BT + 1)];
+
+    const int lane = threadIdx.x;
+    const int r = lane & 15;
+    const int q4 = lane >> 4;
+    const int colbase = 4 * q4;
+    const int NT = p.NT, H = p.H, T = p.T;
+    const int c = blockIdx.x % NT;
+    const int bh = blockIdx.x / NT;
+    const int b = bh / H, h = bh - (bh / H) * H;
+    const int t0 = c * BT;
+    const int nvalid = min(BT, T - t0);
+    const bool valid = r < nvalid;
+    const int64_t tok = (int64_t)b * T + t0 + r;  // token of this lane's row
+    const int64_t rowoff = (tok * H + h) * DK;    // element offset of that row
+
+    // ---- loads (kernels.py:97-106); padded rows read as zero -------------
+    float qf[32], kf[32], vf[32], gf[32];
+    load_bf16x32(p.q + rowoff, valid, colbase, qf);
+    load_bf16x32(p.k + rowoff, valid, colbase, kf);
+    load_bf16x32(p.v + rowoff, valid, colbase, vf);
+    if (p.g_bf16) {
+        load_bf16x32(static_cast<const uint16_t*>(p.g) + rowoff, valid, colbase, gf);
+    } else {
+        const float* gsrc = static_cast<const float*>(p.g) + rowoff;
+#pragma unroll
+        for (int kt = 0; kt < 8; ++kt) {
+            f32x4 a = {0.f, 0.f, 0.f, 0.f};
+            if (valid) a = *reinterpret_cast<const f32x4*>(gsrc + 16 * kt + colbase);
+            gf[4 * kt + 0] = a.x;
+            gf[4 * kt + 1] = a.y;
+            gf[4 * kt + 2] = a.z;
+            gf[4 * kt + 3] = a.w;
+        }
+    }
+    float beta = 0.f;
+    if (valid) {
+        const int64_t bi = tok * H + h;
+        beta = p.beta_bf16 ? bf2f(static_cast<const uint16_t*>(p.beta)[bi])
+                           : static_cast<const float*>(p.beta)[bi];
+    }
+    if (p.use_beta_sigmoid) beta = 1.f / (1.f + expf(-beta));
+
+    // ---- q/k l2norm, rounded back to bf16 (kernels.py:108-113) -----------
+    if (p.use_l2norm) {
+        float sq = 0.f, sk = 0.f;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            sq = fmaf(qf[j], qf[j], sq);
+            sk = fmaf(kf[j], kf[j], sk);
+        }
+        sq += __shfl_xor(sq, 16);
+        sk += __shfl_xor(sk, 16);
+        sq += __shfl_xor(sq, 32);
+        sk += __shfl_xor(sk, 32);
+        const float rq = 1.f / sqrtf(sq + L2_EPS);
+        const float rk = 1.f / sqrtf(sk + L2_EPS);
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            qf[j] = round_bf(qf[j] * rq);
+            kf[j] = round_bf(kf[j] * rk);
+        }
+    }
+
+    // ---- gate and chunk-local log2 cumsum (kernels.py:115-124) -----------
+    float G[32];
+    if (p.use_gate) {
+        const float ea = expf(p.A_log[h]);
+        const float* bias = p.dt_bias ? p.dt_bias + h * DK : nullptr;
+#pragma unroll
+        for (int kt = 0; kt < 8; ++kt) {
+            f32x4 bb = {0.f, 0.f, 0.f, 0.f};
+            if (bias) bb = *reinterpret_cast<const f32x4*>(bias + 16 * kt + colbase);
+            const float bv[4] = {bb.x, bb.y, bb.z, bb.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float s = bias ? gf[4 * kt + i] + bv[i] : gf[4 * kt + i];
+                float gate = p.lower_bound * (1.f / (1.f + expf(-(ea * s))));
+                gate = valid ? gate : 0.f;
+                G[4 * kt + i] = row_scan16(gate) * RCP_LN2;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 32; ++j) G[j] = gf[j];
+    }
+
+    // ---- mid-row recentring, grams on matrix cores (kernels.py:129-155) ---
+    const int mid = min(BT / 2, nvalid - 1);
+    const int last = nvalid - 1;
+    const int row0 = lane & 48;
+    float Glast[32];
+    f32x4 acc_qk = {0.f, 0.f, 0.f, 0.f};
+    f32x4 acc_kk = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        const float gmid = shfl(G[j], row0 | mid);
+        Glast[j] = shfl(G[j], row0 | last);
+        const float gm = G[j] - gmid;
+        const float gq = valid ? exp2f(gm) : 0.f;
+        const float gk = valid ? exp2f(-gm) : 0.f;
+        const float Qs = qf[j] * gq;
+        const float Ks = kf[j] * gk;
+        const float Kq = kf[j] * gq;
+        // A = Ks (rows s), B = Qs / Kq (columns t): lane (t, q4) receives
+        // Aqk[t][4*q4 + i] and Akk[t][4*q4 + i].
+        acc_qk = mfma_f32_16x16x4(Ks, Qs, acc_qk);
+        acc_kk = mfma_f32_16x16x4(Ks, Kq, acc_kk);
+    }
+
+    uint8_t* rec = p.ws + ((int64_t)bh * NT + c) * REC_BYTES;
+
+    f32x4 aqk, L;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int s = 4 * q4 + i;
+        aqk[i] = (r >= s) ? acc_qk[i] * p.scale : 0.f;
+        L[i] = (r > s) ? acc_kk[i] * beta : 0.f;
+    }
+    const u32x2 aqk_bf = pack4(aqk);
+    *reinterpret_cast<u32x2*>(rec + REC_AQK + lane * 8) = aqk_bf;
+
+    // ---- (I + L)^-1 by forward substitution (kernels.py:157-167) ---------
+    // Lane r solves column s = r: a[t] = A_inv[t][s], with a[s] = 1,
+    // a[t < s] = 0 and a[t > s] = -sum_{j<t} L[t][j] a[j].
+    *reinterpret_cast<f32x4*>(s_L + r * BT + 4 * q4) = L;
+    __syncthreads();
+    {
+        float a[BT];
+#pragma unroll
+        for (int t = 0; t < BT; ++t) {
+            float acc = 0.f;
+#pragma unroll
+            for (int j4 = 0; j4 < (t + 3) / 4; ++j4) {
+                const f32x4 lr = *reinterpret_cast<const f32x4*>(s_L + t * BT + 4 * j4);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if (4 * j4 + i < t) acc = fmaf(-lr[i], a[4 * j4 + i], acc);
+                }
+            }
+            a[t] = (t > r) ? acc : (t == r ? 1.f : 0.f);
+        }
+        if (q4 == 0) {
+#pragma unroll
+            for (int t = 0; t < BT; ++t) s_X[r * (BT + 1) + t] = a[t];
+        }
+    }
+    __syncthreads();
+    f32x4 ainv;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ainv[i] = s_X[(4 * q4 + i) * (BT + 1) + r];
+    const u32x2 ainv_bf = pack4(ainv);  // A = bf16(A_inv), kernels.py:170
+    const i16x4 A_op = as_i16x4(ainv_bf);
+
+    // ---- W/U operands (kernels.py:171-174) and stage-2 operands ----------
+    float qg[32];
+    {
+        float kb[32], vb[32], kg[32];
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            const float e = exp2f(G[j]);
+            kb[j] = round_bf(round_bf(kf[j] * beta) * e);
+            vb[j] = round_bf(vf[j] * beta);
+            qg[j] = round_bf(qf[j] * e);                      // kernels.py:266
+            kg[j] = round_bf(kf[j] * exp2f(Glast[j] - G[j]));  // kernels.py:283-285
+        }
+        store_lds_row(s_kb, r, colbase, kb);
+        store_lds_row(s_vb, r, colbase, vb);
+        store_lds_row(s_kg, r, colbase, kg);
+    }
+    __syncthreads();
+
+    // u = A @ vb: one 16x16x16 tile per 16 value columns.  The result lands
+    // as u[4*q4 + i][16*vt + r], the order stage 2 subtracts it in.
+    {
+        i16x4 vbT[8];
+        load_lds_T(s_vb, r, q4, vbT);
+#pragma unroll
+        for (int vt = 0; vt < 8; ++vt) {
+            const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+            const f32x4 uacc = mfma_bf16_16x16x16(A_op, vbT[vt], zero);
+            const u32x2 ub = pack4(uacc);
+            *reinterpret_cast<u32x2*>(rec + REC_U + vt * 512 + lane * 8) = ub;
+            if (p.dbg_u) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int row = 4 * q4 + i;
+                    if (row < nvalid) {
+                        const int64_t o = (((int64_t)b * T + t0 + row) * H + h) * DK + 16 * vt + r;
+                        p.dbg_u[o] = (uint16_t)(i == 0 ? ub.x : i == 1 ? (ub.x >> 16)
+                                                : i == 2 ? ub.y : (ub.y >> 16));
+                    }
+                }
+            }
+        }
+    }
+
+    // w^T = kb^T @ A^T: tile kt yields w[r][16*kt + 4*q4 + i] in lane (r, q4),
+    // i.e. w in F order.
+    u32x2 wpk[8];
+    {
+        i16x4 kbT[8];
+        load_lds_T(s_kb, r, q4, kbT);
+#pragma unroll
+        for (int kt = 0; kt < 8; ++kt) {
+            const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+            wpk[kt] = pack4(mfma_bf16_16x16x16(kbT[kt], A_op, zero));
+        }
+    }
+    {
+        u32x4* dst = reinterpret_cast<u32x4*>(rec + REC_W + lane * 64);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            dst[j] = u32x4{wpk[2 * j].x, wpk[2 * j].y, wpk[2 * j + 1].x, wpk[2 * j + 1].y};
+    }
+    {
+        u32x4* dst = reinterpret_cast<u32x4*>(rec + REC_QG + lane * 64);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            dst[j] = u32x4{pack2(qg[8 * j + 0], qg[8 * j + 1]), pack2(qg[8 * j + 2], qg[8 * j + 3]),
+                           pack2(qg[8 * j + 4], qg[8 * j + 5]), pack2(qg[8 * j + 6], qg[8 * j + 7])};
+    }
+    {
+        i16x4 kgT[8];
+        load_lds_T(s_kg, r, q4, kgT);
+        u32x4* dst = reinterpret_cast<u32x4*>(rec + REC_KG + lane * 64);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const u32x2 a = __builtin_bit_cast(u32x2, kgT[2 * j]);
+            const u32x2 bq = __builtin_bit_cast(u32x2, kgT[2 * j + 1]);
+            dst[j] = u32x4{a.x, a.y, bq.x, bq.y};
+        }
+    }
+    if (r == 0) {
+        f32x4* dst = reinterpret_cast<f32x4*>(rec + REC_DECAY + q4 * 128);
+#pragma unroll
+        for (int kt = 0; kt < 8; ++kt)
+            dst[kt] = f32x4{exp2f(Glast[4 * kt + 0]), exp2f(Glast[4 * kt + 1]),
+                            exp2f(Glast[4 * kt + 2]), exp2f(Glast[4 * kt + 3])};
+    }
+
+    // ---- optional reference-layout intermediates (kernels.py:125,153,178-184)
+    if (p.dbg_w && valid) {
+        const int64_t bt16 = (tok * H + h) * BT + 4 * q4;
+        *reinterpret_cast<u32x2*>(p.dbg_Aqk + bt16) = aqk_bf;
+        *reinterpret_cast<u32x2*>(p.dbg_A_inv + bt16) = ainv_bf;
+#pragma unroll
+        for (int kt = 0; kt < 8; ++kt) {
+            *reinterpret_cast<u32x2*>(p.dbg_w + rowoff + 16 * kt + colbase) = wpk[kt];
+            *reinterpret_cast<f32x4*>(p.dbg_g + rowoff + 16 * kt + colbase) =
+                f32x4{G[4 * kt + 0], G[4 * kt + 1], G[4 * kt + 2], G[4 * kt + 3]};
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_k1(const Params& p, hipStream_t stream) {
+    const int64_t grid = (int64_t)p.B * p.H * p.NT;
+    hipLaunchKernelGGL(k1_kernel, dim3((unsigned)grid), dim3(64), 0, stream, p);
+    return hipGetLastError();
+}
+
+}  // namespace kda

@@ -1,0 +1,23 @@
+"""kda_bt16 -- KDA (Kimi Delta Attention) BT=16 chunked forward for MI355X.
+
+Public surface of ``/root/reference/src/kda_bt16/__init__.py:1-16``:
+``kda_bt16_fwd`` and ``kda_bt16_debug`` with the same signatures.  The raw
+Triton kernels the reference also exports are replaced by
+``kda_bt16_stage_launchers`` (stage-1 / stage-2 launch closures over the
+HIP library); ``kda_bt16_kernel_fused`` raises NotImplementedError.
+"""
+
+from .kernels import (
+    kda_bt16_debug,
+    kda_bt16_fwd,
+    kda_bt16_kernel_fused,
+    kda_bt16_stage_launchers,
+)
+
+__all__ = [
+    "kda_bt16_fwd",
+    "kda_bt16_debug",
+    "kda_bt16_kernel_fused",
+    "kda_bt16_stage_launchers",
+]
+__version__ = "0.1.0"

@@ -1,0 +1,58 @@
+"""Build libkda_bt16_hip.so in-tree with hipcc for gfx950.
+
+Usage: ``python -m kda_bt16._build`` (with ``kda-ascendc_amd`` on sys.path),
+or ``build()`` from Python.  The library lands next to this file, where
+:mod:`kda_bt16._hip` loads it from.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+CSRC = PKG_DIR.parent / "csrc"
+INCLUDE = PKG_DIR.parents[1] / "include"
+LIB_NAME = "libkda_bt16_hip.so"
+LIB_PATH = PKG_DIR / LIB_NAME
+SOURCES = ["kda_capi.hip", "kda_k1.hip", "kda_k2.hip"]
+HEADERS = ["kda_common.h"]
+
+ARCH = "gfx950"
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    "-Wall",
+    # Keep the compiler from forming packed fp32 VALU ops.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (looked in $HIPCC, /opt/rocm/bin, PATH)")
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every HIP source into ``libkda_bt16_hip.so``; return its path."""
+    srcs = [str(CSRC / s) for s in SOURCES]
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", *srcs, "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

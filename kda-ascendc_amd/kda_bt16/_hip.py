@@ -1,0 +1,121 @@
+"""ctypes binding of ``libkda_bt16_hip.so`` (C ABI in ``include/kda_bt16_hip.h``).
+
+The library is loaded lazily on first use.  There is no fallback: if the
+library is missing or fails to load, every call raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libkda_bt16_hip.so"
+
+ABI_VERSION = 1
+
+USE_GATE = 1 << 0
+USE_QK_L2NORM = 1 << 1
+USE_BETA_SIGMOID = 1 << 2
+STATE_V_FIRST = 1 << 3
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+
+EXPORTED_SYMBOLS = (
+    "kda_bt16_workspace_bytes",
+    "kda_bt16_fwd_hip",
+    "kda_bt16_k1_hip",
+    "kda_bt16_k2_hip",
+    "kda_bt16_strerror",
+    "kda_bt16_abi_version",
+)
+
+
+class KdaBt16Args(ctypes.Structure):
+    """Mirror of ``struct KdaBt16Args``."""
+
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("B", ctypes.c_int32),
+        ("T", ctypes.c_int32),
+        ("H", ctypes.c_int32),
+        ("HV", ctypes.c_int32),
+        ("K", ctypes.c_int32),
+        ("V", ctypes.c_int32),
+        ("flags", ctypes.c_uint32),
+        ("scale", ctypes.c_float),
+        ("lower_bound", ctypes.c_float),
+        ("g_dtype", ctypes.c_int32),
+        ("beta_dtype", ctypes.c_int32),
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("g", ctypes.c_void_p),
+        ("beta", ctypes.c_void_p),
+        ("A_log", ctypes.c_void_p),
+        ("dt_bias", ctypes.c_void_p),
+        ("h0", ctypes.c_void_p),
+        ("o", ctypes.c_void_p),
+        ("ht", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+        ("dbg_Aqk", ctypes.c_void_p),
+        ("dbg_A_inv", ctypes.c_void_p),
+        ("dbg_w", ctypes.c_void_p),
+        ("dbg_u", ctypes.c_void_p),
+        ("dbg_g", ctypes.c_void_p),
+    ]
+
+
+class KdaHipError(RuntimeError):
+    """A non-zero return code from the HIP library."""
+
+    def __init__(self, fn: str, code: int, msg: str):
+        super().__init__(f"{fn} failed with code {code}: {msg}")
+        self.code = code
+
+
+_lib = None
+_lock = threading.Lock()
+
+
+def lib() -> ctypes.CDLL:
+    """Load (once) and return the library; raise if it is absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise ImportError(
+                f"{LIB_PATH.name} is not built; run `python -m kda_bt16._build` "
+                "(or __graft_entry__.build()) first"
+            )
+        h = ctypes.CDLL(str(LIB_PATH))
+        h.kda_bt16_workspace_bytes.restype = ctypes.c_size_t
+        h.kda_bt16_workspace_bytes.argtypes = [ctypes.c_int32] * 5
+        for name in ("kda_bt16_fwd_hip", "kda_bt16_k1_hip", "kda_bt16_k2_hip"):
+            fn = getattr(h, name)
+            fn.restype = ctypes.c_int
+            fn.argtypes = [ctypes.POINTER(KdaBt16Args), ctypes.c_void_p]
+        h.kda_bt16_strerror.restype = ctypes.c_char_p
+        h.kda_bt16_strerror.argtypes = [ctypes.c_int]
+        h.kda_bt16_abi_version.restype = ctypes.c_int
+        h.kda_bt16_abi_version.argtypes = []
+        got = h.kda_bt16_abi_version()
+        if got != ABI_VERSION:
+            raise ImportError(f"{LIB_PATH.name} has ABI version {got}, expected {ABI_VERSION}")
+        _lib = h
+        return _lib
+
+
+def workspace_bytes(B: int, T: int, H: int, K: int, V: int) -> int:
+    return int(lib().kda_bt16_workspace_bytes(B, T, H, K, V))
+
+
+def call(name: str, args: KdaBt16Args, stream: int) -> None:
+    rc = getattr(lib(), name)(ctypes.byref(args), ctypes.c_void_p(stream))
+    if rc != 0:
+        raise KdaHipError(name, rc, lib().kda_bt16_strerror(rc).decode())

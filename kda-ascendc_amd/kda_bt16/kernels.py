@@ -1,0 +1,454 @@
+"""KDA BT=16 chunked forward on MI355X: the Python API and host driver.
+
+Drop-in for ``/root/reference/src/kda_bt16/kernels.py``:
+
+* :func:`kda_bt16_fwd` and :func:`kda_bt16_debug` keep the reference's
+  signatures, defaults, validation order, messages and exception types
+  (kernels.py:609-850);
+* the two stages run as hand-written gfx950 HIP kernels in
+  ``libkda_bt16_hip.so`` (``csrc/kda_k1.hip``, ``csrc/kda_k2.hip``), called
+  through the C ABI declared in ``include/kda_bt16_hip.h`` on the caller's
+  current stream, with no host synchronisation.
+
+Differences from the reference, all supersets of its contract:
+
+* ``g`` and ``beta`` may be bfloat16 as well as float32 (the kernels widen
+  them to fp32 at load, exactly as the reference's ``.to(tl.float32)``);
+* ``state_v_first=False`` is handled by stage 2 reading/writing the
+  ``[K, V]`` state directly instead of transposing at the boundary
+  (kernels.py:499-510); the values are identical;
+* ``use_fused_kernel=True`` is accepted and runs the same two-stage path
+  (the reference's own test requires the two to agree, tests/test_kda_bt16.py:174-200).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _hip, workspace
+
+# Module-level cache for ``reuse_workspace=True`` (kernels.py:35, 525-536):
+# o / ht alias this cache and are overwritten by the next call with the
+# same geometry.  Not thread safe, like the reference's.
+_WORKSPACE_CACHE: dict[tuple, dict[str, torch.Tensor]] = {}
+
+_RCP_LN2 = 1.4426950216
+_EPS = 1e-6
+_BT = 16
+
+
+def _validate_kda_inputs(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    g: torch.Tensor,
+    beta: torch.Tensor,
+    initial_state: torch.Tensor | None,
+    use_gate_in_kernel: bool,
+    safe_gate: bool,
+    lower_bound: float | None,
+    A_log: torch.Tensor | None,
+    dt_bias: torch.Tensor | None,
+    state_v_first: bool,
+) -> tuple[int, int, int, int, int, int]:
+    """Input contract of kernels.py:609-749, same order and messages.
+
+    Returns ``(B, T, H, K, HV, V)``; raises ``ValueError`` / ``TypeError``.
+    """
+    if q.ndim != 4:
+        raise ValueError(f"q must be 4D [B, T, H, D], got {q.ndim}D with shape {q.shape}")
+    if k.ndim != 4:
+        raise ValueError(f"k must be 4D [B, T, H, D], got {k.ndim}D with shape {k.shape}")
+    if v.ndim != 4:
+        raise ValueError(f"v must be 4D [B, T, HV, V], got {v.ndim}D with shape {v.shape}")
+    if g.ndim != 4:
+        raise ValueError(f"g must be 4D [B, T, HV, D], got {g.ndim}D with shape {g.shape}")
+    if beta.ndim != 3:
+        raise ValueError(f"beta must be 3D [B, T, HV], got {beta.ndim}D with shape {beta.shape}")
+
+    B, T, H, K = q.shape
+    HV, V = v.shape[2], v.shape[-1]
+
+    if B <= 0 or T <= 0 or H <= 0 or K <= 0:
+        raise ValueError(f"q dimensions must be positive, got B={B}, T={T}, H={H}, K={K}")
+    if HV <= 0 or V <= 0:
+        raise ValueError(f"v dimensions must be positive, got HV={HV}, V={V}")
+
+    if not q.is_contiguous():
+        raise ValueError("q must be contiguous (kernel assumes stride [H*K, K, 1])")
+    if not k.is_contiguous():
+        raise ValueError("k must be contiguous")
+    if not v.is_contiguous():
+        raise ValueError("v must be contiguous")
+    if not g.is_contiguous():
+        raise ValueError("g must be contiguous")
+    if not beta.is_contiguous():
+        raise ValueError("beta must be contiguous")
+
+    if q.dtype != torch.bfloat16:
+        raise TypeError(f"q must be bfloat16, got {q.dtype}")
+    if k.dtype != torch.bfloat16:
+        raise TypeError(f"k must be bfloat16, got {k.dtype}")
+    if v.dtype != torch.bfloat16:
+        raise TypeError(f"v must be bfloat16, got {v.dtype}")
+    if use_gate_in_kernel and g.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"g must be float32 when use_gate_in_kernel=True, got {g.dtype}")
+    if g.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"g must be float32 or bfloat16, got {g.dtype}")
+    if beta.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"beta must be float32, got {beta.dtype}")
+
+    if k.shape != q.shape:
+        raise ValueError(f"k.shape {k.shape} must match q.shape {q.shape}")
+    if v.shape != (B, T, HV, V):
+        raise ValueError(f"v.shape {v.shape} must be [B={B}, T={T}, HV={HV}, V={V}]")
+    if g.shape != (B, T, HV, K):
+        raise ValueError(f"g.shape {g.shape} must be [B={B}, T={T}, HV={HV}, K={K}]")
+    if beta.shape != (B, T, HV):
+        raise ValueError(f"beta.shape {beta.shape} must be [B={B}, T={T}, HV={HV}]")
+
+    if not all(x.device == q.device for x in [k, v, g, beta]):
+        raise ValueError(f"All tensors must be on same device as q ({q.device})")
+
+    if initial_state is not None:
+        if not initial_state.is_contiguous():
+            raise ValueError("initial_state must be contiguous")
+        if initial_state.dtype != torch.float32:
+            raise TypeError(f"initial_state must be float32, got {initial_state.dtype}")
+        if initial_state.device != q.device:
+            raise ValueError(f"initial_state device {initial_state.device} must match q ({q.device})")
+        expected_shape = (B, HV, V, K) if state_v_first else (B, HV, K, V)
+        if initial_state.shape != expected_shape:
+            raise ValueError(
+                f"initial_state.shape {initial_state.shape} must be {expected_shape} "
+                f"(state_v_first={state_v_first})"
+            )
+
+    if A_log is not None:
+        if not A_log.is_contiguous():
+            raise ValueError("A_log must be contiguous")
+        if A_log.dtype != torch.float32:
+            raise TypeError(f"A_log must be float32, got {A_log.dtype}")
+        if A_log.device != q.device:
+            raise ValueError("A_log device must match q")
+        if A_log.shape != (HV,):
+            raise ValueError(f"A_log.shape {A_log.shape} must be (HV={HV},)")
+
+    if dt_bias is not None:
+        if not dt_bias.is_contiguous():
+            raise ValueError("dt_bias must be contiguous")
+        if dt_bias.dtype != torch.float32:
+            raise TypeError(f"dt_bias must be float32, got {dt_bias.dtype}")
+        if dt_bias.device != q.device:
+            raise ValueError("dt_bias device must match q")
+        if dt_bias.shape != (HV * K,):
+            raise ValueError(f"dt_bias.shape {dt_bias.shape} must be (HV*K={HV * K},)")
+
+    if K != 128 or V != 128:
+        raise ValueError(f"prototype targets K=V=128, got K={K}, V={V}")
+    if HV != H:
+        raise ValueError(f"prototype targets MHA (HV == H), got HV={HV}, H={H}")
+
+    if use_gate_in_kernel:
+        if not safe_gate:
+            raise ValueError("use_gate_in_kernel requires safe_gate=True")
+        if lower_bound is None:
+            raise ValueError("use_gate_in_kernel requires lower_bound")
+        if not (-11.0 < lower_bound < 0.0):
+            raise ValueError(
+                f"lower_bound must be in range (-11, 0) to prevent fp32 exp2 overflow "
+                f"(BT=16 can amplify exponent by ~8x), got {lower_bound}"
+            )
+        if A_log is None:
+            raise ValueError("use_gate_in_kernel requires A_log")
+
+    return B, T, H, K, HV, V
+
+
+def _require_gpu(q: torch.Tensor) -> None:
+    if q.device.type != "cuda":
+        raise ValueError(
+            f"kda_bt16 runs on a ROCm GPU (torch 'cuda' device); got tensors on {q.device}"
+        )
+
+
+def _aligned(t: torch.Tensor | None, align: int = 16) -> torch.Tensor | None:
+    """The kernels use 16-byte vector loads: copy the rare contiguous view
+    whose storage offset breaks that alignment."""
+    if t is None or t.data_ptr() % align == 0:
+        return t
+    return t.clone()
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _dtype_tag(t: torch.Tensor) -> int:
+    return _hip.DTYPE_BF16 if t.dtype == torch.bfloat16 else _hip.DTYPE_F32
+
+
+def _make_args(
+    q, k, v, g, beta, scale, lower_bound, A_log, dt_bias, h0, o, ht, ws, ws_bytes,
+    flags, dbg=None,
+) -> _hip.KdaBt16Args:
+    B, T, H, K = q.shape
+    HV, V = v.shape[2], v.shape[-1]
+    a = _hip.KdaBt16Args()
+    a.abi_version = _hip.ABI_VERSION
+    a.B, a.T, a.H, a.HV, a.K, a.V = B, T, H, HV, K, V
+    a.flags = flags
+    a.scale = float(scale)
+    a.lower_bound = float(lower_bound) if lower_bound is not None else 0.0
+    a.g_dtype = _dtype_tag(g)
+    a.beta_dtype = _dtype_tag(beta)
+    a.q, a.k, a.v, a.g, a.beta = (x.data_ptr() for x in (q, k, v, g, beta))
+    a.A_log = _ptr(A_log)
+    a.dt_bias = _ptr(dt_bias)
+    a.h0 = _ptr(h0)
+    a.o = _ptr(o)
+    a.ht = _ptr(ht)
+    a.workspace = _ptr(ws)
+    a.workspace_bytes = ws_bytes
+    if dbg is not None:
+        a.dbg_Aqk = dbg["Aqk"].data_ptr()
+        a.dbg_A_inv = dbg["A_inv"].data_ptr()
+        a.dbg_w = dbg["w"].data_ptr()
+        a.dbg_u = dbg["u"].data_ptr()
+        a.dbg_g = dbg["g"].data_ptr()
+    return a
+
+
+def _flags(use_gate: bool, use_l2norm: bool, use_beta_sigmoid: bool, state_v_first: bool) -> int:
+    f = 0
+    if use_gate:
+        f |= _hip.USE_GATE
+    if use_l2norm:
+        f |= _hip.USE_QK_L2NORM
+    if use_beta_sigmoid:
+        f |= _hip.USE_BETA_SIGMOID
+    if state_v_first:
+        f |= _hip.STATE_V_FIRST
+    return f
+
+
+def _run(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    g: torch.Tensor,
+    beta: torch.Tensor,
+    scale: float,
+    initial_state: torch.Tensor | None,
+    output_final_state: bool,
+    use_qk_l2norm_in_kernel: bool,
+    use_gate_in_kernel: bool,
+    use_beta_sigmoid_in_kernel: bool,
+    lower_bound: float,
+    A_log: torch.Tensor | None,
+    dt_bias: torch.Tensor | None,
+    state_v_first: bool,
+    return_intermediates: bool,
+    use_fused: bool = False,
+    reuse_workspace: bool = False,
+):
+    """Host driver, the counterpart of kernels.py:475-606: allocate outputs,
+    lease the workspace, launch stage 1 and stage 2 through the C ABI."""
+    del use_fused  # one production path; see module docstring
+    _require_gpu(q)
+    q, k, v, g, initial_state, dt_bias = (
+        _aligned(x) for x in (q, k, v, g, initial_state, dt_bias))
+    B, T, H, K = q.shape
+    HV, V = v.shape[2], v.shape[-1]
+    dev = q.device
+
+    cache_key = (dev, B, T, H, HV, K, V, k.dtype, return_intermediates)
+    cache = _WORKSPACE_CACHE.get(cache_key) if reuse_workspace else None
+
+    def alloc(name, shape, dtype):
+        if cache is not None:
+            t = cache.get(name)
+            if t is not None and t.shape == shape and t.dtype == dtype:
+                return t
+        t = torch.empty(shape, dtype=dtype, device=dev)
+        if reuse_workspace:
+            _WORKSPACE_CACHE.setdefault(cache_key, {})[name] = t
+        return t
+
+    o = alloc("o", (B, T, HV, V), k.dtype)
+    ht = None
+    if output_final_state:
+        ht = alloc("ht", (B, HV, V, K) if state_v_first else (B, HV, K, V), torch.float32)
+
+    dbg = None
+    if return_intermediates:
+        dbg = {
+            "Aqk": torch.empty((B, T, HV, _BT), dtype=k.dtype, device=dev),
+            "A_inv": torch.empty((B, T, HV, _BT), dtype=k.dtype, device=dev),
+            "w": torch.empty((B, T, HV, K), dtype=k.dtype, device=dev),
+            "u": torch.empty((B, T, HV, V), dtype=k.dtype, device=dev),
+            "g": torch.empty((B, T, HV, K), dtype=torch.float32, device=dev),
+        }
+
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        ws_bytes = _hip.workspace_bytes(B, T, H, K, V)
+        ws = workspace.lease(dev, stream, ws_bytes)
+        args = _make_args(
+            q, k, v, g, beta, scale, lower_bound if use_gate_in_kernel else None,
+            A_log, dt_bias, initial_state, o, ht, ws, ws_bytes,
+            _flags(use_gate_in_kernel, use_qk_l2norm_in_kernel, use_beta_sigmoid_in_kernel,
+                   state_v_first),
+            dbg,
+        )
+        _hip.call("kda_bt16_fwd_hip", args, stream)
+
+    if return_intermediates:
+        return o, ht, dbg
+    return o, ht
+
+
+def kda_bt16_fwd(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    g: torch.Tensor,
+    beta: torch.Tensor,
+    scale: float | None = None,
+    initial_state: torch.Tensor | None = None,
+    output_final_state: bool = False,
+    use_qk_l2norm_in_kernel: bool = False,
+    use_gate_in_kernel: bool = False,
+    use_beta_sigmoid_in_kernel: bool = False,
+    safe_gate: bool = True,
+    lower_bound: float = -5.0,
+    A_log: torch.Tensor | None = None,
+    dt_bias: torch.Tensor | None = None,
+    state_v_first: bool = True,
+    use_fused_kernel: bool = False,
+    reuse_workspace: bool = False,
+) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """KDA forward (reference: kernels.py:752-810).
+
+    Args:
+        q/k: ``[B, T, H, K]``, bf16, ``K == 128``.
+        v: ``[B, T, HV, V]``, bf16, ``HV == H``, ``V == 128``.
+        g: ``[B, T, HV, K]`` fp32 or bf16: the raw gate if
+            ``use_gate_in_kernel``, else the precomputed chunk-local cumsum
+            in the log2 domain.
+        beta: ``[B, T, HV]`` fp32 or bf16; raw logits if
+            ``use_beta_sigmoid_in_kernel``.
+        initial_state: fp32 ``[B, HV, V, K]`` (``state_v_first=True``) or
+            ``[B, HV, K, V]``.
+
+    Returns:
+        ``o`` of shape ``[B, T, HV, V]`` (bf16) and, if
+        ``output_final_state``, the fp32 final state in the same layout as
+        ``initial_state``.
+    """
+    B, T, H, K, HV, V = _validate_kda_inputs(
+        q, k, v, g, beta, initial_state,
+        use_gate_in_kernel, safe_gate, lower_bound,
+        A_log, dt_bias, state_v_first,
+    )
+    if scale is None:
+        scale = K ** -0.5
+    return _run(
+        q, k, v, g, beta, scale, initial_state, output_final_state,
+        use_qk_l2norm_in_kernel, use_gate_in_kernel, use_beta_sigmoid_in_kernel,
+        lower_bound, A_log, dt_bias, state_v_first,
+        return_intermediates=False,
+        use_fused=use_fused_kernel,
+        reuse_workspace=reuse_workspace,
+    )
+
+
+def kda_bt16_debug(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    g: torch.Tensor,
+    beta: torch.Tensor,
+    scale: float | None = None,
+    initial_state: torch.Tensor | None = None,
+    output_final_state: bool = False,
+    use_qk_l2norm_in_kernel: bool = False,
+    use_gate_in_kernel: bool = False,
+    use_beta_sigmoid_in_kernel: bool = False,
+    safe_gate: bool = True,
+    lower_bound: float = -5.0,
+    A_log: torch.Tensor | None = None,
+    dt_bias: torch.Tensor | None = None,
+    state_v_first: bool = True,
+) -> tuple[torch.Tensor, torch.Tensor | None, dict]:
+    """Like :func:`kda_bt16_fwd`, and also return the stage-1 intermediates
+    ``{Aqk, A_inv, w, u, g}`` in the reference's layouts (kernels.py:813-850):
+    ``Aqk``/``A_inv`` ``[B,T,HV,16]`` bf16, ``w``/``u`` ``[B,T,HV,128]`` bf16,
+    ``g`` ``[B,T,HV,128]`` fp32."""
+    B, T, H, K, HV, V = _validate_kda_inputs(
+        q, k, v, g, beta, initial_state,
+        use_gate_in_kernel, safe_gate, lower_bound,
+        A_log, dt_bias, state_v_first,
+    )
+    if scale is None:
+        scale = K ** -0.5
+    return _run(
+        q, k, v, g, beta, scale, initial_state, output_final_state,
+        use_qk_l2norm_in_kernel, use_gate_in_kernel, use_beta_sigmoid_in_kernel,
+        lower_bound, A_log, dt_bias, state_v_first,
+        return_intermediates=True,
+        use_fused=False,
+        reuse_workspace=False,
+    )
+
+
+def kda_bt16_stage_launchers(
+    q, k, v, g, beta, scale=None, initial_state=None, output_final_state=False,
+    use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True, use_beta_sigmoid_in_kernel=True,
+    lower_bound=-5.0, A_log=None, dt_bias=None, state_v_first=True,
+):
+    """Return ``(k1, k2, o, ht)``: zero-argument callables that launch only
+    stage 1 or only stage 2 on the current stream, over buffers allocated
+    once here.  The per-kernel breakdown of bench_bt16.py:85-118 uses the
+    raw Triton kernels for the same purpose."""
+    B, T, H, K, HV, V = _validate_kda_inputs(
+        q, k, v, g, beta, initial_state, use_gate_in_kernel, True, lower_bound,
+        A_log, dt_bias, state_v_first,
+    )
+    _require_gpu(q)
+    if scale is None:
+        scale = K ** -0.5
+    dev = q.device
+    o = torch.empty((B, T, HV, V), dtype=torch.bfloat16, device=dev)
+    ht = None
+    if output_final_state:
+        ht = torch.empty((B, HV, V, K) if state_v_first else (B, HV, K, V),
+                         dtype=torch.float32, device=dev)
+    ws_bytes = _hip.workspace_bytes(B, T, H, K, V)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    args = _make_args(
+        q, k, v, g, beta, scale, lower_bound if use_gate_in_kernel else None,
+        A_log, dt_bias, initial_state, o, ht, ws, ws_bytes,
+        _flags(use_gate_in_kernel, use_qk_l2norm_in_kernel, use_beta_sigmoid_in_kernel,
+               state_v_first),
+    )
+    keep = (q, k, v, g, beta, A_log, dt_bias, initial_state, ws)
+
+    def k1():
+        _ = keep
+        _hip.call("kda_bt16_k1_hip", args, torch.cuda.current_stream(dev).cuda_stream)
+
+    def k2():
+        _ = keep
+        _hip.call("kda_bt16_k2_hip", args, torch.cuda.current_stream(dev).cuda_stream)
+
+    return k1, k2, o, ht
+
+
+def kda_bt16_kernel_fused(*_args, **_kwargs):
+    """The reference's experimental single-kernel variant (kernels.py:305-472)
+    is not built: ``use_fused_kernel=True`` runs the two-stage path."""
+    raise NotImplementedError(
+        "kda_bt16_kernel_fused is not provided on MI355X; "
+        "kda_bt16_fwd(use_fused_kernel=True) runs the two-stage kernels"
+    )

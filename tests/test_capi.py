@@ -1,0 +1,102 @@
+"""The C ABI library loads and exports what include/kda_bt16_hip.h declares;
+host-side argument checks return their error codes without launching (CPU)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from kda_bt16 import _hip
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "kda_bt16_hip.h"
+
+
+def _declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(kda_bt16_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_binding_symbols():
+    assert _declared_functions() == sorted(_hip.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _hip.lib()
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_header_constants_match_binding():
+    text = HEADER.read_text()
+    consts = dict(re.findall(r"#define\s+(KDA_BT16_\w+)\s+\(?([^\s/]+)", text))
+    assert int(consts["KDA_BT16_ABI_VERSION"]) == _hip.ABI_VERSION
+    assert consts["KDA_BT16_USE_GATE"] == "1u" or "1u << 0" in text
+    assert _hip.lib().kda_bt16_abi_version() == _hip.ABI_VERSION
+
+
+def test_struct_layout_matches_header_field_order():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    body = re.search(r"typedef struct KdaBt16Args \{(.*?)\} KdaBt16Args;", text, re.S).group(1)
+    names = []
+    for decl in body.split(";"):
+        decl = decl.strip()
+        if not decl:
+            continue
+        names += [n.strip().lstrip("*") for n in re.sub(r"^.*?\b(?=\w+\s*(,|$))", "", decl).split(",")]
+    fields = [f for f, _ in _hip.KdaBt16Args._fields_]
+    assert names == fields
+
+
+def test_workspace_bytes():
+    ws = _hip.workspace_bytes
+    assert ws(1, 8192, 32, 128, 128) == 32 * 512 * 17408
+    assert ws(2, 1037, 4, 128, 128) == 2 * 4 * 65 * 17408
+    assert ws(1, 16, 1, 64, 128) == 0
+    assert ws(0, 16, 1, 128, 128) == 0
+
+
+def test_strerror_codes():
+    lib = _hip.lib()
+    for code in (0, -1, -2, -3, -4, -5, -6):
+        assert lib.kda_bt16_strerror(code)
+    assert lib.kda_bt16_strerror(-99) == b"unknown error"
+
+
+def _args(**kw):
+    a = _hip.KdaBt16Args()
+    a.abi_version = _hip.ABI_VERSION
+    a.B, a.T, a.H, a.HV, a.K, a.V = 1, 16, 1, 1, 128, 128
+    a.scale = 0.1
+    a.lower_bound = -5.0
+    for name, val in kw.items():
+        setattr(a, name, val)
+    return a
+
+
+@pytest.mark.parametrize("fn", ["kda_bt16_fwd_hip", "kda_bt16_k1_hip", "kda_bt16_k2_hip"])
+def test_argument_checks_return_codes_without_launching(fn):
+    f = getattr(_hip.lib(), fn)
+    assert f(None, None) == -1
+    assert f(ctypes.byref(_args(abi_version=99)), None) == -5
+    assert f(ctypes.byref(_args(K=64)), None) == -2
+    assert f(ctypes.byref(_args(HV=2)), None) == -2
+    assert f(ctypes.byref(_args(T=0)), None) == -1
+    assert f(ctypes.byref(_args(g_dtype=7)), None) == -1
+    assert f(ctypes.byref(_args(flags=_hip.USE_GATE, lower_bound=-12.0)), None) == -6
+    # missing tensors (stage 1 / full) or output (stage 2)
+    assert f(ctypes.byref(_args()), None) == -1
+    with pytest.raises(_hip.KdaHipError, match="code -1"):
+        _hip.call(fn, _args(), 0)
+
+
+def test_workspace_checked_before_launch():
+    fake = 1 << 40  # never dereferenced: the size check fails first
+    a = _args(q=fake, k=fake, v=fake, g=fake, beta=fake, o=fake, workspace=fake, workspace_bytes=100)
+    assert _hip.lib().kda_bt16_fwd_hip(ctypes.byref(a), None) == -3
+    a = _args(q=fake, k=fake, v=fake, g=fake, beta=fake, o=fake, workspace=fake + 8,
+              workspace_bytes=17408)
+    assert _hip.lib().kda_bt16_fwd_hip(ctypes.byref(a), None) == -3

@@ -1,0 +1,121 @@
+"""Host-side contract of kda_bt16_fwd / kda_bt16_debug (CPU only).
+
+Messages and exception types follow _validate_kda_inputs,
+/root/reference/src/kda_bt16/kernels.py:609-749; the first three cases are
+the reference's own test_kda_bt16_input_validation
+(/root/reference/tests/test_torch_reference.py:354-387).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from kda_bt16 import kda_bt16_debug, kda_bt16_fwd, kda_bt16_kernel_fused
+
+B, T, H, D = 1, 32, 2, 128
+
+
+def _inputs():
+    q = torch.randn(B, T, H, D, dtype=torch.bfloat16)
+    k = torch.randn(B, T, H, D, dtype=torch.bfloat16)
+    v = torch.randn(B, T, H, D, dtype=torch.bfloat16)
+    g = torch.randn(B, T, H, D, dtype=torch.float32)
+    beta = torch.randn(B, T, H, dtype=torch.float32)
+    return q, k, v, g, beta
+
+
+@pytest.mark.parametrize("fn", [kda_bt16_fwd, kda_bt16_debug])
+def test_reference_validation_cases(fn):
+    q, k, v, g, beta = _inputs()
+    with pytest.raises(ValueError, match="q must be contiguous"):
+        fn(q.transpose(1, 2), k, v, g, beta, scale=0.0883)
+    with pytest.raises(TypeError, match="k must be bfloat16"):
+        fn(q, k.float(), v, g, beta, scale=0.0883)
+    v_wrong = torch.randn(B, T, H, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="prototype targets K=V=128"):
+        fn(q, k, v_wrong, g, beta, scale=0.0883)
+
+
+def test_shape_and_rank_errors():
+    q, k, v, g, beta = _inputs()
+    with pytest.raises(ValueError, match="q must be 4D"):
+        kda_bt16_fwd(q[0], k, v, g, beta)
+    with pytest.raises(ValueError, match="beta must be 3D"):
+        kda_bt16_fwd(q, k, v, g, beta[..., None])
+    with pytest.raises(ValueError, match="q dimensions must be positive"):
+        kda_bt16_fwd(q[:, :0], k[:, :0], v[:, :0], g[:, :0], beta[:, :0])
+    with pytest.raises(ValueError, match="k.shape"):
+        kda_bt16_fwd(q, k[:, :16], v, g, beta)
+    with pytest.raises(ValueError, match="g.shape"):
+        kda_bt16_fwd(q, k, v, g[:, :16], beta)
+    with pytest.raises(ValueError, match="beta.shape"):
+        kda_bt16_fwd(q, k, v, g, beta[:, :16])
+    with pytest.raises(ValueError, match="beta must be contiguous"):
+        kda_bt16_fwd(q, k, v, g, beta.transpose(1, 2).contiguous().transpose(1, 2))
+
+
+def test_dtype_errors():
+    q, k, v, g, beta = _inputs()
+    with pytest.raises(TypeError, match="q must be bfloat16"):
+        kda_bt16_fwd(q.half(), k, v, g, beta)
+    with pytest.raises(TypeError, match="v must be bfloat16"):
+        kda_bt16_fwd(q, k, v.float(), g, beta)
+    with pytest.raises(TypeError, match="g must be float32 when use_gate_in_kernel=True"):
+        kda_bt16_fwd(q, k, v, g.half(), beta, use_gate_in_kernel=True, A_log=torch.zeros(H))
+    with pytest.raises(TypeError, match="beta must be float32"):
+        kda_bt16_fwd(q, k, v, g, beta.double())
+
+
+def test_state_and_gate_parameter_errors():
+    q, k, v, g, beta = _inputs()
+    h0 = torch.zeros(B, H, D, D)
+    with pytest.raises(TypeError, match="initial_state must be float32"):
+        kda_bt16_fwd(q, k, v, g, beta, initial_state=h0.bfloat16())
+    with pytest.raises(ValueError, match="initial_state.shape"):
+        kda_bt16_fwd(q, k, v, g, beta, initial_state=torch.zeros(B, H, D, 64))
+    with pytest.raises(ValueError, match="initial_state must be contiguous"):
+        kda_bt16_fwd(q, k, v, g, beta, initial_state=h0.transpose(-1, -2))
+    with pytest.raises(ValueError, match="A_log.shape"):
+        kda_bt16_fwd(q, k, v, g, beta, A_log=torch.zeros(H + 1))
+    with pytest.raises(TypeError, match="A_log must be float32"):
+        kda_bt16_fwd(q, k, v, g, beta, A_log=torch.zeros(H, dtype=torch.float64))
+    with pytest.raises(ValueError, match="dt_bias.shape"):
+        kda_bt16_fwd(q, k, v, g, beta, dt_bias=torch.zeros(H))
+    with pytest.raises(ValueError, match="use_gate_in_kernel requires safe_gate=True"):
+        kda_bt16_fwd(q, k, v, g, beta, use_gate_in_kernel=True, safe_gate=False, A_log=torch.zeros(H))
+    with pytest.raises(ValueError, match="lower_bound must be in range"):
+        kda_bt16_fwd(q, k, v, g, beta, use_gate_in_kernel=True, lower_bound=-11.0, A_log=torch.zeros(H))
+    with pytest.raises(ValueError, match="lower_bound must be in range"):
+        kda_bt16_fwd(q, k, v, g, beta, use_gate_in_kernel=True, lower_bound=0.0, A_log=torch.zeros(H))
+    with pytest.raises(ValueError, match="use_gate_in_kernel requires A_log"):
+        kda_bt16_fwd(q, k, v, g, beta, use_gate_in_kernel=True)
+
+
+def test_mha_only():
+    q, k, v, g, beta = _inputs()
+    v2 = torch.randn(B, T, 2 * H, D, dtype=torch.bfloat16)
+    g2 = torch.randn(B, T, 2 * H, D)
+    b2 = torch.randn(B, T, 2 * H)
+    with pytest.raises(ValueError, match="prototype targets MHA"):
+        kda_bt16_fwd(q, k, v2, g2, b2)
+
+
+def test_valid_cpu_inputs_are_refused_before_launch():
+    """Valid shapes on the CPU: refused with a clear error, no launch and no
+    CPU fallback."""
+    q, k, v, g, beta = _inputs()
+    with pytest.raises(ValueError, match="ROCm GPU"):
+        kda_bt16_fwd(q, k, v, g, beta, use_gate_in_kernel=True, A_log=torch.zeros(H))
+
+
+def test_bf16_gate_and_beta_are_accepted_by_validation():
+    q, k, v, g, beta = _inputs()
+    with pytest.raises(ValueError, match="ROCm GPU"):
+        kda_bt16_fwd(q, k, v, g.bfloat16(), beta.bfloat16(), use_gate_in_kernel=True,
+                     A_log=torch.zeros(H))
+
+
+def test_fused_kernel_symbol_raises():
+    with pytest.raises(NotImplementedError):
+        kda_bt16_kernel_fused()
