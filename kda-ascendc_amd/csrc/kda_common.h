@@ -15,12 +15,15 @@
 // 4*kt + i.
 //
 //   offset  bytes  content
-//   0       4096   w      bf16, F order               (A operand of w @ h)
-//   4096    4096   qg     bf16, F order  = bf16(q^ * 2^G)
-//   8192    4096   kg     bf16, T order  = bf16(k^ * 2^(G_last - G))
+//   0       4096   w      bf16, F order, stored [j][lane][8]: the 16-byte
+//                         operand j (k-tiles 2j, 2j+1) of each lane
+//   4096    4096   qg     bf16, F order, [j][lane][8]  = bf16(q^ * 2^G)
+//   8192    4096   kg     bf16, T order, [j][lane][8]  = bf16(k^ * 2^(G_last - G))
 //   12288   4096   u      bf16, [vt][lane][i] = u[4*q4+i][16*vt+r]
 //   16384    512   Aqk    bf16, [lane][i] = Aqk[r][4*q4+i]
-//   16896    512   decay  fp32, [q4][kt][i] = 2^G_last[16*kt+4*q4+i]
+//   16896    512   decay  fp32, [kt][q4][i] = 2^G_last[16*kt+4*q4+i]
+// Consecutive lanes touch consecutive 16-byte words, so both the global
+// accesses and stage 2's LDS reads are conflict free.
 #pragma once
 
 #include <hip/hip_runtime.h>

@@ -278,34 +278,32 @@ __global__ __launch_bounds__(64) void k1_kernel(Params p) {
         }
     }
     {
-        u32x4* dst = reinterpret_cast<u32x4*>(rec + REC_W + lane * 64);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            dst[j] = u32x4{wpk[2 * j].x, wpk[2 * j].y, wpk[2 * j + 1].x, wpk[2 * j + 1].y};
+            *reinterpret_cast<u32x4*>(rec + REC_W + j * 1024 + lane * 16) =
+                u32x4{wpk[2 * j].x, wpk[2 * j].y, wpk[2 * j + 1].x, wpk[2 * j + 1].y};
     }
     {
-        u32x4* dst = reinterpret_cast<u32x4*>(rec + REC_QG + lane * 64);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            dst[j] = u32x4{pack2(qg[8 * j + 0], qg[8 * j + 1]), pack2(qg[8 * j + 2], qg[8 * j + 3]),
+            *reinterpret_cast<u32x4*>(rec + REC_QG + j * 1024 + lane * 16) = u32x4{pack2(qg[8 * j + 0], qg[8 * j + 1]), pack2(qg[8 * j + 2], qg[8 * j + 3]),
                            pack2(qg[8 * j + 4], qg[8 * j + 5]), pack2(qg[8 * j + 6], qg[8 * j + 7])};
     }
     {
         i16x4 kgT[8];
         load_lds_T(s_kg, r, q4, kgT);
-        u32x4* dst = reinterpret_cast<u32x4*>(rec + REC_KG + lane * 64);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const u32x2 a = __builtin_bit_cast(u32x2, kgT[2 * j]);
             const u32x2 bq = __builtin_bit_cast(u32x2, kgT[2 * j + 1]);
-            dst[j] = u32x4{a.x, a.y, bq.x, bq.y};
+            *reinterpret_cast<u32x4*>(rec + REC_KG + j * 1024 + lane * 16) =
+                u32x4{a.x, a.y, bq.x, bq.y};
         }
     }
     if (r == 0) {
-        f32x4* dst = reinterpret_cast<f32x4*>(rec + REC_DECAY + q4 * 128);
 #pragma unroll
         for (int kt = 0; kt < 8; ++kt)
-            dst[kt] = f32x4{exp2f(Glast[4 * kt + 0]), exp2f(Glast[4 * kt + 1]),
+            *reinterpret_cast<f32x4*>(rec + REC_DECAY + kt * 64 + q4 * 16) = f32x4{exp2f(Glast[4 * kt + 0]), exp2f(Glast[4 * kt + 1]),
                             exp2f(Glast[4 * kt + 2]), exp2f(Glast[4 * kt + 3])};
     }
 

@@ -20,36 +20,43 @@ namespace kda {
 
 namespace {
 
-struct Chunk {
-    u32x4 w[4];
-    u32x4 qg[4];
-    u32x2 kg[8];
-    u32x2 u;
-    u32x2 aqk;
-    f32x4 decay[8];
-};
+// Records are streamed through an LDS ring of RING slots with the gfx950
+// direct global->LDS loads (global_load_lds_dwordx4: 64 lanes x 16 B =
+// 1 KiB per instruction, 17 per record), issued RING-1 chunks ahead of use.
+// The loads complete in issue order, so before reading slot c the wave
+// waits until at most 17 * (chunks issued after c) loads are outstanding;
+// stores counted in the same counter only lengthen that wait.
+constexpr int RING = 4;
+constexpr int LOADS_PER_REC = REC_BYTES / 1024;
+static_assert(LOADS_PER_REC * 1024 == REC_BYTES, "record must be whole KiB");
 
-__device__ __forceinline__ void load_chunk(const uint8_t* __restrict__ rec, int lane, int q4, int vt,
-                                           Chunk& ch) {
-    const u32x4* w = reinterpret_cast<const u32x4*>(rec + REC_W + lane * 64);
-    const u32x4* qg = reinterpret_cast<const u32x4*>(rec + REC_QG + lane * 64);
-    const u32x2* kg = reinterpret_cast<const u32x2*>(rec + REC_KG + lane * 64);
-    const f32x4* dc = reinterpret_cast<const f32x4*>(rec + REC_DECAY + q4 * 128);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        ch.w[j] = w[j];
-        ch.qg[j] = qg[j];
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ void wait_chunks_in_flight(int n_after) {
+    static_assert(RING == 4, "wait ladder covers RING - 1 = 3 chunks");
+    if (n_after >= 3) {
+        wait_vmcnt<3 * LOADS_PER_REC>();
+    } else if (n_after == 2) {
+        wait_vmcnt<2 * LOADS_PER_REC>();
+    } else if (n_after == 1) {
+        wait_vmcnt<LOADS_PER_REC>();
+    } else {
+        wait_vmcnt<0>();
     }
+}
+
+__device__ __forceinline__ void issue_chunk(const uint8_t* __restrict__ src, uint8_t* slot, int lane) {
 #pragma unroll
-    for (int kt = 0; kt < 8; ++kt) {
-        ch.kg[kt] = kg[kt];
-        ch.decay[kt] = dc[kt];
-    }
-    ch.u = *reinterpret_cast<const u32x2*>(rec + REC_U + vt * 512 + lane * 8);
-    ch.aqk = *reinterpret_cast<const u32x2*>(rec + REC_AQK + lane * 8);
+    for (int i = 0; i < LOADS_PER_REC; ++i)
+        __builtin_amdgcn_global_load_lds(src + i * 1024 + lane * 16, slot + i * 1024, 16, 0, 0);
 }
 
 __global__ __launch_bounds__(64) void k2_kernel(Params p) {
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[RING * REC_BYTES];
+
     const int lane = threadIdx.x;
     const int x = lane & 15;  // value column inside the tile
     const int q4 = lane >> 4;
@@ -84,12 +91,14 @@ __global__ __launch_bounds__(64) void k2_kernel(Params p) {
     }
 
     const uint8_t* rec = p.ws + (int64_t)bh * NT * REC_BYTES;
-    Chunk cur;
-    load_chunk(rec, lane, q4, vt, cur);
+    for (int d = 0; d < RING - 1; ++d)
+        if (d < NT) issue_chunk(rec + (int64_t)d * REC_BYTES, ring + d * REC_BYTES, lane);
 
     for (int c = 0; c < NT; ++c) {
-        Chunk nxt;
-        if (c + 1 < NT) load_chunk(rec + (int64_t)(c + 1) * REC_BYTES, lane, q4, vt, nxt);
+        const int cn = c + RING - 1;
+        if (cn < NT) issue_chunk(rec + (int64_t)cn * REC_BYTES, ring + (cn % RING) * REC_BYTES, lane);
+        wait_chunks_in_flight(min(RING - 1, NT - 1 - c));
+        const uint8_t* slot = ring + (c % RING) * REC_BYTES;
 
         // hc = bf16(S), as 16x16x32 B operands (k-tiles 2j and 2j+1).
         bf16x8 hc[4];
@@ -104,26 +113,36 @@ __global__ __launch_bounds__(64) void k2_kernel(Params p) {
         f32x4 oacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            vacc = mfma_bf16_16x16x32(as_bf16x8(cur.w[j]), hc[j], vacc);
-            oacc = mfma_bf16_16x16x32(as_bf16x8(cur.qg[j]), hc[j], oacc);
+            const u32x4 wj = *reinterpret_cast<const u32x4*>(slot + REC_W + j * 1024 + lane * 16);
+            const u32x4 qj = *reinterpret_cast<const u32x4*>(slot + REC_QG + j * 1024 + lane * 16);
+            vacc = mfma_bf16_16x16x32(as_bf16x8(wj), hc[j], vacc);
+            oacc = mfma_bf16_16x16x32(as_bf16x8(qj), hc[j], oacc);
         }
         // v_new[4*q4 + i][v] = u - w @ hc^T, rounded to bf16 (kernels.py:261-266).
-        const float u0 = __builtin_bit_cast(float, cur.u.x << 16);
-        const float u1 = __builtin_bit_cast(float, cur.u.x & 0xffff0000u);
-        const float u2 = __builtin_bit_cast(float, cur.u.y << 16);
-        const float u3 = __builtin_bit_cast(float, cur.u.y & 0xffff0000u);
+        const u32x2 uu = *reinterpret_cast<const u32x2*>(slot + REC_U + vt * 512 + lane * 8);
+        const float u0 = __builtin_bit_cast(float, uu.x << 16);
+        const float u1 = __builtin_bit_cast(float, uu.x & 0xffff0000u);
+        const float u2 = __builtin_bit_cast(float, uu.y << 16);
+        const float u3 = __builtin_bit_cast(float, uu.y & 0xffff0000u);
         const u32x2 vnb = {pack2(u0 - vacc[0], u1 - vacc[1]), pack2(u2 - vacc[2], u3 - vacc[3])};
         const i16x4 vn = as_i16x4(vnb);
 
         // o = scale * qg @ hc^T + Aqk @ v_new (kernels.py:268-279).
+        const u32x2 aq = *reinterpret_cast<const u32x2*>(slot + REC_AQK + lane * 8);
         oacc = oacc * p.scale;
-        oacc = mfma_bf16_16x16x16(as_i16x4(cur.aqk), vn, oacc);
+        oacc = mfma_bf16_16x16x16(as_i16x4(aq), vn, oacc);
 
         // S = S * 2^G_last + (kg^T @ v_new)^T (kernels.py:281-294).
 #pragma unroll
-        for (int kt = 0; kt < 8; ++kt) {
-            St[kt] = St[kt] * cur.decay[kt];
-            St[kt] = mfma_bf16_16x16x16(as_i16x4(cur.kg[kt]), vn, St[kt]);
+        for (int j = 0; j < 4; ++j) {
+            const u32x4 kg = *reinterpret_cast<const u32x4*>(slot + REC_KG + j * 1024 + lane * 16);
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2) {
+                const int kt = 2 * j + h2;
+                const f32x4 dc = *reinterpret_cast<const f32x4*>(slot + REC_DECAY + kt * 64 + q4 * 16);
+                const u32x2 kgt = h2 ? u32x2{kg.z, kg.w} : u32x2{kg.x, kg.y};
+                St[kt] = mfma_bf16_16x16x16(as_i16x4(kgt), vn, St[kt] * dc);
+            }
         }
 
         const int tbase = c * BT + 4 * q4;
@@ -131,7 +150,6 @@ __global__ __launch_bounds__(64) void k2_kernel(Params p) {
         for (int i = 0; i < 4; ++i) {
             if (tbase + i < T) p.o[(((int64_t)b * T + tbase + i) * H + h) * DK + v] = f2bf(oacc[i]);
         }
-        if (c + 1 < NT) cur = nxt;
     }
 
     if (p.ht) {
