@@ -19,11 +19,13 @@
 //                         operand j (k-tiles 2j, 2j+1) of each lane
 //   4096    4096   qg     bf16, F order, [j][lane][8]  = bf16(q^ * 2^G)
 //   8192    4096   kg     bf16, T order, [j][lane][8]  = bf16(k^ * 2^(G_last - G))
-//   12288   4096   u      bf16, [vt][lane][i] = u[4*q4+i][16*vt+r]
-//   16384    512   Aqk    bf16, [lane][i] = Aqk[r][4*q4+i]
-//   16896    512   decay  fp32, [kt][q4][i] = 2^G_last[16*kt+4*q4+i]
-// Consecutive lanes touch consecutive 16-byte words, so both the global
-// accesses and stage 2's LDS reads are conflict free.
+//   12288    512   Aqk    bf16, [lane][i] = Aqk[r][4*q4+i]
+//   12800    512   decay  fp32, [kt][q4][i] = 2^G_last[16*kt+4*q4+i]
+//   13312   4096   u      bf16, [vt][lane][i] = u[4*q4+i][16*vt+r]
+// The first 13 KiB are read by every value tile of a head, the last 4 KiB
+// in 512-byte slices, one per value tile.  Consecutive lanes touch
+// consecutive words, so both the global accesses and stage 2's LDS reads
+// are conflict free.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -37,9 +39,10 @@ constexpr int DK = 128;   // K == V == 128 (kernels.py:727-728)
 constexpr int REC_W = 0;
 constexpr int REC_QG = 4096;
 constexpr int REC_KG = 8192;
-constexpr int REC_U = 12288;
-constexpr int REC_AQK = 16384;
-constexpr int REC_DECAY = 16896;
+constexpr int REC_AQK = 12288;
+constexpr int REC_DECAY = 12800;
+constexpr int REC_U = 13312;
+constexpr int REC_SHARED = 13312;  // bytes every value tile reads
 constexpr int REC_BYTES = 17408;
 
 // RCP_LN2 and the l2norm epsilon, kernels.py:38-39.
@@ -86,8 +89,13 @@ __device__ __forceinline__ uint16_t f2bf(float x) {
 // Round a float to the nearest bf16 value and return it as float.
 __device__ __forceinline__ float round_bf(float x) { return bf2f(f2bf(x)); }
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two floats to two bf16 (round to nearest even) in one v_cvt_pk_bf16_f32;
+// `a` lands in the low half.
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
-    return (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
 }
 
 // Inclusive prefix sum over the 16 lanes of a DPP row (row_shr:1,2,4,8).

@@ -11,7 +11,7 @@
 // 16x16 fp32 accumulator tiles.  The 16x16 accumulator layout (lane
 // v + 16*(k/4), item k%4) is exactly the B-operand layout of the 16x16x16
 // bf16 matrix op, so bf16(S) feeds the next chunk's products straight from
-// registers: the serial chain has no LDS traffic and no barrier.  Pairs of
+// registers: the serial chain itself never goes through LDS.  Pairs of
 // k-tiles form the 8-deep operands of the 16x16x32 op for w @ hc^T and
 // qg @ hc^T; stage 1 stored w and qg in the matching k order.
 #include "kda_common.h"
@@ -20,42 +20,185 @@ namespace kda {
 
 namespace {
 
-// Records are streamed through an LDS ring of RING slots with the gfx950
-// direct global->LDS loads (global_load_lds_dwordx4: 64 lanes x 16 B =
-// 1 KiB per instruction, 17 per record), issued RING-1 chunks ahead of use.
-// The loads complete in issue order, so before reading slot c the wave
-// waits until at most 17 * (chunks issued after c) loads are outstanding;
-// stores counted in the same counter only lengthen that wait.
-constexpr int RING = 4;
-constexpr int LOADS_PER_REC = REC_BYTES / 1024;
-static_assert(LOADS_PER_REC * 1024 == REC_BYTES, "record must be whole KiB");
+// Records stream through an LDS ring of RING slots with the gfx950 direct
+// global->LDS loads (global_load_lds_dwordx4: 16 B per lane, 1 KiB per
+// wave instruction), issued RING-1 chunks ahead of use.  A wave copies the
+// 13 KiB every value tile needs (13 loads) plus its own 512-byte slice of u
+// (two 4-byte-per-lane loads): 15 loads per chunk.  The loads complete in issue order, so before reading a slot
+// the wave waits until at most 14 * (chunks issued after it) loads are
+// outstanding (s_waitcnt's vmcnt field holds at most 63); stores counted in
+// the same counter only lengthen that wait.
+constexpr int RING = 5;
+constexpr int SHARED_LOADS = REC_SHARED / 1024;
+constexpr int LOADS_PER_CHUNK = SHARED_LOADS + 2;
+constexpr int SLOT = REC_SHARED + 512;
+static_assert(SHARED_LOADS * 1024 == REC_SHARED, "shared part must be whole KiB");
+static_assert((RING - 1) * LOADS_PER_CHUNK <= 63, "vmcnt is a 6-bit count");
+
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-__device__ __forceinline__ void wait_chunks_in_flight(int n_after) {
-    static_assert(RING == 4, "wait ladder covers RING - 1 = 3 chunks");
-    if (n_after >= 3) {
-        wait_vmcnt<3 * LOADS_PER_REC>();
+// Wait until the chunk followed by `n_after` issued chunks has landed.
+__device__ __forceinline__ void wait_chunk(int n_after) {
+    static_assert(RING == 5, "ladder below covers 0..4 later chunks");
+    if (n_after >= 4) {
+        wait_vmcnt<4 * LOADS_PER_CHUNK>();
+    } else if (n_after == 3) {
+        wait_vmcnt<3 * LOADS_PER_CHUNK>();
     } else if (n_after == 2) {
-        wait_vmcnt<2 * LOADS_PER_REC>();
+        wait_vmcnt<2 * LOADS_PER_CHUNK>();
     } else if (n_after == 1) {
-        wait_vmcnt<LOADS_PER_REC>();
+        wait_vmcnt<LOADS_PER_CHUNK>();
     } else {
         wait_vmcnt<0>();
     }
 }
 
-__device__ __forceinline__ void issue_chunk(const uint8_t* __restrict__ src, uint8_t* slot, int lane) {
+// Loads [I0, I1) of one chunk's copy; indices SHARED_LOADS and
+// SHARED_LOADS + 1 are the two 256-byte halves of the u slice.
+template <int I0, int I1>
+__device__ __forceinline__ void issue_part(const uint8_t* __restrict__ rec, lds_u8* slot, int vt,
+                                           int lane) {
 #pragma unroll
-    for (int i = 0; i < LOADS_PER_REC; ++i)
-        __builtin_amdgcn_global_load_lds(src + i * 1024 + lane * 16, slot + i * 1024, 16, 0, 0);
+    for (int i = I0; i < I1; ++i) {
+        if (i < SHARED_LOADS) {
+            __builtin_amdgcn_global_load_lds(rec + i * 1024 + lane * 16, slot + i * 1024, 16, 0, 0);
+        } else {
+            const int half = i - SHARED_LOADS;
+            __builtin_amdgcn_global_load_lds(rec + REC_U + vt * 512 + half * 256 + lane * 4,
+                                             slot + REC_SHARED + half * 256, 4, 0, 0);
+        }
+    }
+}
+
+__device__ __forceinline__ void issue_chunk(const uint8_t* __restrict__ rec, lds_u8* slot, int vt,
+                                            int lane) {
+    issue_part<0, LOADS_PER_CHUNK>(rec, slot, vt, lane);
+}
+
+// One chunk's operands in registers, read from the ring one step ahead.
+// Every ring read sits right after the explicit wait for its chunk: the
+// compiler cannot tell ring slots apart, and a ring read that follows a
+// direct-to-LDS load issue without such a wait gets a conservative
+// vmcnt(0) from it, which would stall every step on the newest load.
+struct Ops {
+    u32x4 w[4];
+    u32x4 qg[4];
+    u32x4 kg[4];
+    f32x4 dc[8];
+    u32x2 aqk;
+    u32x2 u;
+};
+
+__device__ __forceinline__ void read_ops(const uint8_t* slot, int lane, int q4, Ops& op) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        op.w[j] = *reinterpret_cast<const u32x4*>(slot + REC_W + j * 1024 + lane * 16);
+    op.u = *reinterpret_cast<const u32x2*>(slot + REC_SHARED + lane * 8);
+    op.aqk = *reinterpret_cast<const u32x2*>(slot + REC_AQK + lane * 8);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        op.qg[j] = *reinterpret_cast<const u32x4*>(slot + REC_QG + j * 1024 + lane * 16);
+        op.kg[j] = *reinterpret_cast<const u32x4*>(slot + REC_KG + j * 1024 + lane * 16);
+    }
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt)
+        op.dc[kt] = *reinterpret_cast<const f32x4*>(slot + REC_DECAY + kt * 64 + q4 * 16);
+}
+
+// The record ring (one per work-group).  Referenced by name everywhere, so
+// every ring address is a known LDS offset; the direct loads take it as an
+// LDS-space pointer, cast before any offset is applied.
+__shared__ __attribute__((aligned(1024))) uint8_t ring[RING * SLOT];
+
+__device__ __forceinline__ lds_u8* ring_lds() { return (lds_u8*)ring; }
+
+// Per-wave constants of the chunk loop.
+struct Ctx {
+    const uint8_t* rec;  // this head's first record
+    uint16_t* obase;     // o[b, 0, h, 16*vt + lane%16]
+    int64_t orow_stride; // elements between consecutive tokens of o
+    float scale;
+    int NT, T, lane, q4, x, vt;
+};
+
+// One chunk of the recurrence.  S (the ring slot of chunk c) is a template
+// argument so that every ring offset is a compile-time constant: alias
+// analysis then sees that the slot being refilled, the slot being read and
+// the slot being prefetched are disjoint, and no conservative wait on the
+// newest direct-to-LDS load is inserted.
+template <int S>
+__device__ __forceinline__ void chunk_step(const Ctx& cx, int c, f32x4 (&St)[8], Ops& cur) {
+    // The copy of chunk c + RING - 1 goes out in three groups spread over
+    // the step, so the address unit drains them while the matrix ops run
+    // instead of stalling the wave on back-to-back issue.
+    const int cn = c + RING - 1;
+    const bool refill = cn < cx.NT;
+    const uint8_t* src = cx.rec + (int64_t)cn * REC_BYTES;
+    lds_u8* dst = ring_lds() + ((S + RING - 1) % RING) * SLOT;
+    if (refill) issue_part<0, 5>(src, dst, cx.vt, cx.lane);
+
+    // hc = bf16(S), as 16x16x32 B operands (k-tiles 2j and 2j+1).
+    bf16x8 hc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const u32x4 pk = {pack2(St[2 * j][0], St[2 * j][1]), pack2(St[2 * j][2], St[2 * j][3]),
+                          pack2(St[2 * j + 1][0], St[2 * j + 1][1]),
+                          pack2(St[2 * j + 1][2], St[2 * j + 1][3])};
+        hc[j] = as_bf16x8(pk);
+    }
+    // v_new = u - w @ hc^T, two independent accumulation chains
+    // (kernels.py:261-266), rounded to bf16.
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    f32x4 va = mfma_bf16_16x16x32(as_bf16x8(cur.w[0]), hc[0], zero);
+    f32x4 vb = mfma_bf16_16x16x32(as_bf16x8(cur.w[2]), hc[2], zero);
+    va = mfma_bf16_16x16x32(as_bf16x8(cur.w[1]), hc[1], va);
+    vb = mfma_bf16_16x16x32(as_bf16x8(cur.w[3]), hc[3], vb);
+    f32x4 oacc = mfma_bf16_16x16x32(as_bf16x8(cur.qg[0]), hc[0], zero);
+#pragma unroll
+    for (int j = 1; j < 4; ++j) oacc = mfma_bf16_16x16x32(as_bf16x8(cur.qg[j]), hc[j], oacc);
+    if (refill) issue_part<5, 10>(src, dst, cx.vt, cx.lane);
+    const f32x4 vacc = va + vb;
+    const float u0 = __builtin_bit_cast(float, cur.u.x << 16);
+    const float u1 = __builtin_bit_cast(float, cur.u.x & 0xffff0000u);
+    const float u2 = __builtin_bit_cast(float, cur.u.y << 16);
+    const float u3 = __builtin_bit_cast(float, cur.u.y & 0xffff0000u);
+    const u32x2 vnb = {pack2(u0 - vacc[0], u1 - vacc[1]), pack2(u2 - vacc[2], u3 - vacc[3])};
+    const i16x4 vn = as_i16x4(vnb);
+
+    // S = S * 2^G_last + (kg^T @ v_new)^T (kernels.py:281-294).
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const u32x2 k0 = {cur.kg[j].x, cur.kg[j].y};
+        const u32x2 k1 = {cur.kg[j].z, cur.kg[j].w};
+        St[2 * j] = mfma_bf16_16x16x16(as_i16x4(k0), vn, St[2 * j] * cur.dc[2 * j]);
+        St[2 * j + 1] = mfma_bf16_16x16x16(as_i16x4(k1), vn, St[2 * j + 1] * cur.dc[2 * j + 1]);
+    }
+
+    // o = scale * qg @ hc^T + Aqk @ v_new (kernels.py:268-279).
+    oacc = oacc * cx.scale;
+    oacc = mfma_bf16_16x16x16(as_i16x4(cur.aqk), vn, oacc);
+    if (refill) issue_part<10, LOADS_PER_CHUNK>(src, dst, cx.vt, cx.lane);
+
+    // Operands of the next chunk: wait for its copy, read them while the
+    // matrix ops above drain.
+    if (c + 1 < cx.NT) {
+        wait_chunk(min(RING - 2, cx.NT - 2 - c));
+        read_ops(ring + ((S + 1) % RING) * SLOT, cx.lane, cx.q4, cur);
+    }
+
+    // o[4*q4 + i][16*vt + x]: each row of the tile is 32 contiguous bytes.
+    const int t0 = c * BT + 4 * cx.q4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        if (t0 + i < cx.T) cx.obase[(int64_t)(t0 + i) * cx.orow_stride] = f2bf(oacc[i]);
 }
 
 __global__ __launch_bounds__(64) void k2_kernel(Params p) {
-    __shared__ __attribute__((aligned(1024))) uint8_t ring[RING * REC_BYTES];
 
     const int lane = threadIdx.x;
     const int x = lane & 15;  // value column inside the tile
@@ -90,66 +233,32 @@ __global__ __launch_bounds__(64) void k2_kernel(Params p) {
         }
     }
 
-    const uint8_t* rec = p.ws + (int64_t)bh * NT * REC_BYTES;
+    Ctx cx;
+    cx.rec = p.ws + (int64_t)bh * NT * REC_BYTES;
+    cx.obase = p.o + ((int64_t)b * T * H + h) * DK + v;
+    cx.orow_stride = (int64_t)H * DK;
+    cx.scale = p.scale;
+    cx.NT = NT;
+    cx.T = T;
+    cx.lane = lane;
+    cx.q4 = q4;
+    cx.x = x;
+    cx.vt = vt;
+
+#pragma unroll
     for (int d = 0; d < RING - 1; ++d)
-        if (d < NT) issue_chunk(rec + (int64_t)d * REC_BYTES, ring + d * REC_BYTES, lane);
+        if (d < NT) issue_chunk(cx.rec + (int64_t)d * REC_BYTES, ring_lds() + d * SLOT, vt, lane);
+    wait_chunk(min(RING - 2, NT - 1));
+    Ops cur;
+    read_ops(ring, lane, q4, cur);
 
-    for (int c = 0; c < NT; ++c) {
-        const int cn = c + RING - 1;
-        if (cn < NT) issue_chunk(rec + (int64_t)cn * REC_BYTES, ring + (cn % RING) * REC_BYTES, lane);
-        wait_chunks_in_flight(min(RING - 1, NT - 1 - c));
-        const uint8_t* slot = ring + (c % RING) * REC_BYTES;
-
-        // hc = bf16(S), as 16x16x32 B operands (k-tiles 2j and 2j+1).
-        bf16x8 hc[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const u32x4 pk = {pack2(St[2 * j][0], St[2 * j][1]), pack2(St[2 * j][2], St[2 * j][3]),
-                              pack2(St[2 * j + 1][0], St[2 * j + 1][1]),
-                              pack2(St[2 * j + 1][2], St[2 * j + 1][3])};
-            hc[j] = as_bf16x8(pk);
-        }
-        f32x4 vacc = {0.f, 0.f, 0.f, 0.f};
-        f32x4 oacc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const u32x4 wj = *reinterpret_cast<const u32x4*>(slot + REC_W + j * 1024 + lane * 16);
-            const u32x4 qj = *reinterpret_cast<const u32x4*>(slot + REC_QG + j * 1024 + lane * 16);
-            vacc = mfma_bf16_16x16x32(as_bf16x8(wj), hc[j], vacc);
-            oacc = mfma_bf16_16x16x32(as_bf16x8(qj), hc[j], oacc);
-        }
-        // v_new[4*q4 + i][v] = u - w @ hc^T, rounded to bf16 (kernels.py:261-266).
-        const u32x2 uu = *reinterpret_cast<const u32x2*>(slot + REC_U + vt * 512 + lane * 8);
-        const float u0 = __builtin_bit_cast(float, uu.x << 16);
-        const float u1 = __builtin_bit_cast(float, uu.x & 0xffff0000u);
-        const float u2 = __builtin_bit_cast(float, uu.y << 16);
-        const float u3 = __builtin_bit_cast(float, uu.y & 0xffff0000u);
-        const u32x2 vnb = {pack2(u0 - vacc[0], u1 - vacc[1]), pack2(u2 - vacc[2], u3 - vacc[3])};
-        const i16x4 vn = as_i16x4(vnb);
-
-        // o = scale * qg @ hc^T + Aqk @ v_new (kernels.py:268-279).
-        const u32x2 aq = *reinterpret_cast<const u32x2*>(slot + REC_AQK + lane * 8);
-        oacc = oacc * p.scale;
-        oacc = mfma_bf16_16x16x16(as_i16x4(aq), vn, oacc);
-
-        // S = S * 2^G_last + (kg^T @ v_new)^T (kernels.py:281-294).
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const u32x4 kg = *reinterpret_cast<const u32x4*>(slot + REC_KG + j * 1024 + lane * 16);
-#pragma unroll
-            for (int h2 = 0; h2 < 2; ++h2) {
-                const int kt = 2 * j + h2;
-                const f32x4 dc = *reinterpret_cast<const f32x4*>(slot + REC_DECAY + kt * 64 + q4 * 16);
-                const u32x2 kgt = h2 ? u32x2{kg.z, kg.w} : u32x2{kg.x, kg.y};
-                St[kt] = mfma_bf16_16x16x16(as_i16x4(kgt), vn, St[kt] * dc);
-            }
-        }
-
-        const int tbase = c * BT + 4 * q4;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            if (tbase + i < T) p.o[(((int64_t)b * T + tbase + i) * H + h) * DK + v] = f2bf(oacc[i]);
-        }
+    static_assert(RING == 5, "the unrolled loop below names every slot");
+    for (int c = 0; c < NT; c += RING) {
+        chunk_step<0>(cx, c, St, cur);
+        if (c + 1 < NT) chunk_step<1>(cx, c + 1, St, cur);
+        if (c + 2 < NT) chunk_step<2>(cx, c + 2, St, cur);
+        if (c + 3 < NT) chunk_step<3>(cx, c + 3, St, cur);
+        if (c + 4 < NT) chunk_step<4>(cx, c + 4, St, cur);
     }
 
     if (p.ht) {

@@ -30,6 +30,10 @@ HIPCC_FLAGS = [
     "-Wall",
     # Keep the compiler from forming packed fp32 VALU ops.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Matrix-op accumulators in ordinary VGPRs: stage 2 scales its state
+    # with VALU ops every chunk, and AGPR-resident accumulators would need a
+    # copy out and back each time.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 
