@@ -98,6 +98,18 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
 }
 
+// exp2 on the transcendental unit (v_exp_f32, 1 ulp), without the library
+// routine's denormal-range fixups: every exponent that reaches it is either
+// in the normal range or so negative that the result is a negligible
+// underflow, as with Triton's exp2 on GPUs.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// sigmoid(x) = 1 / (1 + e^-x) with v_exp_f32 and v_rcp_f32 (~2 ulp).
+// Saturates correctly: x -> -inf gives rcp(inf) = 0, x -> +inf gives 1.
+__device__ __forceinline__ float fast_sigmoid(float x) {
+    return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
+}
+
 // Inclusive prefix sum over the 16 lanes of a DPP row (row_shr:1,2,4,8).
 // Lanes shifted in from outside the row contribute 0.
 __device__ __forceinline__ float row_scan16(float x) {

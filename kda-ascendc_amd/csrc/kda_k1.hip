@@ -24,25 +24,29 @@ namespace {
 
 constexpr int LROW = DK + 8;  // bf16 elements per LDS row (padding spreads banks)
 
-__device__ __forceinline__ void load_bf16x32(const uint16_t* __restrict__ src, bool valid,
-                                             int colbase, float out[32]) {
+// 32 bf16 values of one row in F order, packed: item 4*kt + i is half
+// (i & 1) of word (i >> 1) of v[kt].
+struct Row32 {
+    u32x2 v[8];
+};
+
+__device__ __forceinline__ float elem(const Row32& a, int p) {
+    const uint32_t w = (p & 2) ? a.v[p >> 2].y : a.v[p >> 2].x;
+    return (p & 1) ? __builtin_bit_cast(float, w & 0xffff0000u) : __builtin_bit_cast(float, w << 16);
+}
+
+__device__ __forceinline__ void load_row(const uint16_t* __restrict__ src, bool valid, int colbase,
+                                         Row32& out) {
 #pragma unroll
     for (int kt = 0; kt < 8; ++kt) {
-        u32x2 a = {0u, 0u};
-        if (valid) a = *reinterpret_cast<const u32x2*>(src + 16 * kt + colbase);
-        out[4 * kt + 0] = __builtin_bit_cast(float, a.x << 16);
-        out[4 * kt + 1] = __builtin_bit_cast(float, a.x & 0xffff0000u);
-        out[4 * kt + 2] = __builtin_bit_cast(float, a.y << 16);
-        out[4 * kt + 3] = __builtin_bit_cast(float, a.y & 0xffff0000u);
+        out.v[kt] = u32x2{0u, 0u};
+        if (valid) out.v[kt] = *reinterpret_cast<const u32x2*>(src + 16 * kt + colbase);
     }
 }
 
-__device__ __forceinline__ void store_lds_row(uint16_t* lds, int r, int colbase, const float x[32]) {
-#pragma unroll
-    for (int kt = 0; kt < 8; ++kt) {
-        u32x2 pk = {pack2(x[4 * kt + 0], x[4 * kt + 1]), pack2(x[4 * kt + 2], x[4 * kt + 3])};
-        *reinterpret_cast<u32x2*>(lds + r * LROW + 16 * kt + colbase) = pk;
-    }
+// Row r of an LDS tile, F order: 4 values at columns 16*kt + colbase.
+__device__ __forceinline__ void lds_put(uint16_t* lds, int r, int colbase, int kt, u32x2 pk) {
+    *reinterpret_cast<u32x2*>(lds + r * LROW + 16 * kt + colbase) = pk;
 }
 
 // T order read: item 4*kt + i = M[4*q4 + i][16*kt + r], packed for the
@@ -59,14 +63,13 @@ __device__ __forceinline__ void load_lds_T(const uint16_t* lds, int r, int q4, i
     }
 }
 
-__device__ __forceinline__ u32x2 pack4(f32x4 v) {
-    return u32x2{pack2(v.x, v.y), pack2(v.z, v.w)};
+__device__ __forceinline__ u32x2 pack4(float a, float b, float c, float d) {
+    return u32x2{pack2(a, b), pack2(c, d)};
 }
+__device__ __forceinline__ u32x2 pack4(f32x4 v) { return pack4(v.x, v.y, v.z, v.w); }
 
 __global__ __launch_bounds__(64) void k1_kernel(Params p) {
-    __shared__ __attribute__((aligned(16))) uint16_t s_kb[BT * LROW];
-    __shared__ __attribute__((aligned(16))) uint16_t s_vb[BT * LROW];
-    __shared__ __attribute__((aligned(16))) uint16_t s_kg[BT * LROW];
+    __shared__ __attribute__((aligned(16))) uint16_t s_T[BT * LROW];  // transpose tile
     __shared__ __attribute__((aligned(16))) float s_L[BT * BT];
     __shared__ float s_X[BT * (BT + 1)];
 
@@ -85,22 +88,24 @@ __global__ __launch_bounds__(64) void k1_kernel(Params p) {
     const int64_t rowoff = (tok * H + h) * DK;    // element offset of that row
 
     // ---- loads (kernels.py:97-106); padded rows read as zero -------------
-    float qf[32], kf[32], vf[32], gf[32];
-    load_bf16x32(p.q + rowoff, valid, colbase, qf);
-    load_bf16x32(p.k + rowoff, valid, colbase, kf);
-    load_bf16x32(p.v + rowoff, valid, colbase, vf);
+    Row32 qp, kp, vp;
+    load_row(p.q + rowoff, valid, colbase, qp);
+    load_row(p.k + rowoff, valid, colbase, kp);
+    load_row(p.v + rowoff, valid, colbase, vp);
+    float G[32];
     if (p.g_bf16) {
-        load_bf16x32(static_cast<const uint16_t*>(p.g) + rowoff, valid, colbase, gf);
+        Row32 gp;
+        load_row(static_cast<const uint16_t*>(p.g) + rowoff, valid, colbase, gp);
+#pragma unroll
+        for (int j = 0; j < 32; ++j) G[j] = elem(gp, j);
     } else {
         const float* gsrc = static_cast<const float*>(p.g) + rowoff;
 #pragma unroll
         for (int kt = 0; kt < 8; ++kt) {
             f32x4 a = {0.f, 0.f, 0.f, 0.f};
             if (valid) a = *reinterpret_cast<const f32x4*>(gsrc + 16 * kt + colbase);
-            gf[4 * kt + 0] = a.x;
-            gf[4 * kt + 1] = a.y;
-            gf[4 * kt + 2] = a.z;
-            gf[4 * kt + 3] = a.w;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) G[4 * kt + i] = a[i];
         }
     }
     float beta = 0.f;
@@ -109,15 +114,15 @@ __global__ __launch_bounds__(64) void k1_kernel(Params p) {
         beta = p.beta_bf16 ? bf2f(static_cast<const uint16_t*>(p.beta)[bi])
                            : static_cast<const float*>(p.beta)[bi];
     }
-    if (p.use_beta_sigmoid) beta = 1.f / (1.f + expf(-beta));
+    if (p.use_beta_sigmoid) beta = fast_sigmoid(beta);
 
     // ---- q/k l2norm, rounded back to bf16 (kernels.py:108-113) -----------
     if (p.use_l2norm) {
         float sq = 0.f, sk = 0.f;
 #pragma unroll
         for (int j = 0; j < 32; ++j) {
-            sq = fmaf(qf[j], qf[j], sq);
-            sk = fmaf(kf[j], kf[j], sk);
+            sq = fmaf(elem(qp, j), elem(qp, j), sq);
+            sk = fmaf(elem(kp, j), elem(kp, j), sk);
         }
         sq += __shfl_xor(sq, 16);
         sk += __shfl_xor(sk, 16);
@@ -126,14 +131,15 @@ __global__ __launch_bounds__(64) void k1_kernel(Params p) {
         const float rq = 1.f / sqrtf(sq + L2_EPS);
         const float rk = 1.f / sqrtf(sk + L2_EPS);
 #pragma unroll
-        for (int j = 0; j < 32; ++j) {
-            qf[j] = round_bf(qf[j] * rq);
-            kf[j] = round_bf(kf[j] * rk);
+        for (int kt = 0; kt < 8; ++kt) {
+            qp.v[kt] = pack4(elem(qp, 4 * kt) * rq, elem(qp, 4 * kt + 1) * rq,
+                             elem(qp, 4 * kt + 2) * rq, elem(qp, 4 * kt + 3) * rq);
+            kp.v[kt] = pack4(elem(kp, 4 * kt) * rk, elem(kp, 4 * kt + 1) * rk,
+                             elem(kp, 4 * kt + 2) * rk, elem(kp, 4 * kt + 3) * rk);
         }
     }
 
     // ---- gate and chunk-local log2 cumsum (kernels.py:115-124) -----------
-    float G[32];
     if (p.use_gate) {
         const float ea = expf(p.A_log[h]);
         const float* bias = p.dt_bias ? p.dt_bias + h * DK : nullptr;
@@ -141,41 +147,32 @@ __global__ __launch_bounds__(64) void k1_kernel(Params p) {
         for (int kt = 0; kt < 8; ++kt) {
             f32x4 bb = {0.f, 0.f, 0.f, 0.f};
             if (bias) bb = *reinterpret_cast<const f32x4*>(bias + 16 * kt + colbase);
-            const float bv[4] = {bb.x, bb.y, bb.z, bb.w};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float s = bias ? gf[4 * kt + i] + bv[i] : gf[4 * kt + i];
-                float gate = p.lower_bound * (1.f / (1.f + expf(-(ea * s))));
+                const float s = bias ? G[4 * kt + i] + bb[i] : G[4 * kt + i];
+                float gate = p.lower_bound * fast_sigmoid(ea * s);
                 gate = valid ? gate : 0.f;
                 G[4 * kt + i] = row_scan16(gate) * RCP_LN2;
             }
         }
-    } else {
-#pragma unroll
-        for (int j = 0; j < 32; ++j) G[j] = gf[j];
     }
 
     // ---- mid-row recentring, grams on matrix cores (kernels.py:129-155) ---
     const int mid = min(BT / 2, nvalid - 1);
     const int last = nvalid - 1;
     const int row0 = lane & 48;
-    float Glast[32];
     f32x4 acc_qk = {0.f, 0.f, 0.f, 0.f};
     f32x4 acc_kk = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 32; ++j) {
-        const float gmid = shfl(G[j], row0 | mid);
-        Glast[j] = shfl(G[j], row0 | last);
-        const float gm = G[j] - gmid;
-        const float gq = valid ? exp2f(gm) : 0.f;
-        const float gk = valid ? exp2f(-gm) : 0.f;
-        const float Qs = qf[j] * gq;
-        const float Ks = kf[j] * gk;
-        const float Kq = kf[j] * gq;
+        const float gm = G[j] - shfl(G[j], row0 | mid);
+        const float gq = valid ? fast_exp2(gm) : 0.f;
+        const float gk = valid ? fast_exp2(-gm) : 0.f;
+        const float qv = elem(qp, j), kv = elem(kp, j);
         // A = Ks (rows s), B = Qs / Kq (columns t): lane (t, q4) receives
         // Aqk[t][4*q4 + i] and Akk[t][4*q4 + i].
-        acc_qk = mfma_f32_16x16x4(Ks, Qs, acc_qk);
-        acc_kk = mfma_f32_16x16x4(Ks, Kq, acc_kk);
+        acc_qk = mfma_f32_16x16x4(kv * gk, qv * gq, acc_qk);
+        acc_kk = mfma_f32_16x16x4(kv * gk, kv * gq, acc_kk);
     }
 
     uint8_t* rec = p.ws + ((int64_t)bh * NT + c) * REC_BYTES;
@@ -222,34 +219,22 @@ __global__ __launch_bounds__(64) void k1_kernel(Params p) {
     const u32x2 ainv_bf = pack4(ainv);  // A = bf16(A_inv), kernels.py:170
     const i16x4 A_op = as_i16x4(ainv_bf);
 
-    // ---- W/U operands (kernels.py:171-174) and stage-2 operands ----------
-    float qg[32];
-    {
-        float kb[32], vb[32], kg[32];
+    // ---- u = A @ bf16(v * beta) (kernels.py:173-174) ----------------------
+    // One 16x16x16 tile per 16 value columns; u lands as
+    // u[4*q4 + i][16*vt + r], the order stage 2 subtracts it in.
 #pragma unroll
-        for (int j = 0; j < 32; ++j) {
-            const float e = exp2f(G[j]);
-            kb[j] = round_bf(round_bf(kf[j] * beta) * e);
-            vb[j] = round_bf(vf[j] * beta);
-            qg[j] = round_bf(qf[j] * e);                      // kernels.py:266
-            kg[j] = round_bf(kf[j] * exp2f(Glast[j] - G[j]));  // kernels.py:283-285
-        }
-        store_lds_row(s_kb, r, colbase, kb);
-        store_lds_row(s_vb, r, colbase, vb);
-        store_lds_row(s_kg, r, colbase, kg);
-    }
+    for (int kt = 0; kt < 8; ++kt)
+        lds_put(s_T, r, colbase, kt,
+                pack4(elem(vp, 4 * kt) * beta, elem(vp, 4 * kt + 1) * beta,
+                      elem(vp, 4 * kt + 2) * beta, elem(vp, 4 * kt + 3) * beta));
     __syncthreads();
-
-    // u = A @ vb: one 16x16x16 tile per 16 value columns.  The result lands
-    // as u[4*q4 + i][16*vt + r], the order stage 2 subtracts it in.
     {
         i16x4 vbT[8];
-        load_lds_T(s_vb, r, q4, vbT);
+        load_lds_T(s_T, r, q4, vbT);
 #pragma unroll
         for (int vt = 0; vt < 8; ++vt) {
             const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-            const f32x4 uacc = mfma_bf16_16x16x16(A_op, vbT[vt], zero);
-            const u32x2 ub = pack4(uacc);
+            const u32x2 ub = pack4(mfma_bf16_16x16x16(A_op, vbT[vt], zero));
             *reinterpret_cast<u32x2*>(rec + REC_U + vt * 512 + lane * 8) = ub;
             if (p.dbg_u) {
 #pragma unroll
@@ -264,34 +249,65 @@ __global__ __launch_bounds__(64) void k1_kernel(Params p) {
             }
         }
     }
+    __syncthreads();
 
-    // w^T = kb^T @ A^T: tile kt yields w[r][16*kt + 4*q4 + i] in lane (r, q4),
-    // i.e. w in F order.
+    // ---- w = A @ bf16(bf16(k^ * beta) * 2^G) (kernels.py:171-172), and
+    // qg = bf16(q^ * 2^G), the gated query stage 2 multiplies the state by
+    // (kernels.py:269).  w is computed transposed, w^T = kb^T @ A^T, so that
+    // tile kt lands as w[r][16*kt + 4*q4 + i]: F order, stage 2's operand.
+    u32x2 qgp[8];
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) {
+        float kb[4], qg[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float e = fast_exp2(G[4 * kt + i]);
+            kb[i] = round_bf(elem(kp, 4 * kt + i) * beta) * e;
+            qg[i] = elem(qp, 4 * kt + i) * e;
+        }
+        lds_put(s_T, r, colbase, kt, pack4(kb[0], kb[1], kb[2], kb[3]));
+        qgp[kt] = pack4(qg[0], qg[1], qg[2], qg[3]);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        *reinterpret_cast<u32x4*>(rec + REC_QG + j * 1024 + lane * 16) =
+            u32x4{qgp[2 * j].x, qgp[2 * j].y, qgp[2 * j + 1].x, qgp[2 * j + 1].y};
+    __syncthreads();
     u32x2 wpk[8];
     {
         i16x4 kbT[8];
-        load_lds_T(s_kb, r, q4, kbT);
+        load_lds_T(s_T, r, q4, kbT);
 #pragma unroll
         for (int kt = 0; kt < 8; ++kt) {
             const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
             wpk[kt] = pack4(mfma_bf16_16x16x16(kbT[kt], A_op, zero));
         }
     }
-    {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            *reinterpret_cast<u32x4*>(rec + REC_W + j * 1024 + lane * 16) =
-                u32x4{wpk[2 * j].x, wpk[2 * j].y, wpk[2 * j + 1].x, wpk[2 * j + 1].y};
-    }
-    {
+    for (int j = 0; j < 4; ++j)
+        *reinterpret_cast<u32x4*>(rec + REC_W + j * 1024 + lane * 16) =
+            u32x4{wpk[2 * j].x, wpk[2 * j].y, wpk[2 * j + 1].x, wpk[2 * j + 1].y};
+    __syncthreads();
+
+    // ---- kg = bf16(k^ * 2^(G_last - G)) and the decay 2^G_last of the state
+    // (kernels.py:282-290), kg stored in T order (stage 2's A operand).
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            *reinterpret_cast<u32x4*>(rec + REC_QG + j * 1024 + lane * 16) = u32x4{pack2(qg[8 * j + 0], qg[8 * j + 1]), pack2(qg[8 * j + 2], qg[8 * j + 3]),
-                           pack2(qg[8 * j + 4], qg[8 * j + 5]), pack2(qg[8 * j + 6], qg[8 * j + 7])};
+    for (int kt = 0; kt < 8; ++kt) {
+        float kg[4], gl[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            gl[i] = shfl(G[4 * kt + i], row0 | last);
+            kg[i] = elem(kp, 4 * kt + i) * fast_exp2(gl[i] - G[4 * kt + i]);
+        }
+        lds_put(s_T, r, colbase, kt, pack4(kg[0], kg[1], kg[2], kg[3]));
+        if (r == 0)
+            *reinterpret_cast<f32x4*>(rec + REC_DECAY + kt * 64 + q4 * 16) =
+                f32x4{fast_exp2(gl[0]), fast_exp2(gl[1]), fast_exp2(gl[2]), fast_exp2(gl[3])};
     }
+    __syncthreads();
     {
         i16x4 kgT[8];
-        load_lds_T(s_kg, r, q4, kgT);
+        load_lds_T(s_T, r, q4, kgT);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const u32x2 a = __builtin_bit_cast(u32x2, kgT[2 * j]);
@@ -299,12 +315,6 @@ __global__ __launch_bounds__(64) void k1_kernel(Params p) {
             *reinterpret_cast<u32x4*>(rec + REC_KG + j * 1024 + lane * 16) =
                 u32x4{a.x, a.y, bq.x, bq.y};
         }
-    }
-    if (r == 0) {
-#pragma unroll
-        for (int kt = 0; kt < 8; ++kt)
-            *reinterpret_cast<f32x4*>(rec + REC_DECAY + kt * 64 + q4 * 16) = f32x4{exp2f(Glast[4 * kt + 0]), exp2f(Glast[4 * kt + 1]),
-                            exp2f(Glast[4 * kt + 2]), exp2f(Glast[4 * kt + 3])};
     }
 
     // ---- optional reference-layout intermediates (kernels.py:125,153,178-184)

@@ -21,19 +21,21 @@ namespace kda {
 namespace {
 
 // Records stream through an LDS ring of RING slots with the gfx950 direct
-// global->LDS loads (global_load_lds_dwordx4: 16 B per lane, 1 KiB per
+// global->LDS loads (buffer_load_dwordx4 ... lds: 16 B per lane, 1 KiB per
 // wave instruction), issued RING-1 chunks ahead of use.  A wave copies the
-// 13 KiB every value tile needs (13 loads) plus its own 512-byte slice of u
-// (two 4-byte-per-lane loads): 15 loads per chunk.  The loads complete in issue order, so before reading a slot
-// the wave waits until at most 14 * (chunks issued after it) loads are
-// outstanding (s_waitcnt's vmcnt field holds at most 63); stores counted in
-// the same counter only lengthen that wait.
+// 13 KiB every value tile needs plus the 1 KiB pair of u slices that holds
+// its own 512-byte slice: 14 loads per chunk.  The loads complete in issue
+// order, so before reading a slot the wave waits until at most
+// 14 * (chunks issued after it) loads are outstanding; stores counted in the
+// same counter only lengthen that wait.  A wave may have at most 63 vector
+// memory operations in flight (the vmcnt field is 6 bits) before issue
+// stalls: (RING - 1) * 14 loads plus the step's single store stay below.
 constexpr int RING = 5;
 constexpr int SHARED_LOADS = REC_SHARED / 1024;
-constexpr int LOADS_PER_CHUNK = SHARED_LOADS + 2;
-constexpr int SLOT = REC_SHARED + 512;
+constexpr int LOADS_PER_CHUNK = SHARED_LOADS + 1;
+constexpr int SLOT = REC_SHARED + 1024;
 static_assert(SHARED_LOADS * 1024 == REC_SHARED, "shared part must be whole KiB");
-static_assert((RING - 1) * LOADS_PER_CHUNK <= 63, "vmcnt is a 6-bit count");
+static_assert((RING - 1) * LOADS_PER_CHUNK + 1 <= 63, "vmcnt is a 6-bit count");
 
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
@@ -58,26 +60,29 @@ __device__ __forceinline__ void wait_chunk(int n_after) {
     }
 }
 
-// Loads [I0, I1) of one chunk's copy; indices SHARED_LOADS and
-// SHARED_LOADS + 1 are the two 256-byte halves of the u slice.
+// Buffer descriptor word 3 for raw byte-addressed buffers on gfx9-family
+// parts (gfx950 included).
+constexpr int BUF_DWORD3 = 0x00020000;
+
+// Loads [I0, I1) of one chunk's copy; index SHARED_LOADS is the 1 KiB pair
+// of u slices (value tiles 2*(vt/2) and 2*(vt/2)+1), always inside the
+// record.  Buffer loads with the chunk offset in an SGPR and a fixed
+// per-lane VGPR offset: no per-step address arithmetic on the vector ALU.
 template <int I0, int I1>
-__device__ __forceinline__ void issue_part(const uint8_t* __restrict__ rec, lds_u8* slot, int vt,
-                                           int lane) {
+__device__ __forceinline__ void issue_part(__amdgpu_buffer_rsrc_t rs, uint32_t chunk_off,
+                                           lds_u8* slot, int vt, uint32_t voff16) {
 #pragma unroll
     for (int i = I0; i < I1; ++i) {
-        if (i < SHARED_LOADS) {
-            __builtin_amdgcn_global_load_lds(rec + i * 1024 + lane * 16, slot + i * 1024, 16, 0, 0);
-        } else {
-            const int half = i - SHARED_LOADS;
-            __builtin_amdgcn_global_load_lds(rec + REC_U + vt * 512 + half * 256 + lane * 4,
-                                             slot + REC_SHARED + half * 256, 4, 0, 0);
-        }
+        const uint32_t src = i < SHARED_LOADS ? chunk_off + i * 1024
+                                              : chunk_off + REC_U + (uint32_t)(vt >> 1) * 1024;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_u8*)(slot + i * 1024), 16, voff16, src,
+                                                 0, 0);
     }
 }
 
-__device__ __forceinline__ void issue_chunk(const uint8_t* __restrict__ rec, lds_u8* slot, int vt,
-                                            int lane) {
-    issue_part<0, LOADS_PER_CHUNK>(rec, slot, vt, lane);
+__device__ __forceinline__ void issue_chunk(__amdgpu_buffer_rsrc_t rs, uint32_t chunk_off,
+                                            lds_u8* slot, int vt, uint32_t voff16) {
+    issue_part<0, LOADS_PER_CHUNK>(rs, chunk_off, slot, vt, voff16);
 }
 
 // One chunk's operands in registers, read from the ring one step ahead.
@@ -94,11 +99,11 @@ struct Ops {
     u32x2 u;
 };
 
-__device__ __forceinline__ void read_ops(const uint8_t* slot, int lane, int q4, Ops& op) {
+__device__ __forceinline__ void read_ops(const uint8_t* slot, int lane, int q4, int vt, Ops& op) {
 #pragma unroll
     for (int j = 0; j < 4; ++j)
         op.w[j] = *reinterpret_cast<const u32x4*>(slot + REC_W + j * 1024 + lane * 16);
-    op.u = *reinterpret_cast<const u32x2*>(slot + REC_SHARED + lane * 8);
+    op.u = *reinterpret_cast<const u32x2*>(slot + REC_SHARED + (vt & 1) * 512 + lane * 8);
     op.aqk = *reinterpret_cast<const u32x2*>(slot + REC_AQK + lane * 8);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -117,10 +122,39 @@ __shared__ __attribute__((aligned(1024))) uint8_t ring[RING * SLOT];
 
 __device__ __forceinline__ lds_u8* ring_lds() { return (lds_u8*)ring; }
 
+// 4x4 transpose of 16-bit values across the 4 lanes of a quad.  Lane j
+// enters with p0 = (M[0][j], M[1][j]) and p1 = (M[2][j], M[3][j]) and leaves
+// with (M[j][0], M[j][1]) and (M[j][2], M[j][3]).  Two DPP exchanges:
+// lanes j and j^2 swap the 2x2 blocks off the diagonal, then lanes j and
+// j^1 swap 16-bit halves.
+__device__ __forceinline__ u32x2 quad_transpose(uint32_t p0, uint32_t p1, int j) {
+    constexpr int QP_XOR2 = 2 | (3 << 2) | (0 << 4) | (1 << 6);  // quad_perm [2,3,0,1]
+    constexpr int QP_XOR1 = 1 | (0 << 2) | (3 << 4) | (2 << 6);  // quad_perm [1,0,3,2]
+    const bool lo2 = (j & 2) == 0;
+    // after this, the lane holds rows {r, r+1} (r = 0 for j < 2, else 2)
+    // for columns {j & 1, (j & 1) + 2} as (a: column j&1, b: column (j&1)+2)
+    const uint32_t send2 = lo2 ? p1 : p0;
+    const uint32_t recv2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)send2, QP_XOR2, 0xf, 0xf, false);
+    const uint32_t a = lo2 ? p0 : recv2;
+    const uint32_t bb = lo2 ? recv2 : p1;
+    // lane with j even keeps the low halves (its row), sends the high halves
+    const bool even = (j & 1) == 0;
+    const uint32_t send1 = even ? __builtin_amdgcn_perm(bb, a, 0x07060302u)   // (a.hi, b.hi)
+                                : __builtin_amdgcn_perm(bb, a, 0x05040100u);  // (a.lo, b.lo)
+    const uint32_t recv1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)send1, QP_XOR1, 0xf, 0xf, false);
+    // even lane: (a.lo, recv.lo), (b.lo, recv.hi); odd lane: (recv.lo, a.hi), (recv.hi, b.hi)
+    const uint32_t w0 = even ? __builtin_amdgcn_perm(recv1, a, 0x05040100u)
+                             : __builtin_amdgcn_perm(a, recv1, 0x07060100u);
+    const uint32_t w1 = even ? __builtin_amdgcn_perm(recv1, bb, 0x07060100u)
+                             : __builtin_amdgcn_perm(bb, recv1, 0x07060302u);
+    return u32x2{w0, w1};
+}
+
 // Per-wave constants of the chunk loop.
 struct Ctx {
-    const uint8_t* rec;  // this head's first record
-    uint16_t* obase;     // o[b, 0, h, 16*vt + lane%16]
+    __amdgpu_buffer_rsrc_t rs;  // this head's records, NT * REC_BYTES bytes
+    uint32_t voff16;            // lane * 16
+    uint16_t* obase;     // o[b, 0, h, 16*vt + 4*((lane%16)/4)]
     int64_t orow_stride; // elements between consecutive tokens of o
     float scale;
     int NT, T, lane, q4, x, vt;
@@ -138,9 +172,9 @@ __device__ __forceinline__ void chunk_step(const Ctx& cx, int c, f32x4 (&St)[8],
     // instead of stalling the wave on back-to-back issue.
     const int cn = c + RING - 1;
     const bool refill = cn < cx.NT;
-    const uint8_t* src = cx.rec + (int64_t)cn * REC_BYTES;
+    const uint32_t src = (uint32_t)cn * REC_BYTES;
     lds_u8* dst = ring_lds() + ((S + RING - 1) % RING) * SLOT;
-    if (refill) issue_part<0, 5>(src, dst, cx.vt, cx.lane);
+    if (refill) issue_part<0, 5>(cx.rs, src, dst, cx.vt, cx.voff16);
 
     // hc = bf16(S), as 16x16x32 B operands (k-tiles 2j and 2j+1).
     bf16x8 hc[4];
@@ -161,7 +195,7 @@ __device__ __forceinline__ void chunk_step(const Ctx& cx, int c, f32x4 (&St)[8],
     f32x4 oacc = mfma_bf16_16x16x32(as_bf16x8(cur.qg[0]), hc[0], zero);
 #pragma unroll
     for (int j = 1; j < 4; ++j) oacc = mfma_bf16_16x16x32(as_bf16x8(cur.qg[j]), hc[j], oacc);
-    if (refill) issue_part<5, 10>(src, dst, cx.vt, cx.lane);
+    if (refill) issue_part<5, 10>(cx.rs, src, dst, cx.vt, cx.voff16);
     const f32x4 vacc = va + vb;
     const float u0 = __builtin_bit_cast(float, cur.u.x << 16);
     const float u1 = __builtin_bit_cast(float, cur.u.x & 0xffff0000u);
@@ -182,20 +216,21 @@ __device__ __forceinline__ void chunk_step(const Ctx& cx, int c, f32x4 (&St)[8],
     // o = scale * qg @ hc^T + Aqk @ v_new (kernels.py:268-279).
     oacc = oacc * cx.scale;
     oacc = mfma_bf16_16x16x16(as_i16x4(cur.aqk), vn, oacc);
-    if (refill) issue_part<10, LOADS_PER_CHUNK>(src, dst, cx.vt, cx.lane);
+    if (refill) issue_part<10, LOADS_PER_CHUNK>(cx.rs, src, dst, cx.vt, cx.voff16);
 
     // Operands of the next chunk: wait for its copy, read them while the
     // matrix ops above drain.
     if (c + 1 < cx.NT) {
         wait_chunk(min(RING - 2, cx.NT - 2 - c));
-        read_ops(ring + ((S + 1) % RING) * SLOT, cx.lane, cx.q4, cur);
+        read_ops(ring + ((S + 1) % RING) * SLOT, cx.lane, cx.q4, cx.vt, cur);
     }
 
-    // o[4*q4 + i][16*vt + x]: each row of the tile is 32 contiguous bytes.
-    const int t0 = c * BT + 4 * cx.q4;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        if (t0 + i < cx.T) cx.obase[(int64_t)(t0 + i) * cx.orow_stride] = f2bf(oacc[i]);
+    // o: lane (x = 4a + b, q4) holds o[4*q4 + i][16*vt + x], i = 0..3.  A
+    // 4x4 transpose of 16-bit values inside each quad of lanes leaves lane b
+    // with row 4*q4 + b, columns 4a..4a+3: one 8-byte store per lane.
+    const u32x2 ot = quad_transpose(pack2(oacc[0], oacc[1]), pack2(oacc[2], oacc[3]), cx.lane & 3);
+    const int t = c * BT + 4 * cx.q4 + (cx.lane & 3);
+    if (t < cx.T) *reinterpret_cast<u32x2*>(cx.obase + (int64_t)t * cx.orow_stride) = ot;
 }
 
 __global__ __launch_bounds__(64) void k2_kernel(Params p) {
@@ -234,8 +269,10 @@ __global__ __launch_bounds__(64) void k2_kernel(Params p) {
     }
 
     Ctx cx;
-    cx.rec = p.ws + (int64_t)bh * NT * REC_BYTES;
-    cx.obase = p.o + ((int64_t)b * T * H + h) * DK + v;
+    cx.rs = __builtin_amdgcn_make_buffer_rsrc(p.ws + (int64_t)bh * NT * REC_BYTES, (short)0,
+                                              NT * REC_BYTES, BUF_DWORD3);
+    cx.voff16 = lane * 16;
+    cx.obase = p.o + ((int64_t)b * T * H + h) * DK + 16 * vt + 4 * (x >> 2);
     cx.orow_stride = (int64_t)H * DK;
     cx.scale = p.scale;
     cx.NT = NT;
@@ -247,10 +284,11 @@ __global__ __launch_bounds__(64) void k2_kernel(Params p) {
 
 #pragma unroll
     for (int d = 0; d < RING - 1; ++d)
-        if (d < NT) issue_chunk(cx.rec + (int64_t)d * REC_BYTES, ring_lds() + d * SLOT, vt, lane);
+        if (d < NT)
+            issue_chunk(cx.rs, (uint32_t)d * REC_BYTES, ring_lds() + d * SLOT, vt, cx.voff16);
     wait_chunk(min(RING - 2, NT - 1));
     Ops cur;
-    read_ops(ring, lane, q4, cur);
+    read_ops(ring, lane, q4, vt, cur);
 
     static_assert(RING == 5, "the unrolled loop below names every slot");
     for (int c = 0; c < NT; c += RING) {
