@@ -71,7 +71,7 @@ int to_params(const KdaBt16Args* a, Params& p, bool need_inputs, bool need_outpu
     p.use_gate = use_gate;
     p.use_l2norm = (a->flags & KDA_BT16_USE_QK_L2NORM) != 0;
     p.use_beta_sigmoid = (a->flags & KDA_BT16_USE_BETA_SIGMOID) != 0;
-    p.state_v_first = (a->flags & KDA_BT16_STATE_V_FIRST) != 0;
+    p.h0_v_first = p.ht_v_first = (a->flags & KDA_BT16_STATE_V_FIRST) != 0;
     // Grid sizes are 32-bit: B*H*NT work-groups for stage 1, B*H*8 for stage 2.
     if ((int64_t)p.B * p.H * p.NT > 0x7fffffffLL) return KDA_BT16_EUNSUPPORTED;
     return KDA_BT16_OK;

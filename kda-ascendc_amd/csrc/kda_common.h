@@ -63,9 +63,9 @@ struct Params {
     const void* beta;
     const float* A_log;
     const float* dt_bias;
-    const float* h0;
+    const float* h0;  // initial state (null: zeros)
     uint16_t* o;
-    float* ht;
+    float* ht;        // final state (null: not stored)
     uint8_t* ws;
     uint16_t* dbg_Aqk;
     uint16_t* dbg_A_inv;
@@ -75,7 +75,8 @@ struct Params {
     int B, T, H, NT;
     float scale, lower_bound;
     int g_bf16, beta_bf16;
-    int use_gate, use_l2norm, use_beta_sigmoid, state_v_first;
+    int use_gate, use_l2norm, use_beta_sigmoid;
+    int h0_v_first, ht_v_first;  // layouts of h0 / ht: [V, K] if set, else [K, V]
 };
 
 // bf16 <-> fp32.  fp32 -> bf16 rounds to nearest even (the hardware

@@ -259,7 +259,7 @@ __global__ __launch_bounds__(64) void k2_kernel(Params p) {
         St[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
         if (p.h0) {
             const int k0 = 16 * kt + 4 * q4;
-            if (p.state_v_first) {
+            if (p.h0_v_first) {
                 St[kt] = *reinterpret_cast<const f32x4*>(p.h0 + sbase + (int64_t)v * DK + k0);
             } else {
 #pragma unroll
@@ -303,7 +303,7 @@ __global__ __launch_bounds__(64) void k2_kernel(Params p) {
 #pragma unroll
         for (int kt = 0; kt < 8; ++kt) {
             const int k0 = 16 * kt + 4 * q4;
-            if (p.state_v_first) {
+            if (p.ht_v_first) {
                 *reinterpret_cast<f32x4*>(p.ht + sbase + (int64_t)v * DK + k0) = St[kt];
             } else {
 #pragma unroll
