@@ -57,7 +57,9 @@ extern "C" {
 #define KDA_BT16_EINVAL            -1 /* null pointer, non-positive size, bad dtype tag,
                                          misaligned tensor (16 B; beta its element size;
                                          Aqk/A_inv 8 B) */
-#define KDA_BT16_EUNSUPPORTED      -2 /* K != 128, V != 128 or HV != H (kernels.py:727-730) */
+#define KDA_BT16_EUNSUPPORTED      -2 /* K != 128, V != 128 or HV != H (kernels.py:727-730);
+                                         also T * H * B or T beyond the 32-bit grid and
+                                         per-head record sizes (T > 1973776) */
 #define KDA_BT16_EWORKSPACE        -3 /* workspace missing or smaller than kda_bt16_workspace_bytes */
 #define KDA_BT16_ELAUNCH           -4 /* HIP launch error */
 #define KDA_BT16_EABI              -5 /* args->abi_version != KDA_BT16_ABI_VERSION */

@@ -19,6 +19,12 @@ int to_params(const KdaBt16Args* a, Params& p, bool need_inputs, bool need_outpu
     if (a->B <= 0 || a->T <= 0 || a->H <= 0 || a->HV <= 0 || a->K <= 0 || a->V <= 0)
         return KDA_BT16_EINVAL;
     if (a->K != kda::DK || a->V != kda::DK || a->HV != a->H) return KDA_BT16_EUNSUPPORTED;
+    // Grid sizes are 32-bit (B*H*NT work-groups for stage 1, B*H*8 for stage
+    // 2), and stage 2 addresses one head's records through a buffer
+    // descriptor with a 32-bit size (NT * REC_BYTES bytes).
+    const int64_t nt = ((int64_t)a->T + kda::BT - 1) / kda::BT;
+    if ((int64_t)a->B * a->H * nt > 0x7fffffffLL || nt * kda::REC_BYTES > 0x7fffffffLL)
+        return KDA_BT16_EUNSUPPORTED;
     if ((a->g_dtype != KDA_BT16_DTYPE_F32 && a->g_dtype != KDA_BT16_DTYPE_BF16) ||
         (a->beta_dtype != KDA_BT16_DTYPE_F32 && a->beta_dtype != KDA_BT16_DTYPE_BF16))
         return KDA_BT16_EINVAL;
@@ -72,8 +78,6 @@ int to_params(const KdaBt16Args* a, Params& p, bool need_inputs, bool need_outpu
     p.use_l2norm = (a->flags & KDA_BT16_USE_QK_L2NORM) != 0;
     p.use_beta_sigmoid = (a->flags & KDA_BT16_USE_BETA_SIGMOID) != 0;
     p.h0_v_first = p.ht_v_first = (a->flags & KDA_BT16_STATE_V_FIRST) != 0;
-    // Grid sizes are 32-bit: B*H*NT work-groups for stage 1, B*H*8 for stage 2.
-    if ((int64_t)p.B * p.H * p.NT > 0x7fffffffLL) return KDA_BT16_EUNSUPPORTED;
     return KDA_BT16_OK;
 }
 
@@ -117,7 +121,7 @@ const char* kda_bt16_strerror(int code) {
     switch (code) {
         case KDA_BT16_OK: return "ok";
         case KDA_BT16_EINVAL: return "invalid argument (null pointer, non-positive size or bad dtype tag)";
-        case KDA_BT16_EUNSUPPORTED: return "unsupported geometry (needs K=V=128 and HV == H)";
+        case KDA_BT16_EUNSUPPORTED: return "unsupported geometry (needs K=V=128, HV == H and T <= 1973776)";
         case KDA_BT16_EWORKSPACE: return "workspace missing, misaligned or smaller than kda_bt16_workspace_bytes()";
         case KDA_BT16_ELAUNCH: return "HIP kernel launch failed";
         case KDA_BT16_EABI: return "abi_version mismatch";

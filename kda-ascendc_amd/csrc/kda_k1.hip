@@ -273,14 +273,18 @@ __global__ __launch_bounds__(64) void k1_kernel(Params p) {
         *reinterpret_cast<u32x4*>(rec + REC_QG + j * 1024 + lane * 16) =
             u32x4{qgp[2 * j].x, qgp[2 * j].y, qgp[2 * j + 1].x, qgp[2 * j + 1].y};
     __syncthreads();
+    // The record holds -w (stage 2 forms u - w @ hc^T as one accumulation
+    // that starts at u): the product with -A, exact since negation commutes
+    // with the bf16 products, the fp32 sums and the rounding.
     u32x2 wpk[8];
     {
         i16x4 kbT[8];
         load_lds_T(s_T, r, q4, kbT);
+        const i16x4 A_neg = as_i16x4(ainv_bf ^ 0x80008000u);
 #pragma unroll
         for (int kt = 0; kt < 8; ++kt) {
             const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-            wpk[kt] = pack4(mfma_bf16_16x16x16(kbT[kt], A_op, zero));
+            wpk[kt] = pack4(mfma_bf16_16x16x16(kbT[kt], A_neg, zero));
         }
     }
 #pragma unroll
@@ -324,7 +328,7 @@ __global__ __launch_bounds__(64) void k1_kernel(Params p) {
         *reinterpret_cast<u32x2*>(p.dbg_A_inv + bt16) = ainv_bf;
 #pragma unroll
         for (int kt = 0; kt < 8; ++kt) {
-            *reinterpret_cast<u32x2*>(p.dbg_w + rowoff + 16 * kt + colbase) = wpk[kt];
+            *reinterpret_cast<u32x2*>(p.dbg_w + rowoff + 16 * kt + colbase) = wpk[kt] ^ 0x80008000u;
             *reinterpret_cast<f32x4*>(p.dbg_g + rowoff + 16 * kt + colbase) =
                 f32x4{G[4 * kt + 0], G[4 * kt + 1], G[4 * kt + 2], G[4 * kt + 3]};
         }

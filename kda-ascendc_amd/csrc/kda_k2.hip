@@ -6,121 +6,154 @@
 //   v_new = bf16(u - w @ hc^T)
 //   o     = bf16(scale * (qg @ hc^T) + Aqk @ v_new)
 //   S     = S * 2^G_last[None, :] + (kg^T @ v_new)^T
-// with S the [V, K] fp32 state.  One 64-lane wave owns 16 value columns of
-// one (batch, head) and keeps its slice of S transposed, S^T[k][v], as eight
-// 16x16 fp32 accumulator tiles.  The 16x16 accumulator layout (lane
-// v + 16*(k/4), item k%4) is exactly the B-operand layout of the 16x16x16
-// bf16 matrix op, so bf16(S) feeds the next chunk's products straight from
-// registers: the serial chain itself never goes through LDS.  Pairs of
-// k-tiles form the 8-deep operands of the 16x16x32 op for w @ hc^T and
-// qg @ hc^T; stage 1 stored w and qg in the matching k order.
+// with S the [V, K] fp32 state.
+//
+// One work-group of three waves per (batch, head, 16 value columns), each
+// wave on its own SIMD:
+//   * the state wave runs the recurrence.  It keeps its slice of S
+//     transposed, S^T[k][v], as eight 16x16 fp32 accumulator tiles; the
+//     16x16 accumulator layout (lane v + 16*(k/4), item k%4) is exactly the
+//     B-operand layout of the 16x16x16 bf16 matrix op, so bf16(S) feeds the
+//     next chunk's products straight from registers.  Pairs of k-tiles form
+//     the 8-deep operands of the 16x16x32 op for w @ hc^T; stage 1 stored w
+//     and qg in the matching k order.  It reads the next chunk's operands
+//     while it computes this one, and hands hc and v_new to the output wave.
+//   * the output wave forms o one chunk behind, from hc, v_new, qg and Aqk,
+//     and stores it.
+//   * the copy wave streams the chunk records from HBM into an LDS ring
+//     ahead of use (gfx950 direct buffer->LDS loads).
+// The three meet at one barrier per chunk.  Only the copy wave waits on
+// loads and only the output wave stores, so neither memory latency sits on
+// the state wave's chain.
 #include "kda_common.h"
 
 namespace kda {
 
 namespace {
 
-// Records stream through an LDS ring of RING slots with the gfx950 direct
-// global->LDS loads (buffer_load_dwordx4 ... lds: 16 B per lane, 1 KiB per
-// wave instruction), issued RING-1 chunks ahead of use.  A wave copies the
-// 13 KiB every value tile needs plus the 1 KiB pair of u slices that holds
-// its own 512-byte slice: 14 loads per chunk.  The loads complete in issue
-// order, so before reading a slot the wave waits until at most
-// 14 * (chunks issued after it) loads are outstanding; stores counted in the
-// same counter only lengthen that wait.  A wave may have at most 63 vector
-// memory operations in flight (the vmcnt field is 6 bits) before issue
-// stalls: (RING - 1) * 14 loads plus the step's single store stay below.
-constexpr int RING = 5;
-constexpr int SHARED_LOADS = REC_SHARED / 1024;
+// Record ring: RING slots, each the 13 KiB every value tile needs plus the
+// 1 KiB pair of u slices that holds this tile's (14 loads of 1 KiB).
+// Chunk j lives in slot j % RING.  The state wave reads it during chunk
+// j - 1, the output wave during chunk j + 1, and the copy wave refills the
+// slot with chunk j + RING during chunk j + RING - LEAD; LEAD <= RING - 2
+// keeps the refill after both reads.  The copy wave issues chunk c + LEAD
+// during chunk c and, before the barrier that ends chunk c, waits for chunk
+// c + 2 (read by the state wave during chunk c + 1): its loads complete in
+// issue order, so that wait leaves at most 14 * (LEAD - 2) loads
+// outstanding.
+constexpr int RING = 6;
+constexpr int LEAD = 4;
+constexpr int SHARED_LOADS = REC_SHARED / 1024;  // 13
 constexpr int LOADS_PER_CHUNK = SHARED_LOADS + 1;
 constexpr int SLOT = REC_SHARED + 1024;
 static_assert(SHARED_LOADS * 1024 == REC_SHARED, "shared part must be whole KiB");
-static_assert((RING - 1) * LOADS_PER_CHUNK + 1 <= 63, "vmcnt is a 6-bit count");
+static_assert(RING % 2 == 0, "hand-off buffers alternate with the chunk parity");
+static_assert(LEAD >= 2 && LEAD <= RING - 2, "ring reuse order");
+static_assert((LEAD - 1) * LOADS_PER_CHUNK <= 63, "vmcnt is a 6-bit count");
+
+// Hand-off from the state wave to the output wave, double-buffered by chunk
+// parity: hc as the four 16x16x32 B operands (lane l's 16 bytes of operand
+// j at 1024 * j + 16 * l) and v_new as the 16x16x16 B operand (8 bytes at
+// 8 * l).
+constexpr int HC_BYTES = 4 * 1024;
+constexpr int VN_BYTES = 512;
 
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N));
 }
 
-// Wait until the chunk followed by `n_after` issued chunks has landed.
-__device__ __forceinline__ void wait_chunk(int n_after) {
-    static_assert(RING == 5, "ladder below covers 0..4 later chunks");
-    if (n_after >= 4) {
-        wait_vmcnt<4 * LOADS_PER_CHUNK>();
-    } else if (n_after == 3) {
-        wait_vmcnt<3 * LOADS_PER_CHUNK>();
-    } else if (n_after == 2) {
-        wait_vmcnt<2 * LOADS_PER_CHUNK>();
-    } else if (n_after == 1) {
-        wait_vmcnt<LOADS_PER_CHUNK>();
-    } else {
+// Copy wave: wait until the chunk followed by `n_after` issued chunks has
+// landed (0 <= n_after <= LEAD - 2).
+template <int N>
+__device__ __forceinline__ void wait_chunk_ladder(int n_after) {
+    if constexpr (N == 0) {
         wait_vmcnt<0>();
+    } else {
+        if (n_after >= N) {
+            wait_vmcnt<N * LOADS_PER_CHUNK>();
+        } else {
+            wait_chunk_ladder<N - 1>(n_after);
+        }
     }
 }
+
+__device__ __forceinline__ void wait_chunk(int n_after) { wait_chunk_ladder<LEAD - 2>(n_after); }
 
 // Buffer descriptor word 3 for raw byte-addressed buffers on gfx9-family
 // parts (gfx950 included).
 constexpr int BUF_DWORD3 = 0x00020000;
 
-// Loads [I0, I1) of one chunk's copy; index SHARED_LOADS is the 1 KiB pair
-// of u slices (value tiles 2*(vt/2) and 2*(vt/2)+1), always inside the
-// record.  Buffer loads with the chunk offset in an SGPR and a fixed
-// per-lane VGPR offset: no per-step address arithmetic on the vector ALU.
-template <int I0, int I1>
-__device__ __forceinline__ void issue_part(__amdgpu_buffer_rsrc_t rs, uint32_t chunk_off,
-                                           lds_u8* slot, int vt, uint32_t voff16) {
+// One chunk's copy: 13 shared KiB, then the u pair.  Buffer loads with the
+// chunk offset in an SGPR and a fixed per-lane VGPR offset.
+__device__ __forceinline__ void issue_chunk(__amdgpu_buffer_rsrc_t rs, uint32_t chunk_off,
+                                            lds_u8* slot, uint32_t u_off, uint32_t voff16) {
 #pragma unroll
-    for (int i = I0; i < I1; ++i) {
-        const uint32_t src = i < SHARED_LOADS ? chunk_off + i * 1024
-                                              : chunk_off + REC_U + (uint32_t)(vt >> 1) * 1024;
+    for (int i = 0; i < LOADS_PER_CHUNK; ++i) {
+        const uint32_t src = i < SHARED_LOADS ? chunk_off + i * 1024 : chunk_off + u_off;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_u8*)(slot + i * 1024), 16, voff16, src,
                                                  0, 0);
     }
 }
 
-__device__ __forceinline__ void issue_chunk(__amdgpu_buffer_rsrc_t rs, uint32_t chunk_off,
-                                            lds_u8* slot, int vt, uint32_t voff16) {
-    issue_part<0, LOADS_PER_CHUNK>(rs, chunk_off, slot, vt, voff16);
-}
-
-// One chunk's operands in registers, read from the ring one step ahead.
-// Every ring read sits right after the explicit wait for its chunk: the
-// compiler cannot tell ring slots apart, and a ring read that follows a
-// direct-to-LDS load issue without such a wait gets a conservative
-// vmcnt(0) from it, which would stall every step on the newest load.
-struct Ops {
+// The state wave's operands of one chunk.
+struct StateOps {
     u32x4 w[4];
-    u32x4 qg[4];
     u32x4 kg[4];
     f32x4 dc[8];
-    u32x2 aqk;
     u32x2 u;
 };
 
-__device__ __forceinline__ void read_ops(const uint8_t* slot, int lane, int q4, int vt, Ops& op) {
+// Read in two parts, so that no more LDS reads are outstanding than the
+// 4-bit lgkmcnt can count (otherwise the compiler waits for all of them).
+__device__ __forceinline__ void read_state_ops_a(const uint8_t* slot, int lane, int vt,
+                                                 StateOps& op) {
 #pragma unroll
     for (int j = 0; j < 4; ++j)
         op.w[j] = *reinterpret_cast<const u32x4*>(slot + REC_W + j * 1024 + lane * 16);
     op.u = *reinterpret_cast<const u32x2*>(slot + REC_SHARED + (vt & 1) * 512 + lane * 8);
-    op.aqk = *reinterpret_cast<const u32x2*>(slot + REC_AQK + lane * 8);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        op.qg[j] = *reinterpret_cast<const u32x4*>(slot + REC_QG + j * 1024 + lane * 16);
+    for (int j = 0; j < 4; ++j)
         op.kg[j] = *reinterpret_cast<const u32x4*>(slot + REC_KG + j * 1024 + lane * 16);
-    }
+}
+
+__device__ __forceinline__ void read_state_ops_b(const uint8_t* slot, int q4, StateOps& op) {
 #pragma unroll
     for (int kt = 0; kt < 8; ++kt)
         op.dc[kt] = *reinterpret_cast<const f32x4*>(slot + REC_DECAY + kt * 64 + q4 * 16);
 }
 
-// The record ring (one per work-group).  Referenced by name everywhere, so
-// every ring address is a known LDS offset; the direct loads take it as an
-// LDS-space pointer, cast before any offset is applied.
+// The record ring and the hand-off buffers of the work-group, referenced
+// by name so that every address is a known LDS offset.  The direct loads
+// take the ring as an LDS-space pointer, cast before any offset is applied.
 __shared__ __attribute__((aligned(1024))) uint8_t ring[RING * SLOT];
+__shared__ __attribute__((aligned(1024))) uint8_t hc_buf[2][HC_BYTES];
+__shared__ __attribute__((aligned(16))) uint8_t vn_buf[2][VN_BYTES];
 
 __device__ __forceinline__ lds_u8* ring_lds() { return (lds_u8*)ring; }
+
+// s_waitcnt immediate for "lgkmcnt(0)" on gfx9-family parts: vmcnt field
+// (bits 3:0 and 15:14) and expcnt (bits 6:4) at their maxima, lgkmcnt
+// (bits 11:8) zero.
+constexpr int WAITCNT_LGKM0 = 0xC07F;
+
+// Chunk barrier of the state and output waves: their LDS writes (hand-off)
+// and reads are complete, then all three waves meet.  The wait and barrier
+// are one inline asm block whose memory clobber keeps every LDS access on
+// its side; as asm, the barrier carries no implied wait on the output
+// wave's stores.  The builtin wait after it costs nothing (the count is
+// already zero) but tells the compiler so, which keeps it from adding
+// conservative waits for LDS reads issued before the barrier.
+__device__ __forceinline__ void chunk_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(WAITCNT_LGKM0);
+}
+
+// The copy wave's side of the barrier: no clobber, so the compiler adds no
+// wait for its loads in flight.
+__device__ __forceinline__ void copy_barrier() { asm volatile("s_barrier"); }
 
 // 4x4 transpose of 16-bit values across the 4 lanes of a quad.  Lane j
 // enters with p0 = (M[0][j], M[1][j]) and p1 = (M[2][j], M[3][j]) and leaves
@@ -150,107 +183,267 @@ __device__ __forceinline__ u32x2 quad_transpose(uint32_t p0, uint32_t p1, int j)
     return u32x2{w0, w1};
 }
 
-// Per-wave constants of the chunk loop.
+// Constants of the chunk loop.
 struct Ctx {
-    __amdgpu_buffer_rsrc_t rs;  // this head's records, NT * REC_BYTES bytes
-    uint32_t voff16;            // lane * 16
-    uint16_t* obase;     // o[b, 0, h, 16*vt + 4*((lane%16)/4)]
-    int64_t orow_stride; // elements between consecutive tokens of o
+    __amdgpu_buffer_rsrc_t rs;  // copy: this head's records, NT * REC_BYTES bytes
+    uint32_t voff16;            // copy: lane * 16
+    uint32_t u_off;             // copy: REC_U + 1024 * (vt / 2)
+    uint16_t* obase;            // output: o[b, 0, h, 16*vt + 4*((lane%16)/4)]
+    int64_t orow_stride;        // output: elements between consecutive tokens of o
     float scale;
-    int NT, T, lane, q4, x, vt;
+    int NT, T, lane, q4, vt;
 };
 
-// One chunk of the recurrence.  S (the ring slot of chunk c) is a template
-// argument so that every ring offset is a compile-time constant: alias
-// analysis then sees that the slot being refilled, the slot being read and
-// the slot being prefetched are disjoint, and no conservative wait on the
-// newest direct-to-LDS load is inserted.
+// State wave, chunk c in ring slot S (a template argument, so every LDS
+// offset is a compile-time constant).
+//
+// The step is software-pipelined across the chunk boundary: it starts with
+// the state update of chunk c - 1,
+//   S = S * 2^G_last + kg^T v_new      (kernels.py:281-294; S * 2^G_last
+//                                       was formed during chunk c - 1),
+// then forms chunk c's
+//   hc = bf16(S),  v_new = bf16(u - w @ hc^T)   (kernels.py:261-266)
+// with one accumulation chain that starts at u (the record holds -w), and
+// hands hc and v_new to the output wave.  One wave issues at most one
+// instruction per four cycles and stalls behind a matrix op the busy pipe
+// cannot take, so the step is laid out by hand in small fenced groups that
+// put VALU work (conversions, decay products, unpacking u) and LDS traffic
+// (chunk c + 1's operands, the hand-off) behind each matrix op.
+//
+// op[S & 1] holds chunk c's operands.  op[(S + 1) & 1] holds chunk c - 1's
+// until its kg has fed the update products, then receives chunk c + 1's.
+// vn carries v_new from one step to the next.
+template <int S, bool HAS_PREV, bool HAS_NEXT>
+__device__ __forceinline__ void state_step(const Ctx& cx, f32x4 (&St)[8], StateOps (&op)[2],
+                                           i16x4& vn) {
+    const StateOps& cur = op[S & 1];
+    StateOps& oth = op[(S + 1) & 1];
+    const uint8_t* ns = ring + ((S + 1) % RING) * SLOT;
+    uint8_t* hbuf = hc_buf[S & 1] + cx.lane * 16;
+    const int lane = cx.lane;
+
+    auto update = [&](int kt) {  // tile kt of chunk c - 1's update
+        if (HAS_PREV) {
+            const u32x4 kg = oth.kg[kt >> 1];
+            const u32x2 a = (kt & 1) ? u32x2{kg.z, kg.w} : u32x2{kg.x, kg.y};
+            St[kt] = mfma_bf16_16x16x16(as_i16x4(a), vn, St[kt]);
+        }
+    };
+    auto read_w = [&](int j) {
+        if (HAS_NEXT) oth.w[j] = *reinterpret_cast<const u32x4*>(ns + REC_W + j * 1024 + lane * 16);
+    };
+    auto read_kg = [&](int j) {
+        if (HAS_NEXT)
+            oth.kg[j] = *reinterpret_cast<const u32x4*>(ns + REC_KG + j * 1024 + lane * 16);
+    };
+    auto read_dc = [&](int kt) {
+        if (HAS_NEXT)
+            oth.dc[kt] = *reinterpret_cast<const f32x4*>(ns + REC_DECAY + kt * 64 + cx.q4 * 16);
+    };
+    auto pack_hc = [&](int j) {  // bf16(S^T) of k-tiles 2j, 2j+1: a 16x16x32 B operand
+        return u32x4{pack2(St[2 * j][0], St[2 * j][1]), pack2(St[2 * j][2], St[2 * j][3]),
+                     pack2(St[2 * j + 1][0], St[2 * j + 1][1]),
+                     pack2(St[2 * j + 1][2], St[2 * j + 1][3])};
+    };
+    auto decay = [&](int j) {
+        St[2 * j] = St[2 * j] * cur.dc[2 * j];
+        St[2 * j + 1] = St[2 * j + 1] * cur.dc[2 * j + 1];
+    };
+#define KDA_FENCE() __builtin_amdgcn_sched_barrier(0)
+
+    // Matrix pipe order: U0 U1 U2 U3 W0 U4 U5 W1 U6 U7 W2 W3 (Ukt: update
+    // of tile kt, Wj: w product j).  Behind each, VALU work whose inputs
+    // are done: hc_j needs U(2j), U(2j+1); decay_j follows hc_j.
+    update(0);
+    read_w(0);
+    read_w(1);
+    KDA_FENCE();
+    update(1);
+    read_w(2);
+    read_w(3);
+    // u as the fp32 accumulator the chain starts from
+    const f32x4 u = {__builtin_bit_cast(float, cur.u.x << 16),
+                     __builtin_bit_cast(float, cur.u.x & 0xffff0000u),
+                     __builtin_bit_cast(float, cur.u.y << 16),
+                     __builtin_bit_cast(float, cur.u.y & 0xffff0000u)};
+    KDA_FENCE();
+    update(2);
+    const u32x4 hc0 = pack_hc(0);
+    KDA_FENCE();
+    update(3);
+    decay(0);
+    KDA_FENCE();
+    f32x4 va = mfma_bf16_16x16x32(as_bf16x8(cur.w[0]), as_bf16x8(hc0), u);
+    const u32x4 hc1 = pack_hc(1);
+    if (HAS_NEXT)
+        oth.u = *reinterpret_cast<const u32x2*>(ns + REC_SHARED + (cx.vt & 1) * 512 + lane * 8);
+    read_dc(0);
+    KDA_FENCE();
+    update(4);
+    decay(1);
+    KDA_FENCE();
+    update(5);
+    read_dc(1);
+    read_dc(2);
+    KDA_FENCE();
+    va = mfma_bf16_16x16x32(as_bf16x8(cur.w[1]), as_bf16x8(hc1), va);
+    *reinterpret_cast<u32x4*>(hbuf + 0 * 1024) = hc0;
+    *reinterpret_cast<u32x4*>(hbuf + 1 * 1024) = hc1;
+    KDA_FENCE();
+    update(6);
+    const u32x4 hc2 = pack_hc(2);
+    KDA_FENCE();
+    update(7);
+    decay(2);
+    read_dc(3);
+    read_dc(4);
+    KDA_FENCE();
+    va = mfma_bf16_16x16x32(as_bf16x8(cur.w[2]), as_bf16x8(hc2), va);
+    const u32x4 hc3 = pack_hc(3);
+    read_dc(5);
+    read_dc(6);
+    read_dc(7);
+    KDA_FENCE();
+    va = mfma_bf16_16x16x32(as_bf16x8(cur.w[3]), as_bf16x8(hc3), va);
+    decay(3);
+    *reinterpret_cast<u32x4*>(hbuf + 2 * 1024) = hc2;
+    *reinterpret_cast<u32x4*>(hbuf + 3 * 1024) = hc3;
+    read_kg(0);
+    read_kg(1);
+    read_kg(2);
+    read_kg(3);
+    KDA_FENCE();
+
+    const u32x2 vnb = {pack2(va[0], va[1]), pack2(va[2], va[3])};
+    *reinterpret_cast<u32x2*>(vn_buf[S & 1] + lane * 8) = vnb;
+    vn = as_i16x4(vnb);
+    chunk_barrier();
+    KDA_FENCE();
+    if (!HAS_NEXT) {
+        // the last chunk's update
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const u32x2 k0 = {cur.kg[j].x, cur.kg[j].y};
+            const u32x2 k1 = {cur.kg[j].z, cur.kg[j].w};
+            St[2 * j] = mfma_bf16_16x16x16(as_i16x4(k0), vn, St[2 * j]);
+            St[2 * j + 1] = mfma_bf16_16x16x16(as_i16x4(k1), vn, St[2 * j + 1]);
+        }
+    }
+#undef KDA_FENCE
+}
+
+// Output wave, chunk c (slot S) after the barrier that ends it:
+// o = scale * qg @ hc^T + Aqk @ v_new (kernels.py:268-279).
 template <int S>
-__device__ __forceinline__ void chunk_step(const Ctx& cx, int c, f32x4 (&St)[8], Ops& cur) {
-    // The copy of chunk c + RING - 1 goes out in three groups spread over
-    // the step, so the address unit drains them while the matrix ops run
-    // instead of stalling the wave on back-to-back issue.
-    const int cn = c + RING - 1;
-    const bool refill = cn < cx.NT;
-    const uint32_t src = (uint32_t)cn * REC_BYTES;
-    lds_u8* dst = ring_lds() + ((S + RING - 1) % RING) * SLOT;
-    if (refill) issue_part<0, 5>(cx.rs, src, dst, cx.vt, cx.voff16);
-
-    // hc = bf16(S), as 16x16x32 B operands (k-tiles 2j and 2j+1).
-    bf16x8 hc[4];
+__device__ __forceinline__ void output_step(const Ctx& cx, int c) {
+    chunk_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    const uint8_t* slot = ring + S * SLOT;
+    u32x4 hc[4], qg[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const u32x4 pk = {pack2(St[2 * j][0], St[2 * j][1]), pack2(St[2 * j][2], St[2 * j][3]),
-                          pack2(St[2 * j + 1][0], St[2 * j + 1][1]),
-                          pack2(St[2 * j + 1][2], St[2 * j + 1][3])};
-        hc[j] = as_bf16x8(pk);
+        hc[j] = *reinterpret_cast<const u32x4*>(hc_buf[S & 1] + j * 1024 + cx.lane * 16);
+        qg[j] = *reinterpret_cast<const u32x4*>(slot + REC_QG + j * 1024 + cx.lane * 16);
     }
-    // v_new = u - w @ hc^T, two independent accumulation chains
-    // (kernels.py:261-266), rounded to bf16.
+    const u32x2 vn = *reinterpret_cast<const u32x2*>(vn_buf[S & 1] + cx.lane * 8);
+    // Aqk is read 16 bytes at a time (this lane's 8 and its neighbour's):
+    // the compiler puts a vmcnt(0) before an 8-byte LDS read of the ring
+    // here, which would wait for this wave's own stores.
+    const u32x4 aq2 = *reinterpret_cast<const u32x4*>(slot + REC_AQK + (cx.lane >> 1) * 16);
+    const u32x2 aqk = (cx.lane & 1) ? u32x2{aq2.z, aq2.w} : u32x2{aq2.x, aq2.y};
     const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-    f32x4 va = mfma_bf16_16x16x32(as_bf16x8(cur.w[0]), hc[0], zero);
-    f32x4 vb = mfma_bf16_16x16x32(as_bf16x8(cur.w[2]), hc[2], zero);
-    va = mfma_bf16_16x16x32(as_bf16x8(cur.w[1]), hc[1], va);
-    vb = mfma_bf16_16x16x32(as_bf16x8(cur.w[3]), hc[3], vb);
-    f32x4 oacc = mfma_bf16_16x16x32(as_bf16x8(cur.qg[0]), hc[0], zero);
+    f32x4 oacc = mfma_bf16_16x16x32(as_bf16x8(qg[0]), as_bf16x8(hc[0]), zero);
 #pragma unroll
-    for (int j = 1; j < 4; ++j) oacc = mfma_bf16_16x16x32(as_bf16x8(cur.qg[j]), hc[j], oacc);
-    if (refill) issue_part<5, 10>(cx.rs, src, dst, cx.vt, cx.voff16);
-    const f32x4 vacc = va + vb;
-    const float u0 = __builtin_bit_cast(float, cur.u.x << 16);
-    const float u1 = __builtin_bit_cast(float, cur.u.x & 0xffff0000u);
-    const float u2 = __builtin_bit_cast(float, cur.u.y << 16);
-    const float u3 = __builtin_bit_cast(float, cur.u.y & 0xffff0000u);
-    const u32x2 vnb = {pack2(u0 - vacc[0], u1 - vacc[1]), pack2(u2 - vacc[2], u3 - vacc[3])};
-    const i16x4 vn = as_i16x4(vnb);
-
-    // S = S * 2^G_last + (kg^T @ v_new)^T (kernels.py:281-294).
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const u32x2 k0 = {cur.kg[j].x, cur.kg[j].y};
-        const u32x2 k1 = {cur.kg[j].z, cur.kg[j].w};
-        St[2 * j] = mfma_bf16_16x16x16(as_i16x4(k0), vn, St[2 * j] * cur.dc[2 * j]);
-        St[2 * j + 1] = mfma_bf16_16x16x16(as_i16x4(k1), vn, St[2 * j + 1] * cur.dc[2 * j + 1]);
-    }
-
-    // o = scale * qg @ hc^T + Aqk @ v_new (kernels.py:268-279).
+    for (int j = 1; j < 4; ++j)
+        oacc = mfma_bf16_16x16x32(as_bf16x8(qg[j]), as_bf16x8(hc[j]), oacc);
     oacc = oacc * cx.scale;
-    oacc = mfma_bf16_16x16x16(as_i16x4(cur.aqk), vn, oacc);
-    if (refill) issue_part<10, LOADS_PER_CHUNK>(cx.rs, src, dst, cx.vt, cx.voff16);
-
-    // Operands of the next chunk: wait for its copy, read them while the
-    // matrix ops above drain.
-    if (c + 1 < cx.NT) {
-        wait_chunk(min(RING - 2, cx.NT - 2 - c));
-        read_ops(ring + ((S + 1) % RING) * SLOT, cx.lane, cx.q4, cx.vt, cur);
-    }
-
-    // o: lane (x = 4a + b, q4) holds o[4*q4 + i][16*vt + x], i = 0..3.  A
-    // 4x4 transpose of 16-bit values inside each quad of lanes leaves lane b
-    // with row 4*q4 + b, columns 4a..4a+3: one 8-byte store per lane.
+    oacc = mfma_bf16_16x16x16(as_i16x4(aqk), as_i16x4(vn), oacc);
+    // Lane (x, q4) holds o rows 4*q4 .. +3 of column x; after the quad
+    // transpose it holds row 4*q4 + x%4, columns 4*(x/4) .. +3.
     const u32x2 ot = quad_transpose(pack2(oacc[0], oacc[1]), pack2(oacc[2], oacc[3]), cx.lane & 3);
     const int t = c * BT + 4 * cx.q4 + (cx.lane & 3);
     if (t < cx.T) *reinterpret_cast<u32x2*>(cx.obase + (int64_t)t * cx.orow_stride) = ot;
 }
 
-__global__ __launch_bounds__(64) void k2_kernel(Params p) {
+// Copy wave, chunk c (slot S).
+template <int S>
+__device__ __forceinline__ void copy_step(const Ctx& cx, int c) {
+    if (c + LEAD < cx.NT)
+        issue_chunk(cx.rs, (uint32_t)(c + LEAD) * REC_BYTES,
+                    ring_lds() + ((S + LEAD) % RING) * SLOT, cx.u_off, cx.voff16);
+    // chunk c + 2 is read by the state wave after this barrier
+    if (c + 2 < cx.NT) wait_chunk(min(LEAD - 2, cx.NT - 3 - c));
+    copy_barrier();
+}
 
-    const int lane = threadIdx.x;
-    const int x = lane & 15;  // value column inside the tile
-    const int q4 = lane >> 4;
-    const int H = p.H, T = p.T, NT = p.NT;
-    const int nbh = p.B * H;
+// One pass over the ring: chunks c .. c + RING - 1 (those below NT), each
+// with its slot as a compile-time constant.
+// N chunks from slot S on, each followed by another (so with a next
+// chunk to prefetch) and preceded by one.
+template <int S, int N>
+__device__ __forceinline__ void state_round_full(const Ctx& cx, f32x4 (&St)[8],
+                                                 StateOps (&op)[2], i16x4& vn) {
+    state_step<S, true, true>(cx, St, op, vn);
+    if constexpr (N > 1) state_round_full<(S + 1) % RING, N - 1>(cx, St, op, vn);
+}
 
-    // Work-group -> (head, value tile), XCD aware: consecutive work-group ids
-    // go to different XCDs round-robin, so the 8 tiles of one head get ids
-    // of one residue class mod 8 and share that XCD's L2 for the records.
-    const int wg = blockIdx.x;
-    const int lin = (wg & 7) * nbh + (wg >> 3);
-    const int bh = lin >> 3;
-    const int vt = lin & 7;
-    const int b = bh / H, h = bh - (bh / H) * H;
-    const int v = 16 * vt + x;
+// The remaining chunks c .. NT - 1 (at most N of them) from slot S on.
+template <int S, int N>
+__device__ __forceinline__ void state_round_tail(const Ctx& cx, int c, f32x4 (&St)[8],
+                                                 StateOps (&op)[2], i16x4& vn) {
+    if (c >= cx.NT) return;
+    if (c + 1 < cx.NT) {
+        state_step<S, true, true>(cx, St, op, vn);
+    } else {
+        state_step<S, true, false>(cx, St, op, vn);
+    }
+    if constexpr (N > 1) state_round_tail<(S + 1) % RING, N - 1>(cx, c + 1, St, op, vn);
+}
 
+template <int S>
+__device__ __forceinline__ void output_round(const Ctx& cx, int c) {
+    output_step<S>(cx, c);
+    if constexpr (S + 1 < RING) {
+        if (c + 1 < cx.NT) output_round<S + 1>(cx, c + 1);
+    }
+}
+
+template <int S>
+__device__ __forceinline__ void copy_round(const Ctx& cx, int c) {
+    copy_step<S>(cx, c);
+    if constexpr (S + 1 < RING) {
+        if (c + 1 < cx.NT) copy_round<S + 1>(cx, c + 1);
+    }
+}
+
+__device__ __forceinline__ void copy_wave(const Params& p, Ctx& cx, int bh) {
+    const int NT = cx.NT;
+    cx.rs = __builtin_amdgcn_make_buffer_rsrc(p.ws + (int64_t)bh * NT * REC_BYTES, (short)0,
+                                              NT * REC_BYTES, BUF_DWORD3);
+    cx.voff16 = cx.lane * 16;
+    cx.u_off = REC_U + 1024 * (cx.vt >> 1);
+#pragma unroll
+    for (int d = 0; d < LEAD; ++d)
+        if (d < NT)
+            issue_chunk(cx.rs, (uint32_t)d * REC_BYTES, ring_lds() + d * SLOT, cx.u_off,
+                        cx.voff16);
+    // chunks 0 and 1 (those that exist) before the first barrier
+    wait_chunk(NT >= 2 ? min(LEAD, NT) - 2 : 0);
+    copy_barrier();
+    for (int c = 0; c < NT; c += RING) copy_round<0>(cx, c);
+}
+
+__device__ __forceinline__ void output_wave(const Params& p, Ctx& cx, int b, int h) {
+    const int x = cx.lane & 15;
+    cx.obase = p.o + ((int64_t)b * cx.T * p.H + h) * DK + 16 * cx.vt + 4 * (x >> 2);
+    cx.orow_stride = (int64_t)p.H * DK;
+    chunk_barrier();
+    for (int c = 0; c < cx.NT; c += RING) output_round<0>(cx, c);
+}
+
+__device__ __forceinline__ void state_wave(const Params& p, const Ctx& cx, int bh) {
+    const int lane = cx.lane, q4 = cx.q4, vt = cx.vt;
+    const int v = 16 * vt + (lane & 15);
     // S^T tiles: St[kt][i] = S[v][16*kt + 4*q4 + i].
     f32x4 St[8];
     const int64_t sbase = (int64_t)bh * DK * DK;
@@ -267,37 +460,20 @@ __global__ __launch_bounds__(64) void k2_kernel(Params p) {
             }
         }
     }
-
-    Ctx cx;
-    cx.rs = __builtin_amdgcn_make_buffer_rsrc(p.ws + (int64_t)bh * NT * REC_BYTES, (short)0,
-                                              NT * REC_BYTES, BUF_DWORD3);
-    cx.voff16 = lane * 16;
-    cx.obase = p.o + ((int64_t)b * T * H + h) * DK + 16 * vt + 4 * (x >> 2);
-    cx.orow_stride = (int64_t)H * DK;
-    cx.scale = p.scale;
-    cx.NT = NT;
-    cx.T = T;
-    cx.lane = lane;
-    cx.q4 = q4;
-    cx.x = x;
-    cx.vt = vt;
-
-#pragma unroll
-    for (int d = 0; d < RING - 1; ++d)
-        if (d < NT)
-            issue_chunk(cx.rs, (uint32_t)d * REC_BYTES, ring_lds() + d * SLOT, vt, cx.voff16);
-    wait_chunk(min(RING - 2, NT - 1));
-    Ops cur;
-    read_ops(ring, lane, q4, vt, cur);
-
-    static_assert(RING == 5, "the unrolled loop below names every slot");
-    for (int c = 0; c < NT; c += RING) {
-        chunk_step<0>(cx, c, St, cur);
-        if (c + 1 < NT) chunk_step<1>(cx, c + 1, St, cur);
-        if (c + 2 < NT) chunk_step<2>(cx, c + 2, St, cur);
-        if (c + 3 < NT) chunk_step<3>(cx, c + 3, St, cur);
-        if (c + 4 < NT) chunk_step<4>(cx, c + 4, St, cur);
+    chunk_barrier();  // chunks 0 and 1 are in the ring
+    StateOps op[2];
+    read_state_ops_a(ring, lane, vt, op[0]);
+    read_state_ops_b(ring, q4, op[0]);
+    __builtin_amdgcn_s_waitcnt(WAITCNT_LGKM0);
+    i16x4 vn;
+    if (cx.NT > 1) {
+        state_step<0, false, true>(cx, St, op, vn);
+    } else {
+        state_step<0, false, false>(cx, St, op, vn);
     }
+    int c = 1;
+    for (; c + RING < cx.NT; c += RING) state_round_full<1, RING>(cx, St, op, vn);
+    state_round_tail<1 % RING, RING>(cx, c, St, op, vn);
 
     if (p.ht) {
 #pragma unroll
@@ -313,11 +489,50 @@ __global__ __launch_bounds__(64) void k2_kernel(Params p) {
     }
 }
 
+enum Role { STATE = 0, OUTPUT = 1, COPY = 2 };
+
+// Every wave executes exactly NT + 1 barriers: one after the prologue, then
+// one ending each chunk.  Each role ends its wave itself: with no join of
+// the roles' code paths, the compiler's wait analysis of one role never
+// sees another role's memory operations.
+__global__ __launch_bounds__(192) void k2_kernel(Params p) {
+    const int lane = threadIdx.x & 63;
+    const int role = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nbh = p.B * p.H;
+
+    // Work-group -> (head, value tile), XCD aware: consecutive work-group ids
+    // go to different XCDs round-robin, so the 8 tiles of one head get ids
+    // of one residue class mod 8 and share that XCD's L2 for the records.
+    const int wg = blockIdx.x;
+    const int lin = (wg & 7) * nbh + (wg >> 3);
+    const int bh = lin >> 3;
+    const int b = bh / p.H, h = bh - b * p.H;
+
+    Ctx cx;
+    cx.scale = p.scale;
+    cx.NT = p.NT;
+    cx.T = p.T;
+    cx.lane = lane;
+    cx.q4 = lane >> 4;
+    cx.vt = lin & 7;
+
+    if (role == STATE) {
+        state_wave(p, cx, bh);
+        __builtin_amdgcn_endpgm();
+    }
+    if (role == OUTPUT) {
+        output_wave(p, cx, b, h);
+        __builtin_amdgcn_endpgm();
+    }
+    copy_wave(p, cx, bh);
+    __builtin_amdgcn_endpgm();
+}
+
 }  // namespace
 
 hipError_t launch_k2(const Params& p, hipStream_t stream) {
     const int64_t grid = (int64_t)p.B * p.H * 8;
-    hipLaunchKernelGGL(k2_kernel, dim3((unsigned)grid), dim3(64), 0, stream, p);
+    hipLaunchKernelGGL(k2_kernel, dim3((unsigned)grid), dim3(192), 0, stream, p);
     return hipGetLastError();
 }
 

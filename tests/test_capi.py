@@ -84,6 +84,7 @@ def test_argument_checks_return_codes_without_launching(fn):
     assert f(ctypes.byref(_args(abi_version=99)), None) == -5
     assert f(ctypes.byref(_args(K=64)), None) == -2
     assert f(ctypes.byref(_args(HV=2)), None) == -2
+    assert f(ctypes.byref(_args(T=1973776 + 1)), None) == -2  # 32-bit per-head record size
     assert f(ctypes.byref(_args(T=0)), None) == -1
     assert f(ctypes.byref(_args(g_dtype=7)), None) == -1
     assert f(ctypes.byref(_args(flags=_hip.USE_GATE, lower_bound=-12.0)), None) == -6
