@@ -18,13 +18,15 @@
 //     the 8-deep operands of the 16x16x32 op for w @ hc^T; stage 1 stored w
 //     and qg in the matching k order.  It reads the next chunk's operands
 //     while it computes this one, and hands hc and v_new to the output wave.
-//   * the output wave forms o one chunk behind, from hc, v_new, qg and Aqk,
+//   * the output wave forms o two chunks behind, from hc, v_new, qg and Aqk,
 //     and stores it.
 //   * the copy wave streams the chunk records from HBM into an LDS ring
 //     ahead of use (gfx950 direct buffer->LDS loads).
 // The three meet at one barrier per chunk.  Only the copy wave waits on
 // loads and only the output wave stores, so neither memory latency sits on
 // the state wave's chain.
+#include <type_traits>
+
 #include "kda_common.h"
 
 namespace kda {
@@ -34,27 +36,29 @@ namespace {
 // Record ring: RING slots, each the 13 KiB every value tile needs plus the
 // 1 KiB pair of u slices that holds this tile's (14 loads of 1 KiB).
 // Chunk j lives in slot j % RING.  The state wave reads it during chunk
-// j - 1, the output wave during chunk j + 1, and the copy wave refills the
-// slot with chunk j + RING during chunk j + RING - LEAD; LEAD <= RING - 2
-// keeps the refill after both reads.  The copy wave issues chunk c + LEAD
-// during chunk c and, before the barrier that ends chunk c, waits for chunk
-// c + 2 (read by the state wave during chunk c + 1): its loads complete in
-// issue order, so that wait leaves at most 14 * (LEAD - 2) loads
-// outstanding.
-constexpr int RING = 6;
+// j - 1 and the output wave, two chunks behind, during chunk j + 2; the
+// copy wave refills the slot with chunk j + RING during chunk
+// j + RING - LEAD, and LEAD <= RING - 3 keeps that after both reads.  The
+// copy wave issues chunk c + LEAD during chunk c and, before the barrier
+// that ends chunk c, waits for chunk c + 2 (read by the state wave during
+// chunk c + 1): its loads complete in issue order, so that wait leaves at
+// most 14 * (LEAD - 2) loads outstanding.
+constexpr int RING = 8;
 constexpr int LEAD = 4;
+// Hand-off slots from the state wave to the output wave: chunk c's hc and
+// v_new are written during chunk c and read during chunk c + 2.
+constexpr int HANDOFF = 4;
 constexpr int SHARED_LOADS = REC_SHARED / 1024;  // 13
 constexpr int LOADS_PER_CHUNK = SHARED_LOADS + 1;
 constexpr int SLOT = REC_SHARED + 1024;
 static_assert(SHARED_LOADS * 1024 == REC_SHARED, "shared part must be whole KiB");
-static_assert(RING % 2 == 0, "hand-off buffers alternate with the chunk parity");
-static_assert(LEAD >= 2 && LEAD <= RING - 2, "ring reuse order");
+static_assert(RING % HANDOFF == 0 && RING % 2 == 0, "slot indices follow the chunk index");
+static_assert(LEAD >= 2 && LEAD <= RING - 3, "ring reuse order");
 static_assert((LEAD - 1) * LOADS_PER_CHUNK <= 63, "vmcnt is a 6-bit count");
 
-// Hand-off from the state wave to the output wave, double-buffered by chunk
-// parity: hc as the four 16x16x32 B operands (lane l's 16 bytes of operand
-// j at 1024 * j + 16 * l) and v_new as the 16x16x16 B operand (8 bytes at
-// 8 * l).
+// Hand-off from the state wave to the output wave, in slot c % HANDOFF:
+// hc as the four 16x16x32 B operands (lane l's 16 bytes of operand j at
+// 1024 * j + 16 * l) and v_new as the 16x16x16 B operand (8 bytes at 8 * l).
 constexpr int HC_BYTES = 4 * 1024;
 constexpr int VN_BYTES = 512;
 
@@ -102,12 +106,14 @@ __device__ __forceinline__ void issue_chunk(__amdgpu_buffer_rsrc_t rs, uint32_t 
 struct StateOps {
     u32x4 w[4];
     u32x4 kg[4];
-    f32x4 dc[8];
+    // 2^G_last[16*kt + 4*q4 + i] for the two (kt, i) with 4*kt + i = 2*x and
+    // 2*x + 1 (x = lane % 16); the 16 lanes of a row hold their row's 32.
+    f32x2 dc;
     u32x2 u;
 };
 
-// Read in two parts, so that no more LDS reads are outstanding than the
-// 4-bit lgkmcnt can count (otherwise the compiler waits for all of them).
+// The prologue's read of chunk 0's operands (inside the loop the next
+// chunk's operands are read piecewise, spread through the step).
 __device__ __forceinline__ void read_state_ops_a(const uint8_t* slot, int lane, int vt,
                                                  StateOps& op) {
 #pragma unroll
@@ -119,36 +125,67 @@ __device__ __forceinline__ void read_state_ops_a(const uint8_t* slot, int lane, 
         op.kg[j] = *reinterpret_cast<const u32x4*>(slot + REC_KG + j * 1024 + lane * 16);
 }
 
-__device__ __forceinline__ void read_state_ops_b(const uint8_t* slot, int q4, StateOps& op) {
-#pragma unroll
-    for (int kt = 0; kt < 8; ++kt)
-        op.dc[kt] = *reinterpret_cast<const f32x4*>(slot + REC_DECAY + kt * 64 + q4 * 16);
+// Lane (x, q4) reads 2^G_last at [kt = x/2][q4][i = 2*(x%2) .. +1].
+__device__ __forceinline__ uint32_t decay_offset(int lane) {
+    const int x = lane & 15, q4 = lane >> 4;
+    return REC_DECAY + (x >> 1) * 64 + q4 * 16 + (x & 1) * 8;
+}
+
+__device__ __forceinline__ void read_state_ops_b(const uint8_t* slot, int lane, StateOps& op) {
+    op.dc = *reinterpret_cast<const f32x2*>(slot + decay_offset(lane));
+}
+
+// Scales the state tile kt by its decay: element i of lane (x, q4) takes
+// 2^G_last[16*kt + 4*q4 + i] from lane 2*kt + i/2 of its row (DPP
+// row_newbcast), component i % 2.
+template <int LANE>
+__device__ __forceinline__ float row_bcast(float v) {
+    constexpr int ROW_NEWBCAST = 0x150;  // DPP: lane LANE of each row to the whole row
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                                 ROW_NEWBCAST + LANE, 0xf, 0xf,
+                                                                 false));
+}
+
+template <int KT>
+__device__ __forceinline__ f32x4 decay_tile(f32x4 st, f32x2 dc) {
+    return f32x4{st[0] * row_bcast<2 * KT>(dc.x), st[1] * row_bcast<2 * KT>(dc.y),
+                 st[2] * row_bcast<2 * KT + 1>(dc.x), st[3] * row_bcast<2 * KT + 1>(dc.y)};
 }
 
 // The record ring and the hand-off buffers of the work-group, referenced
 // by name so that every address is a known LDS offset.  The direct loads
 // take the ring as an LDS-space pointer, cast before any offset is applied.
 __shared__ __attribute__((aligned(1024))) uint8_t ring[RING * SLOT];
-__shared__ __attribute__((aligned(1024))) uint8_t hc_buf[2][HC_BYTES];
-__shared__ __attribute__((aligned(16))) uint8_t vn_buf[2][VN_BYTES];
+__shared__ __attribute__((aligned(1024))) uint8_t hc_buf[HANDOFF][HC_BYTES];
+__shared__ __attribute__((aligned(16))) uint8_t vn_buf[HANDOFF][VN_BYTES];
 
 __device__ __forceinline__ lds_u8* ring_lds() { return (lds_u8*)ring; }
 
-// s_waitcnt immediate for "lgkmcnt(0)" on gfx9-family parts: vmcnt field
-// (bits 3:0 and 15:14) and expcnt (bits 6:4) at their maxima, lgkmcnt
-// (bits 11:8) zero.
+// s_waitcnt immediates on gfx9-family parts: vmcnt field (bits 3:0 and
+// 15:14) and expcnt (bits 6:4) at their maxima, lgkmcnt (bits 11:8) 0 or 15.
 constexpr int WAITCNT_LGKM0 = 0xC07F;
+constexpr int WAITCNT_LGKM15 = 0xCF7F;
 
-// Chunk barrier of the state and output waves: their LDS writes (hand-off)
-// and reads are complete, then all three waves meet.  The wait and barrier
-// are one inline asm block whose memory clobber keeps every LDS access on
-// its side; as asm, the barrier carries no implied wait on the output
-// wave's stores.  The builtin wait after it costs nothing (the count is
-// already zero) but tells the compiler so, which keeps it from adding
-// conservative waits for LDS reads issued before the barrier.
+// Chunk barrier: the wave's LDS accesses are complete, then all three waves
+// meet.  The wait and barrier are one inline asm block whose memory clobber
+// keeps every LDS access on its side; as asm, the barrier carries no
+// implied wait on the output wave's stores.  The builtin wait after it
+// costs nothing (the count is already zero) but tells the compiler so,
+// which keeps it from adding conservative waits for LDS reads issued
+// before the barrier.
 __device__ __forceinline__ void chunk_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     __builtin_amdgcn_s_waitcnt(WAITCNT_LGKM0);
+}
+
+// The state wave's barrier after a chunk that is followed by another: its
+// last LDS accesses (the v_new hand-off, the next chunk's kg) need not be
+// complete yet.  The hand-off a chunk writes is read two barriers later;
+// every later chunk issues more than 15 LDS accesses before that barrier,
+// and LDS accesses complete in order, so lgkmcnt(15) there covers it.
+__device__ __forceinline__ void chunk_barrier_nodrain() {
+    asm volatile("s_waitcnt lgkmcnt(15)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(WAITCNT_LGKM15);
 }
 
 // The copy wave's side of the barrier: no clobber, so the compiler adds no
@@ -219,7 +256,7 @@ __device__ __forceinline__ void state_step(const Ctx& cx, f32x4 (&St)[8], StateO
     const StateOps& cur = op[S & 1];
     StateOps& oth = op[(S + 1) & 1];
     const uint8_t* ns = ring + ((S + 1) % RING) * SLOT;
-    uint8_t* hbuf = hc_buf[S & 1] + cx.lane * 16;
+    uint8_t* hbuf = hc_buf[S % HANDOFF] + cx.lane * 16;
     const int lane = cx.lane;
 
     auto update = [&](int kt) {  // tile kt of chunk c - 1's update
@@ -236,18 +273,18 @@ __device__ __forceinline__ void state_step(const Ctx& cx, f32x4 (&St)[8], StateO
         if (HAS_NEXT)
             oth.kg[j] = *reinterpret_cast<const u32x4*>(ns + REC_KG + j * 1024 + lane * 16);
     };
-    auto read_dc = [&](int kt) {
-        if (HAS_NEXT)
-            oth.dc[kt] = *reinterpret_cast<const f32x4*>(ns + REC_DECAY + kt * 64 + cx.q4 * 16);
+    auto read_dc = [&]() {
+        if (HAS_NEXT) oth.dc = *reinterpret_cast<const f32x2*>(ns + decay_offset(lane));
     };
     auto pack_hc = [&](int j) {  // bf16(S^T) of k-tiles 2j, 2j+1: a 16x16x32 B operand
         return u32x4{pack2(St[2 * j][0], St[2 * j][1]), pack2(St[2 * j][2], St[2 * j][3]),
                      pack2(St[2 * j + 1][0], St[2 * j + 1][1]),
                      pack2(St[2 * j + 1][2], St[2 * j + 1][3])};
     };
-    auto decay = [&](int j) {
-        St[2 * j] = St[2 * j] * cur.dc[2 * j];
-        St[2 * j + 1] = St[2 * j + 1] * cur.dc[2 * j + 1];
+    auto decay = [&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        St[2 * j] = decay_tile<2 * j>(St[2 * j], cur.dc);
+        St[2 * j + 1] = decay_tile<2 * j + 1>(St[2 * j + 1], cur.dc);
     };
 #define KDA_FENCE() __builtin_amdgcn_sched_barrier(0)
 
@@ -271,20 +308,18 @@ __device__ __forceinline__ void state_step(const Ctx& cx, f32x4 (&St)[8], StateO
     const u32x4 hc0 = pack_hc(0);
     KDA_FENCE();
     update(3);
-    decay(0);
+    decay(std::integral_constant<int, 0>{});
     KDA_FENCE();
     f32x4 va = mfma_bf16_16x16x32(as_bf16x8(cur.w[0]), as_bf16x8(hc0), u);
     const u32x4 hc1 = pack_hc(1);
     if (HAS_NEXT)
         oth.u = *reinterpret_cast<const u32x2*>(ns + REC_SHARED + (cx.vt & 1) * 512 + lane * 8);
-    read_dc(0);
+    read_dc();
     KDA_FENCE();
     update(4);
-    decay(1);
+    decay(std::integral_constant<int, 1>{});
     KDA_FENCE();
     update(5);
-    read_dc(1);
-    read_dc(2);
     KDA_FENCE();
     va = mfma_bf16_16x16x32(as_bf16x8(cur.w[1]), as_bf16x8(hc1), va);
     *reinterpret_cast<u32x4*>(hbuf + 0 * 1024) = hc0;
@@ -294,18 +329,13 @@ __device__ __forceinline__ void state_step(const Ctx& cx, f32x4 (&St)[8], StateO
     const u32x4 hc2 = pack_hc(2);
     KDA_FENCE();
     update(7);
-    decay(2);
-    read_dc(3);
-    read_dc(4);
+    decay(std::integral_constant<int, 2>{});
     KDA_FENCE();
     va = mfma_bf16_16x16x32(as_bf16x8(cur.w[2]), as_bf16x8(hc2), va);
     const u32x4 hc3 = pack_hc(3);
-    read_dc(5);
-    read_dc(6);
-    read_dc(7);
     KDA_FENCE();
     va = mfma_bf16_16x16x32(as_bf16x8(cur.w[3]), as_bf16x8(hc3), va);
-    decay(3);
+    decay(std::integral_constant<int, 3>{});
     *reinterpret_cast<u32x4*>(hbuf + 2 * 1024) = hc2;
     *reinterpret_cast<u32x4*>(hbuf + 3 * 1024) = hc3;
     read_kg(0);
@@ -315,9 +345,13 @@ __device__ __forceinline__ void state_step(const Ctx& cx, f32x4 (&St)[8], StateO
     KDA_FENCE();
 
     const u32x2 vnb = {pack2(va[0], va[1]), pack2(va[2], va[3])};
-    *reinterpret_cast<u32x2*>(vn_buf[S & 1] + lane * 8) = vnb;
+    *reinterpret_cast<u32x2*>(vn_buf[S % HANDOFF] + lane * 8) = vnb;
     vn = as_i16x4(vnb);
-    chunk_barrier();
+    if (HAS_NEXT) {
+        chunk_barrier_nodrain();
+    } else {
+        chunk_barrier();
+    }
     KDA_FENCE();
     if (!HAS_NEXT) {
         // the last chunk's update
@@ -332,7 +366,7 @@ __device__ __forceinline__ void state_step(const Ctx& cx, f32x4 (&St)[8], StateO
 #undef KDA_FENCE
 }
 
-// Output wave, chunk c (slot S) after the barrier that ends it:
+// Output wave, chunk c (slot S) after the barrier that ends chunk c + 1:
 // o = scale * qg @ hc^T + Aqk @ v_new (kernels.py:268-279).
 template <int S>
 __device__ __forceinline__ void output_step(const Ctx& cx, int c) {
@@ -342,10 +376,10 @@ __device__ __forceinline__ void output_step(const Ctx& cx, int c) {
     u32x4 hc[4], qg[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        hc[j] = *reinterpret_cast<const u32x4*>(hc_buf[S & 1] + j * 1024 + cx.lane * 16);
+        hc[j] = *reinterpret_cast<const u32x4*>(hc_buf[S % HANDOFF] + j * 1024 + cx.lane * 16);
         qg[j] = *reinterpret_cast<const u32x4*>(slot + REC_QG + j * 1024 + cx.lane * 16);
     }
-    const u32x2 vn = *reinterpret_cast<const u32x2*>(vn_buf[S & 1] + cx.lane * 8);
+    const u32x2 vn = *reinterpret_cast<const u32x2*>(vn_buf[S % HANDOFF] + cx.lane * 8);
     // Aqk is read 16 bytes at a time (this lane's 8 and its neighbour's):
     // the compiler puts a vmcnt(0) before an 8-byte LDS read of the ring
     // here, which would wait for this wave's own stores.
@@ -362,7 +396,9 @@ __device__ __forceinline__ void output_step(const Ctx& cx, int c) {
     // transpose it holds row 4*q4 + x%4, columns 4*(x/4) .. +3.
     const u32x2 ot = quad_transpose(pack2(oacc[0], oacc[1]), pack2(oacc[2], oacc[3]), cx.lane & 3);
     const int t = c * BT + 4 * cx.q4 + (cx.lane & 3);
-    if (t < cx.T) *reinterpret_cast<u32x2*>(cx.obase + (int64_t)t * cx.orow_stride) = ot;
+    // o is written once and never read back here: a non-temporal store.
+    if (t < cx.T)
+        __builtin_nontemporal_store(ot, reinterpret_cast<u32x2*>(cx.obase + (int64_t)t * cx.orow_stride));
 }
 
 // Copy wave, chunk c (slot S).
@@ -431,12 +467,14 @@ __device__ __forceinline__ void copy_wave(const Params& p, Ctx& cx, int bh) {
     wait_chunk(NT >= 2 ? min(LEAD, NT) - 2 : 0);
     copy_barrier();
     for (int c = 0; c < NT; c += RING) copy_round<0>(cx, c);
+    copy_barrier();  // the output wave's last chunk
 }
 
 __device__ __forceinline__ void output_wave(const Params& p, Ctx& cx, int b, int h) {
     const int x = cx.lane & 15;
     cx.obase = p.o + ((int64_t)b * cx.T * p.H + h) * DK + 16 * cx.vt + 4 * (x >> 2);
     cx.orow_stride = (int64_t)p.H * DK;
+    chunk_barrier();
     chunk_barrier();
     for (int c = 0; c < cx.NT; c += RING) output_round<0>(cx, c);
 }
@@ -463,7 +501,7 @@ __device__ __forceinline__ void state_wave(const Params& p, const Ctx& cx, int b
     chunk_barrier();  // chunks 0 and 1 are in the ring
     StateOps op[2];
     read_state_ops_a(ring, lane, vt, op[0]);
-    read_state_ops_b(ring, q4, op[0]);
+    read_state_ops_b(ring, lane, op[0]);
     __builtin_amdgcn_s_waitcnt(WAITCNT_LGKM0);
     i16x4 vn;
     if (cx.NT > 1) {
@@ -474,6 +512,7 @@ __device__ __forceinline__ void state_wave(const Params& p, const Ctx& cx, int b
     int c = 1;
     for (; c + RING < cx.NT; c += RING) state_round_full<1, RING>(cx, St, op, vn);
     state_round_tail<1 % RING, RING>(cx, c, St, op, vn);
+    chunk_barrier();  // the output wave's last chunk
 
     if (p.ht) {
 #pragma unroll
@@ -491,8 +530,9 @@ __device__ __forceinline__ void state_wave(const Params& p, const Ctx& cx, int b
 
 enum Role { STATE = 0, OUTPUT = 1, COPY = 2 };
 
-// Every wave executes exactly NT + 1 barriers: one after the prologue, then
-// one ending each chunk.  Each role ends its wave itself: with no join of
+// Every wave executes exactly NT + 2 barriers: one after the prologue, one
+// ending each chunk, and one more for the output wave's last chunk (it runs
+// two chunks behind the state wave).  Each role ends its wave itself: with no join of
 // the roles' code paths, the compiler's wait analysis of one role never
 // sees another role's memory operations.
 __global__ __launch_bounds__(192) void k2_kernel(Params p) {
