@@ -175,6 +175,9 @@ __global__ __launch_bounds__(64) void k1_kernel(Params p) {
         acc_kk = mfma_f32_16x16x4(kv * gk, kv * gq, acc_kk);
     }
 
+    // This chunk's record.  Its stores are non-temporal: the records are
+    // written once here and read once by stage 2, and left dirty in L2 they
+    // slow stage 2's own stores by the write-backs they force.
     uint8_t* rec = p.ws + ((int64_t)bh * NT + c) * REC_BYTES;
 
     f32x4 aqk, L;
@@ -185,7 +188,7 @@ __global__ __launch_bounds__(64) void k1_kernel(Params p) {
         L[i] = (r > s) ? acc_kk[i] * beta : 0.f;
     }
     const u32x2 aqk_bf = pack4(aqk);
-    *reinterpret_cast<u32x2*>(rec + REC_AQK + lane * 8) = aqk_bf;
+    __builtin_nontemporal_store(aqk_bf, reinterpret_cast<u32x2*>(rec + REC_AQK + lane * 8));
 
     // ---- (I + L)^-1 by forward substitution (kernels.py:157-167) ---------
     // Lane r solves column s = r: a[t] = A_inv[t][s], with a[s] = 1,
@@ -235,7 +238,8 @@ __global__ __launch_bounds__(64) void k1_kernel(Params p) {
         for (int vt = 0; vt < 8; ++vt) {
             const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
             const u32x2 ub = pack4(mfma_bf16_16x16x16(A_op, vbT[vt], zero));
-            *reinterpret_cast<u32x2*>(rec + REC_U + vt * 512 + lane * 8) = ub;
+            __builtin_nontemporal_store(
+                ub, reinterpret_cast<u32x2*>(rec + REC_U + vt * 512 + lane * 8));
             if (p.dbg_u) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -269,9 +273,11 @@ __global__ __launch_bounds__(64) void k1_kernel(Params p) {
         qgp[kt] = pack4(qg[0], qg[1], qg[2], qg[3]);
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-        *reinterpret_cast<u32x4*>(rec + REC_QG + j * 1024 + lane * 16) =
-            u32x4{qgp[2 * j].x, qgp[2 * j].y, qgp[2 * j + 1].x, qgp[2 * j + 1].y};
+    for (int j = 0; j < 4; ++j) {
+        const u32x4 qgj = {qgp[2 * j].x, qgp[2 * j].y, qgp[2 * j + 1].x, qgp[2 * j + 1].y};
+        __builtin_nontemporal_store(qgj,
+                                    reinterpret_cast<u32x4*>(rec + REC_QG + j * 1024 + lane * 16));
+    }
     __syncthreads();
     // The record holds -w (stage 2 forms u - w @ hc^T as one accumulation
     // that starts at u): the product with -A, exact since negation commutes
@@ -288,9 +294,10 @@ __global__ __launch_bounds__(64) void k1_kernel(Params p) {
         }
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-        *reinterpret_cast<u32x4*>(rec + REC_W + j * 1024 + lane * 16) =
-            u32x4{wpk[2 * j].x, wpk[2 * j].y, wpk[2 * j + 1].x, wpk[2 * j + 1].y};
+    for (int j = 0; j < 4; ++j) {
+        const u32x4 wj = {wpk[2 * j].x, wpk[2 * j].y, wpk[2 * j + 1].x, wpk[2 * j + 1].y};
+        __builtin_nontemporal_store(wj, reinterpret_cast<u32x4*>(rec + REC_W + j * 1024 + lane * 16));
+    }
     __syncthreads();
 
     // ---- kg = bf16(k^ * 2^(G_last - G)) and the decay 2^G_last of the state
@@ -305,8 +312,9 @@ __global__ __launch_bounds__(64) void k1_kernel(Params p) {
         }
         lds_put(s_T, r, colbase, kt, pack4(kg[0], kg[1], kg[2], kg[3]));
         if (r == 0)
-            *reinterpret_cast<f32x4*>(rec + REC_DECAY + kt * 64 + q4 * 16) =
-                f32x4{fast_exp2(gl[0]), fast_exp2(gl[1]), fast_exp2(gl[2]), fast_exp2(gl[3])};
+            __builtin_nontemporal_store(
+                f32x4{fast_exp2(gl[0]), fast_exp2(gl[1]), fast_exp2(gl[2]), fast_exp2(gl[3])},
+                reinterpret_cast<f32x4*>(rec + REC_DECAY + kt * 64 + q4 * 16));
     }
     __syncthreads();
     {
@@ -316,8 +324,9 @@ __global__ __launch_bounds__(64) void k1_kernel(Params p) {
         for (int j = 0; j < 4; ++j) {
             const u32x2 a = __builtin_bit_cast(u32x2, kgT[2 * j]);
             const u32x2 bq = __builtin_bit_cast(u32x2, kgT[2 * j + 1]);
-            *reinterpret_cast<u32x4*>(rec + REC_KG + j * 1024 + lane * 16) =
-                u32x4{a.x, a.y, bq.x, bq.y};
+            __builtin_nontemporal_store(
+                u32x4{a.x, a.y, bq.x, bq.y},
+                reinterpret_cast<u32x4*>(rec + REC_KG + j * 1024 + lane * 16));
         }
     }
 
