@@ -68,7 +68,10 @@ __device__ __forceinline__ u32x2 pack4(float a, float b, float c, float d) {
 }
 __device__ __forceinline__ u32x2 pack4(f32x4 v) { return pack4(v.x, v.y, v.z, v.w); }
 
-__global__ __launch_bounds__(64) void k1_kernel(Params p) {
+// Three waves per SIMD (at most 168 VGPRs; the compiler spills two 8-byte
+// values): each wave spends most of its life waiting on its loads, and a
+// third wave per SIMD hides more of that than the two that 172 VGPRs allow.
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k1_kernel(Params p) {
     __shared__ __attribute__((aligned(16))) uint16_t s_T[BT * LROW];  // transpose tile
     __shared__ __attribute__((aligned(16))) float s_L[BT * BT];
     __shared__ float s_X[BT * (BT + 1)];
