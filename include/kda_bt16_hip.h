@@ -23,7 +23,7 @@
  *   dt_bias   [H * 128]       fp32 (optional)
  *   h0, ht    [B, H, 128, 128] fp32, [V, K] if KDA_BT16_STATE_V_FIRST is
  *                             set, else [K, V] (optional)
- *   o         [B, T, H, 128]  bf16
+ *   o         [B, T, H, 128]  bf16 (fp32 with KDA_BT16_O_FP32, recurrence only)
  * Debug outputs (optional, reference layouts, kernels.py:572-579):
  *   dbg_Aqk, dbg_A_inv [B, T, H, 16] bf16; dbg_w, dbg_u [B, T, H, 128] bf16;
  *   dbg_g [B, T, H, 128] fp32.
@@ -47,6 +47,8 @@ extern "C" {
 #define KDA_BT16_USE_QK_L2NORM     (1u << 1) /* USE_QK_L2NORM     kernels.py:108 */
 #define KDA_BT16_USE_BETA_SIGMOID  (1u << 2) /* USE_BETA_SIGMOID  kernels.py:98  */
 #define KDA_BT16_STATE_V_FIRST     (1u << 3) /* STATE_V_FIRST     kernels.py:218 */
+/* kda_recurrent_fwd_hip only (the chunked entries reject it): o is fp32. */
+#define KDA_BT16_O_FP32            (1u << 4)
 
 /* Element types of g and beta. */
 #define KDA_BT16_DTYPE_F32  0
@@ -59,7 +61,9 @@ extern "C" {
                                          Aqk/A_inv 8 B) */
 #define KDA_BT16_EUNSUPPORTED      -2 /* K != 128, V != 128 or HV != H (kernels.py:727-730);
                                          also T * H * B or T beyond the 32-bit grid and
-                                         per-head record sizes (T > 1973776) */
+                                         per-head record sizes (T > 1973776), and
+                                         KDA_BT16_O_FP32 on a chunked entry.  The token
+                                         recurrence needs HV a multiple of H. */
 #define KDA_BT16_EWORKSPACE        -3 /* workspace missing or smaller than kda_bt16_workspace_bytes */
 #define KDA_BT16_ELAUNCH           -4 /* HIP launch error */
 #define KDA_BT16_EABI              -5 /* args->abi_version != KDA_BT16_ABI_VERSION */
@@ -111,6 +115,23 @@ int kda_bt16_k1_hip(const KdaBt16Args* args, void* stream);
  * writes o and ht.  Replaces the kda_bt16_kernel_k2 launch,
  * kernels.py:593-602. */
 int kda_bt16_k2_hip(const KdaBt16Args* args, void* stream);
+
+/* Token-by-token recurrence in fp32 on `stream`: the decode step (T = 1)
+ * and the fused-recurrent forward for any T.  No counterpart in the
+ * reference, whose roadmap lists the decode step (README.md:503-505) and
+ * whose tests use FLA's fused_recurrent_kda as gold
+ * (tests/test_kda_bt16.py:26-38); same arguments as that call.
+ * Differences from the chunked entries:
+ *   - v, g, beta, A_log, dt_bias, h0, ht and o have HV heads and q, k have
+ *     H, with HV a multiple of H (value head hv reads q/k head hv / (HV/H),
+ *     kernels.py:88);
+ *   - without KDA_BT16_USE_GATE, g is the per-token natural-log decay
+ *     (alpha_t = exp(g_t)), not a chunk-local cumsum;
+ *   - o is fp32 with KDA_BT16_O_FP32, else bf16;
+ *   - no workspace and no debug outputs (workspace fields are ignored, the
+ *     debug pointers must be NULL);
+ *   - h0 and ht may be the same buffer (the state updated in place). */
+int kda_recurrent_fwd_hip(const KdaBt16Args* args, void* stream);
 
 /* Static message for an error code. */
 const char* kda_bt16_strerror(int code);

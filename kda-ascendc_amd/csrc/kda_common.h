@@ -77,6 +77,10 @@ struct Params {
     int g_bf16, beta_bf16;
     int use_gate, use_l2norm, use_beta_sigmoid;
     int h0_v_first, ht_v_first;  // layouts of h0 / ht: [V, K] if set, else [K, V]
+    // Token recurrence only: value heads (v, g, beta, A_log, dt_bias, states
+    // and o use HV heads; q and k use H, HV a multiple of H) and o in fp32.
+    int HV;
+    int o_fp32;
 };
 
 // bf16 <-> fp32.  fp32 -> bf16 rounds to nearest even (the hardware
@@ -154,4 +158,5 @@ __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast
 namespace kda {
 hipError_t launch_k1(const Params& p, hipStream_t stream);
 hipError_t launch_k2(const Params& p, hipStream_t stream);
+hipError_t launch_recurrent(const Params& p, hipStream_t stream);
 }  // namespace kda

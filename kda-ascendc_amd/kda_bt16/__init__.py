@@ -5,6 +5,9 @@ Public surface of ``/root/reference/src/kda_bt16/__init__.py:1-16``:
 Triton kernels the reference also exports are replaced by
 ``kda_bt16_stage_launchers`` (stage-1 / stage-2 launch closures over the
 HIP library); ``kda_bt16_kernel_fused`` raises NotImplementedError.
+
+Beyond the reference: ``kda_recurrent_fwd`` (token-by-token recurrence in
+fp32, the decode step and an on-GPU gold) and ``kda_decode_step``.
 """
 
 from .kernels import (
@@ -12,6 +15,8 @@ from .kernels import (
     kda_bt16_fwd,
     kda_bt16_kernel_fused,
     kda_bt16_stage_launchers,
+    kda_decode_step,
+    kda_recurrent_fwd,
 )
 
 __all__ = [
@@ -19,5 +24,7 @@ __all__ = [
     "kda_bt16_debug",
     "kda_bt16_kernel_fused",
     "kda_bt16_stage_launchers",
+    "kda_recurrent_fwd",
+    "kda_decode_step",
 ]
 __version__ = "0.1.0"

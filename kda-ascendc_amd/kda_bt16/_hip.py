@@ -18,6 +18,7 @@ USE_GATE = 1 << 0
 USE_QK_L2NORM = 1 << 1
 USE_BETA_SIGMOID = 1 << 2
 STATE_V_FIRST = 1 << 3
+O_FP32 = 1 << 4  # token recurrence only
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -27,6 +28,7 @@ EXPORTED_SYMBOLS = (
     "kda_bt16_fwd_hip",
     "kda_bt16_k1_hip",
     "kda_bt16_k2_hip",
+    "kda_recurrent_fwd_hip",
     "kda_bt16_strerror",
     "kda_bt16_abi_version",
 )
@@ -96,7 +98,8 @@ def lib() -> ctypes.CDLL:
         h = ctypes.CDLL(str(LIB_PATH))
         h.kda_bt16_workspace_bytes.restype = ctypes.c_size_t
         h.kda_bt16_workspace_bytes.argtypes = [ctypes.c_int32] * 5
-        for name in ("kda_bt16_fwd_hip", "kda_bt16_k1_hip", "kda_bt16_k2_hip"):
+        for name in ("kda_bt16_fwd_hip", "kda_bt16_k1_hip", "kda_bt16_k2_hip",
+                     "kda_recurrent_fwd_hip"):
             fn = getattr(h, name)
             fn.restype = ctypes.c_int
             fn.argtypes = [ctypes.POINTER(KdaBt16Args), ctypes.c_void_p]

@@ -50,10 +50,13 @@ def _validate_kda_inputs(
     A_log: torch.Tensor | None,
     dt_bias: torch.Tensor | None,
     state_v_first: bool,
+    allow_gva: bool = False,
 ) -> tuple[int, int, int, int, int, int]:
     """Input contract of kernels.py:609-749, same order and messages.
 
-    Returns ``(B, T, H, K, HV, V)``; raises ``ValueError`` / ``TypeError``.
+    ``allow_gva`` (token recurrence only) accepts HV a multiple of H instead
+    of HV == H.  Returns ``(B, T, H, K, HV, V)``; raises ``ValueError`` /
+    ``TypeError``.
     """
     if q.ndim != 4:
         raise ValueError(f"q must be 4D [B, T, H, D], got {q.ndim}D with shape {q.shape}")
@@ -146,7 +149,10 @@ def _validate_kda_inputs(
 
     if K != 128 or V != 128:
         raise ValueError(f"prototype targets K=V=128, got K={K}, V={V}")
-    if HV != H:
+    if allow_gva:
+        if HV % H != 0:
+            raise ValueError(f"HV must be a multiple of H (grouped value heads), got HV={HV}, H={H}")
+    elif HV != H:
         raise ValueError(f"prototype targets MHA (HV == H), got HV={HV}, H={H}")
 
     if use_gate_in_kernel:
@@ -443,6 +449,96 @@ def kda_bt16_stage_launchers(
         _hip.call("kda_bt16_k2_hip", args, torch.cuda.current_stream(dev).cuda_stream)
 
     return k1, k2, o, ht
+
+
+def kda_recurrent_fwd(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    g: torch.Tensor,
+    beta: torch.Tensor,
+    scale: float | None = None,
+    initial_state: torch.Tensor | None = None,
+    output_final_state: bool = False,
+    use_qk_l2norm_in_kernel: bool = False,
+    use_gate_in_kernel: bool = False,
+    use_beta_sigmoid_in_kernel: bool = False,
+    lower_bound: float | None = -5.0,
+    A_log: torch.Tensor | None = None,
+    dt_bias: torch.Tensor | None = None,
+    state_v_first: bool = True,
+    output_dtype: torch.dtype = torch.bfloat16,
+    inplace_final_state: bool = False,
+):
+    """Token-by-token KDA recurrence on the GPU, fp32 state: the decode
+    step (T == 1) and the fused-recurrent forward for any T.
+
+    Arguments are those of FLA's ``fused_recurrent_kda`` as the reference's
+    tests call it for their gold (``tests/test_kda_bt16.py:26-38``); the
+    reference itself has no recurrent kernel (its roadmap lists the decode
+    step, ``README.md:503-505``).  Differences from :func:`kda_bt16_fwd`:
+
+    * without ``use_gate_in_kernel``, ``g`` is the per-token log decay
+      (``alpha_t = exp(g_t)``), not a chunk-local cumsum;
+    * v, g, beta, A_log, dt_bias and the states may have ``HV`` heads, a
+      multiple of q/k's ``H`` (grouped value heads, ``kernels.py:88``);
+    * ``output_dtype`` is bf16 or fp32 (fp32 makes this an on-GPU gold);
+    * ``inplace_final_state`` writes the final state into ``initial_state``
+      and returns it as ``ht`` (a decode step that allocates no state).
+
+    Returns ``(o [B, T, HV, V], ht or None)``.
+    """
+    B, T, H, K, HV, V = _validate_kda_inputs(
+        q, k, v, g, beta, initial_state, use_gate_in_kernel, True, lower_bound,
+        A_log, dt_bias, state_v_first, allow_gva=True,
+    )
+    if output_dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"output_dtype must be bfloat16 or float32, got {output_dtype}")
+    if inplace_final_state and initial_state is None:
+        raise ValueError("inplace_final_state requires initial_state")
+    _require_gpu(q)
+    if scale is None:
+        scale = K ** -0.5
+    dev = q.device
+    h0 = initial_state
+    if h0 is not None and h0.data_ptr() % 16 != 0:
+        if inplace_final_state:
+            raise ValueError("inplace_final_state needs a 16-byte aligned initial_state")
+        h0 = h0.clone()
+    o = torch.empty((B, T, HV, V), dtype=output_dtype, device=dev)
+    ht = None
+    if inplace_final_state:
+        ht = initial_state
+    elif output_final_state:
+        ht = torch.empty((B, HV, V, K) if state_v_first else (B, HV, K, V),
+                         dtype=torch.float32, device=dev)
+    flags = _flags(use_gate_in_kernel, use_qk_l2norm_in_kernel, use_beta_sigmoid_in_kernel,
+                   state_v_first)
+    if output_dtype == torch.float32:
+        flags |= _hip.O_FP32
+    args = _make_args(
+        q, k, v, g, beta, scale, lower_bound if use_gate_in_kernel else None,
+        A_log, dt_bias, h0, o, ht, None, 0, flags,
+    )
+    _hip.call("kda_recurrent_fwd_hip", args, torch.cuda.current_stream(dev).cuda_stream)
+    return o, ht
+
+
+def kda_decode_step(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    g: torch.Tensor,
+    beta: torch.Tensor,
+    state: torch.Tensor,
+    **kwargs,
+) -> torch.Tensor:
+    """One decode step (``q``, ``k``, ... with T == 1; any T works): updates
+    ``state`` in place and returns ``o``.  Keyword arguments are those of
+    :func:`kda_recurrent_fwd`."""
+    o, _ = kda_recurrent_fwd(q, k, v, g, beta, initial_state=state,
+                             inplace_final_state=True, **kwargs)
+    return o
 
 
 def kda_bt16_kernel_fused(*_args, **_kwargs):

@@ -236,7 +236,7 @@ def chunked_reference(
 def recurrent_gold(
     q, k, v, g, beta, scale=None, *, A_log=None, dt_bias=None, lower_bound=-5.0,
     initial_state=None, state_v_first=True, use_gate=True, use_l2norm=True,
-    use_beta_sigmoid=True, dtype=torch.float32,
+    use_beta_sigmoid=True, dtype=torch.float32, gate_log=False,
 ):
     """Token-by-token KDA recurrence (the fp32 gold of the reference's tests).
 
@@ -246,39 +246,48 @@ def recurrent_gold(
       S <- S + v_new k^_t^T
       o_t = scale * S q^_t
     Without the in-kernel gate, ``g`` is the chunk-local log2 cumsum and
-    alpha_t = 2^(g_t - g_{t-1}) (g_{-1} = 0 at every chunk start).
+    alpha_t = 2^(g_t - g_{t-1}) (g_{-1} = 0 at every chunk start); with
+    ``gate_log`` it is instead the per-token natural-log decay,
+    alpha_t = exp(g_t) (FLA's fused_recurrent_kda convention).
+    Grouped value heads: v, g, beta, A_log, dt_bias and the states have HV
+    heads and q, k have H; value head hv reads q/k head hv // (HV // H)
+    (kernels.py:88).
     """
     B, T, H, K = q.shape
+    HV = v.shape[2]
     V = v.shape[-1]
     if scale is None:
         scale = K ** -0.5
-    qf = q.to(dtype).movedim(2, 1)  # [B, H, T, K]
-    kf = k.to(dtype).movedim(2, 1)
+    rep = HV // H
+    qf = q.to(dtype).repeat_interleave(rep, dim=2).movedim(2, 1)  # [B, HV, T, K]
+    kf = k.to(dtype).repeat_interleave(rep, dim=2).movedim(2, 1)
     vf = v.to(dtype).movedim(2, 1)
     gf = g.to(dtype).movedim(2, 1)
-    bf = beta.to(dtype).movedim(2, 1)  # [B, H, T]
+    bf = beta.to(dtype).movedim(2, 1)  # [B, HV, T]
     if use_l2norm:
         qf = qf / torch.sqrt((qf * qf).sum(-1, keepdim=True) + EPS)
         kf = kf / torch.sqrt((kf * kf).sum(-1, keepdim=True) + EPS)
     if use_beta_sigmoid:
         bf = torch.sigmoid(bf)
     if use_gate:
-        s = gf if dt_bias is None else gf + dt_bias.to(dtype).view(1, H, 1, K)
-        ea = torch.exp(A_log.to(dtype)).view(1, H, 1, 1)
+        s = gf if dt_bias is None else gf + dt_bias.to(dtype).view(1, HV, 1, K)
+        ea = torch.exp(A_log.to(dtype)).view(1, HV, 1, 1)
         alpha = torch.exp(lower_bound * torch.sigmoid(ea * s))
+    elif gate_log:
+        alpha = torch.exp(gf)
     else:
         prev = torch.zeros_like(gf)
         prev[:, :, 1:] = gf[:, :, :-1]
         prev[:, :, ::BT] = 0
         alpha = torch.exp2(gf - prev)
     if initial_state is None:
-        S = torch.zeros(B, H, V, K, dtype=dtype)
+        S = torch.zeros(B, HV, V, K, dtype=dtype)
     else:
         S = initial_state.to(dtype)
         if not state_v_first:
             S = S.transpose(-1, -2)
         S = S.clone()
-    o = torch.empty(B, H, T, V, dtype=dtype)
+    o = torch.empty(B, HV, T, V, dtype=dtype)
     for t in range(T):
         S = S * alpha[:, :, t, None, :]
         kt = kf[:, :, t]

@@ -17,7 +17,7 @@ HEADER = Path(__file__).resolve().parents[1] / "include" / "kda_bt16_hip.h"
 def _declared_functions() -> list[str]:
     text = HEADER.read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(kda_bt16_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(kda_\w+)\s*\(", text)))
 
 
 def test_header_declares_the_binding_symbols():
@@ -101,3 +101,25 @@ def test_workspace_checked_before_launch():
     a = _args(q=fake, k=fake, v=fake, g=fake, beta=fake, o=fake, workspace=fake + 8,
               workspace_bytes=17408)
     assert _hip.lib().kda_bt16_fwd_hip(ctypes.byref(a), None) == -3
+
+
+def test_recurrent_entry_argument_checks():
+    f = _hip.lib().kda_recurrent_fwd_hip
+    assert f(None, None) == -1
+    assert f(ctypes.byref(_args(abi_version=99)), None) == -5
+    assert f(ctypes.byref(_args(K=64)), None) == -2
+    assert f(ctypes.byref(_args(H=2, HV=3)), None) == -2  # HV not a multiple of H
+    assert f(ctypes.byref(_args(T=0)), None) == -1
+    assert f(ctypes.byref(_args(flags=_hip.USE_GATE, lower_bound=-12.0)), None) == -6
+    assert f(ctypes.byref(_args()), None) == -1  # missing tensors
+    fake = 1 << 40  # never dereferenced: argument checks fail first
+    full = dict(q=fake, k=fake, v=fake, g=fake, beta=fake, o=fake)
+    assert f(ctypes.byref(_args(H=2, HV=4, **full, dbg_Aqk=fake)), None) == -1  # debug outputs
+    assert f(ctypes.byref(_args(**full, ht=fake + 8)), None) == -1  # 16-byte state alignment
+    assert f(ctypes.byref(_args(**{**full, "o": fake + 2}, flags=_hip.O_FP32)), None) == -1
+
+
+def test_o_fp32_is_refused_on_chunked_entries():
+    fake = 1 << 40
+    a = _args(q=fake, k=fake, v=fake, g=fake, beta=fake, o=fake, flags=_hip.O_FP32)
+    assert _hip.lib().kda_bt16_fwd_hip(ctypes.byref(a), None) == -2

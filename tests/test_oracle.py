@@ -3,6 +3,8 @@ the checker of the HIP path.  Everything here runs on the CPU."""
 
 from __future__ import annotations
 
+import math
+
 import pytest
 import torch
 
@@ -169,3 +171,68 @@ def test_resume_invariant():
     o2, h2, _ = chunked_reference(*a2, 0.1, initial_state=h1, **kw)
     assert torch.equal(torch.cat([o1, o2], dim=1), o)
     assert torch.equal(h2, ht)
+
+
+def _gate_alpha_log(inp, lower_bound=-5.0):
+    """ln alpha of the in-kernel gate, written out per element (not through
+    the oracle): lb * sigmoid(exp(A_log) * (g + dt_bias))."""
+    B, T, H, K = inp["g"].shape
+    s = inp["g"].double() + inp["dt_bias"].double().view(1, 1, H, K)
+    ea = torch.exp(inp["A_log"].double()).view(1, 1, H, 1)
+    return lower_bound / (1.0 + torch.exp(-ea * s))
+
+
+def test_recurrent_log_decay_equals_in_kernel_gate():
+    """gate_log (alpha = exp(g)) fed ln alpha of the gate gives the gated
+    recurrence."""
+    inp = make_inputs(2, 21, 2, seed=5, h0_std=0.05)
+    kw = dict(A_log=inp["A_log"], dt_bias=inp["dt_bias"], lower_bound=-5.0,
+              initial_state=inp["h0"], dtype=torch.float64)
+    o_a, ht_a = recurrent_gold(inp["q"], inp["k"], inp["v"], inp["g"].float(),
+                               inp["beta"].float(), 0.1, **kw)
+    o_b, ht_b = recurrent_gold(inp["q"], inp["k"], inp["v"], _gate_alpha_log(inp),
+                               inp["beta"].float(), 0.1, use_gate=False, gate_log=True, **kw)
+    assert maxdiff(o_a, o_b) < 1e-12 and maxdiff(ht_a, ht_b) < 1e-12
+
+
+@pytest.mark.parametrize("T", [5, 16, 37])
+def test_recurrent_log_decay_equals_chunk_cumsum_form(T):
+    """Per-token ln alpha and its chunk-local log2 cumsum (the pre-computed
+    gate the chunked path takes) describe the same recurrence."""
+    inp = make_inputs(1, T, 2, seed=9)
+    g_log = -torch.rand(1, T, 2, 128, dtype=torch.float64) * 0.5
+    G = torch.zeros_like(g_log)
+    for c0 in range(0, T, BT):
+        G[:, c0:c0 + BT] = torch.cumsum(g_log[:, c0:c0 + BT], dim=1) / math.log(2.0)
+    kw = dict(use_gate=False, initial_state=None, dtype=torch.float64)
+    o_a, ht_a = recurrent_gold(inp["q"], inp["k"], inp["v"], g_log, inp["beta"].float(), 0.1,
+                               gate_log=True, **kw)
+    o_b, ht_b = recurrent_gold(inp["q"], inp["k"], inp["v"], G, inp["beta"].float(), 0.1, **kw)
+    assert maxdiff(o_a, o_b) < 1e-10 and maxdiff(ht_a, ht_b) < 1e-10
+
+
+def test_recurrent_grouped_value_heads_map_to_query_head():
+    """HV = 2H: value head hv runs with q/k head hv // 2 -- checked against
+    independent single-head runs (a hv % H mapping fails at H = 2)."""
+    H, HV, T = 2, 4, 13
+    gen = torch.Generator().manual_seed(17)
+    q = torch.randn(1, T, H, 128, generator=gen).bfloat16()
+    k = torch.randn(1, T, H, 128, generator=gen).bfloat16()
+    v = torch.randn(1, T, HV, 128, generator=gen).bfloat16()
+    g = torch.randn(1, T, HV, 128, generator=gen)
+    beta = torch.randn(1, T, HV, generator=gen)
+    A_log = torch.log(torch.rand(HV, generator=gen) * 15 + 1)
+    dt_bias = torch.randn(HV * 128, generator=gen) * 0.1
+    h0 = torch.randn(1, HV, 128, 128, generator=gen) * 0.05
+    o, ht = recurrent_gold(q, k, v, g, beta, 0.1, A_log=A_log, dt_bias=dt_bias,
+                           initial_state=h0, dtype=torch.float64)
+    assert o.shape == (1, T, HV, 128) and ht.shape == (1, HV, 128, 128)
+    for hv in range(HV):
+        h = hv // (HV // H)
+        o1, ht1 = recurrent_gold(
+            q[:, :, h:h + 1], k[:, :, h:h + 1], v[:, :, hv:hv + 1], g[:, :, hv:hv + 1],
+            beta[:, :, hv:hv + 1], 0.1, A_log=A_log[hv:hv + 1],
+            dt_bias=dt_bias[hv * 128:(hv + 1) * 128], initial_state=h0[:, hv:hv + 1],
+            dtype=torch.float64)
+        assert maxdiff(o[:, :, hv:hv + 1], o1) < 1e-12, hv
+        assert maxdiff(ht[:, hv:hv + 1], ht1) < 1e-12, hv

@@ -11,7 +11,13 @@ from __future__ import annotations
 import pytest
 import torch
 
-from kda_bt16 import kda_bt16_debug, kda_bt16_fwd, kda_bt16_kernel_fused
+from kda_bt16 import (
+    kda_bt16_debug,
+    kda_bt16_fwd,
+    kda_bt16_kernel_fused,
+    kda_decode_step,
+    kda_recurrent_fwd,
+)
 
 B, T, H, D = 1, 32, 2, 128
 
@@ -119,3 +125,38 @@ def test_bf16_gate_and_beta_are_accepted_by_validation():
 def test_fused_kernel_symbol_raises():
     with pytest.raises(NotImplementedError):
         kda_bt16_kernel_fused()
+
+
+def _gva_inputs(HV):
+    q, k, _, _, _ = _inputs()
+    v = torch.randn(B, T, HV, D, dtype=torch.bfloat16)
+    g = torch.randn(B, T, HV, D)
+    beta = torch.randn(B, T, HV)
+    return q, k, v, g, beta
+
+
+def test_recurrent_accepts_grouped_value_heads():
+    """kda_recurrent_fwd takes HV a multiple of H; valid CPU inputs are then
+    refused only for want of a GPU."""
+    q, k, v, g, beta = _gva_inputs(2 * H)
+    with pytest.raises(ValueError, match="ROCm GPU"):
+        kda_recurrent_fwd(q, k, v, g, beta, use_gate_in_kernel=True, A_log=torch.zeros(2 * H))
+    with pytest.raises(ValueError, match="A_log.shape"):
+        kda_recurrent_fwd(q, k, v, g, beta, use_gate_in_kernel=True, A_log=torch.zeros(H))
+    q3, k3, v3, g3, b3 = _gva_inputs(3)
+    with pytest.raises(ValueError, match="HV must be a multiple of H"):
+        kda_recurrent_fwd(q3, k3, v3, g3, b3)
+
+
+def test_recurrent_host_errors():
+    q, k, v, g, beta = _inputs()
+    with pytest.raises(TypeError, match="output_dtype"):
+        kda_recurrent_fwd(q, k, v, g, beta, output_dtype=torch.float16)
+    with pytest.raises(ValueError, match="inplace_final_state requires initial_state"):
+        kda_recurrent_fwd(q, k, v, g, beta, inplace_final_state=True)
+    with pytest.raises(ValueError, match="initial_state.shape"):
+        kda_decode_step(q[:, :1], k[:, :1], v[:, :1], g[:, :1], beta[:, :1],
+                        torch.zeros(B, H, D, 64))
+    with pytest.raises(ValueError, match="ROCm GPU"):
+        kda_decode_step(q[:, :1], k[:, :1], v[:, :1], g[:, :1], beta[:, :1],
+                        torch.zeros(B, H, D, D))
