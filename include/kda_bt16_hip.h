@@ -14,19 +14,34 @@
  * KDA_BT16_E* code; nothing is allocated inside the library.
  *
  * Tensor layouts (all row-major, contiguous, on one device):
- *   q, k      [B, T, H, 128]  bf16
- *   v         [B, T, H, 128]  bf16            (HV == H)
- *   g         [B, T, H, 128]  fp32 or bf16    raw gate, or the precomputed
- *                                             chunk-local log2 cumsum
- *   beta      [B, T, H]       fp32 or bf16
- *   A_log     [H]             fp32
- *   dt_bias   [H * 128]       fp32 (optional)
- *   h0, ht    [B, H, 128, 128] fp32, [V, K] if KDA_BT16_STATE_V_FIRST is
- *                             set, else [K, V] (optional)
- *   o         [B, T, H, 128]  bf16 (fp32 with KDA_BT16_O_FP32, recurrence only)
+ *   q, k      [B, T, H, 128]   bf16
+ *   v         [B, T, HV, 128]  bf16   HV a multiple of H: value head hv
+ *                                     reads q/k head hv / (HV / H)
+ *                                     (kernels.py:88; the reference's
+ *                                     validation requires HV == H)
+ *   g         [B, T, HV, 128]  fp32 or bf16: the raw gate (USE_GATE), the
+ *                                     per-token natural-log decay
+ *                                     (G_LOG_DECAY), or else the precomputed
+ *                                     chunk-local log2 cumsum
+ *   beta      [B, T, HV]       fp32 or bf16
+ *   A_log     [HV]             fp32
+ *   dt_bias   [HV * 128]       fp32 (optional)
+ *   h0, ht    [S, HV, 128, 128] fp32, [V, K] if KDA_BT16_STATE_V_FIRST is
+ *                              set, else [K, V] (optional); S = B, or N
+ *                              with cu_seqlens
+ *   o         [B, T, HV, 128]  bf16 (fp32 with KDA_BT16_O_FP32, recurrence only)
+ *   cu_seqlens [N + 1]         int32 or int64 (optional): N sequences packed
+ *                              along T with B == 1, sequence n holding
+ *                              tokens [cu_seqlens[n], cu_seqlens[n+1]),
+ *                              cu_seqlens[0] == 0, cu_seqlens[N] == T,
+ *                              non-decreasing (FLA's varlen convention; the
+ *                              reference lists varlen as a limitation,
+ *                              README.md:420-421).  Values outside that
+ *                              contract give unspecified results but never
+ *                              an access outside the tensors.
  * Debug outputs (optional, reference layouts, kernels.py:572-579):
- *   dbg_Aqk, dbg_A_inv [B, T, H, 16] bf16; dbg_w, dbg_u [B, T, H, 128] bf16;
- *   dbg_g [B, T, H, 128] fp32.
+ *   dbg_Aqk, dbg_A_inv [B, T, HV, 16] bf16; dbg_w, dbg_u [B, T, HV, 128] bf16;
+ *   dbg_g [B, T, HV, 128] fp32.
  */
 #ifndef KDA_BT16_HIP_H
 #define KDA_BT16_HIP_H
@@ -38,7 +53,7 @@
 extern "C" {
 #endif
 
-#define KDA_BT16_ABI_VERSION 1
+#define KDA_BT16_ABI_VERSION 2
 
 /* Flags: the reference's tl.constexpr switches (kernels.py:78-82, 208-212).
  * USE_INITIAL_STATE / STORE_FINAL_STATE / HAS_BIAS / STORE_A_INV follow from
@@ -49,21 +64,28 @@ extern "C" {
 #define KDA_BT16_STATE_V_FIRST     (1u << 3) /* STATE_V_FIRST     kernels.py:218 */
 /* kda_recurrent_fwd_hip only (the chunked entries reject it): o is fp32. */
 #define KDA_BT16_O_FP32            (1u << 4)
+/* Without USE_GATE: g is the per-token natural-log decay (alpha_t = exp(g_t),
+ * FLA's chunk_kda / fused_recurrent_kda convention) and stage 1 forms its
+ * chunk-local log2 cumsum, as kda_gate_chunk_cumsum does for the gate
+ * (tests/test_kda_bt16.py:16).  No effect with USE_GATE. */
+#define KDA_BT16_G_LOG_DECAY       (1u << 5)
 
-/* Element types of g and beta. */
+/* Element types of g and beta, and of cu_seqlens. */
 #define KDA_BT16_DTYPE_F32  0
 #define KDA_BT16_DTYPE_BF16 1
+#define KDA_BT16_DTYPE_I32  2
+#define KDA_BT16_DTYPE_I64  3
 
 /* Error codes. */
 #define KDA_BT16_OK                 0
 #define KDA_BT16_EINVAL            -1 /* null pointer, non-positive size, bad dtype tag,
                                          misaligned tensor (16 B; beta its element size;
-                                         Aqk/A_inv 8 B) */
-#define KDA_BT16_EUNSUPPORTED      -2 /* K != 128, V != 128 or HV != H (kernels.py:727-730);
-                                         also T * H * B or T beyond the 32-bit grid and
-                                         per-head record sizes (T > 1973776), and
-                                         KDA_BT16_O_FP32 on a chunked entry.  The token
-                                         recurrence needs HV a multiple of H. */
+                                         Aqk/A_inv 8 B; cu_seqlens its element size),
+                                         cu_seqlens with B != 1 or N <= 0 */
+#define KDA_BT16_EUNSUPPORTED      -2 /* K != 128, V != 128 (kernels.py:727-728) or HV not
+                                         a multiple of H; work beyond the 32-bit grids or
+                                         per-sequence record sizes (T > 1973776), and
+                                         KDA_BT16_O_FP32 on a chunked entry. */
 #define KDA_BT16_EWORKSPACE        -3 /* workspace missing or smaller than kda_bt16_workspace_bytes */
 #define KDA_BT16_ELAUNCH           -4 /* HIP launch error */
 #define KDA_BT16_EABI              -5 /* args->abi_version != KDA_BT16_ABI_VERSION */
@@ -94,13 +116,21 @@ typedef struct KdaBt16Args {
     void* dbg_w;
     void* dbg_u;
     float* dbg_g;
+    const void* cu_seqlens;   /* optional: packed sequences (varlen) */
+    int32_t cu_seqlens_dtype; /* KDA_BT16_DTYPE_I32 or KDA_BT16_DTYPE_I64 */
+    int32_t N;                /* number of sequences with cu_seqlens */
 } KdaBt16Args;
 
-/* Bytes of scratch the two stages exchange for this geometry (one 17 KiB
- * record per (batch, head, 16-token chunk)).  Replaces the reference's
- * intermediate allocations Aqk / Akk_scratch / w / u / g_cumsum,
+/* Bytes of scratch the two stages exchange for a fixed-length geometry (one
+ * 17 KiB record per (batch, value head, 16-token chunk)).  Replaces the
+ * reference's intermediate allocations Aqk / Akk_scratch / w / u / g_cumsum,
  * kernels.py:572-579.  Returns 0 for an unsupported geometry. */
-size_t kda_bt16_workspace_bytes(int32_t B, int32_t T, int32_t H, int32_t K, int32_t V);
+size_t kda_bt16_workspace_bytes(int32_t B, int32_t T, int32_t HV, int32_t K, int32_t V);
+
+/* The same for any arguments, varlen included (HV * (floor(T/16) + N)
+ * records with cu_seqlens).  Reads only the size fields and cu_seqlens'
+ * presence, never the device memory. */
+size_t kda_bt16_workspace_bytes_args(const KdaBt16Args* args);
 
 /* Full forward: stage 1 then stage 2 on `stream` (a hipStream_t; NULL is the
  * legacy default stream).  Replaces _run's two launches, kernels.py:581-602. */
@@ -121,12 +151,8 @@ int kda_bt16_k2_hip(const KdaBt16Args* args, void* stream);
  * reference, whose roadmap lists the decode step (README.md:503-505) and
  * whose tests use FLA's fused_recurrent_kda as gold
  * (tests/test_kda_bt16.py:26-38); same arguments as that call.
- * Differences from the chunked entries:
- *   - v, g, beta, A_log, dt_bias, h0, ht and o have HV heads and q, k have
- *     H, with HV a multiple of H (value head hv reads q/k head hv / (HV/H),
- *     kernels.py:88);
- *   - without KDA_BT16_USE_GATE, g is the per-token natural-log decay
- *     (alpha_t = exp(g_t)), not a chunk-local cumsum;
+ * Same layouts, flags and g conventions as the chunked entries, varlen and
+ * grouped value heads included.  Differences:
  *   - o is fp32 with KDA_BT16_O_FP32, else bf16;
  *   - no workspace and no debug outputs (workspace fields are ignored, the
  *     debug pointers must be NULL);

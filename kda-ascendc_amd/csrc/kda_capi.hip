@@ -1,8 +1,8 @@
 // C ABI of libkda_bt16_hip.so: argument checks, the two stage launches and
 // the token recurrence.
 // The checks here guard the kernels' indexing assumptions (shapes, pointer
-// presence, workspace size); the user-facing validation with the
-// reference's messages lives in the Python layer.
+// presence, workspace size, 32-bit grids); the user-facing validation with
+// the reference's messages lives in the Python layer.
 #include "../../include/kda_bt16_hip.h"
 #include "kda_common.h"
 
@@ -10,105 +10,44 @@ namespace {
 
 using kda::Params;
 
+constexpr int64_t I32_MAX = 0x7fffffffLL;
+
 bool misaligned(const void* p, uintptr_t align) {
     return (reinterpret_cast<uintptr_t>(p) & (align - 1)) != 0;
 }
 
-int to_params(const KdaBt16Args* a, Params& p, bool need_inputs, bool need_outputs) {
-    if (a == nullptr) return KDA_BT16_EINVAL;
-    if (a->abi_version != KDA_BT16_ABI_VERSION) return KDA_BT16_EABI;
-    if (a->B <= 0 || a->T <= 0 || a->H <= 0 || a->HV <= 0 || a->K <= 0 || a->V <= 0)
-        return KDA_BT16_EINVAL;
-    if (a->K != kda::DK || a->V != kda::DK || a->HV != a->H) return KDA_BT16_EUNSUPPORTED;
-    if (a->flags & KDA_BT16_O_FP32) return KDA_BT16_EUNSUPPORTED;
-    // Grid sizes are 32-bit (B*H*NT work-groups for stage 1, B*H*8 for stage
-    // 2), and stage 2 addresses one head's records through a buffer
-    // descriptor with a 32-bit size (NT * REC_BYTES bytes).
-    const int64_t nt = ((int64_t)a->T + kda::BT - 1) / kda::BT;
-    if ((int64_t)a->B * a->H * nt > 0x7fffffffLL || nt * kda::REC_BYTES > 0x7fffffffLL)
-        return KDA_BT16_EUNSUPPORTED;
-    if ((a->g_dtype != KDA_BT16_DTYPE_F32 && a->g_dtype != KDA_BT16_DTYPE_BF16) ||
-        (a->beta_dtype != KDA_BT16_DTYPE_F32 && a->beta_dtype != KDA_BT16_DTYPE_BF16))
-        return KDA_BT16_EINVAL;
-    const bool use_gate = (a->flags & KDA_BT16_USE_GATE) != 0;
-    if (use_gate && !(a->lower_bound > -11.0f && a->lower_bound < 0.0f)) return KDA_BT16_ERANGE;
-    if (need_inputs) {
-        if (!a->q || !a->k || !a->v || !a->g || !a->beta) return KDA_BT16_EINVAL;
-        if (use_gate && !a->A_log) return KDA_BT16_EINVAL;
-        const bool any_dbg = a->dbg_Aqk || a->dbg_A_inv || a->dbg_w || a->dbg_u || a->dbg_g;
-        const bool all_dbg = a->dbg_Aqk && a->dbg_A_inv && a->dbg_w && a->dbg_u && a->dbg_g;
-        if (any_dbg && !all_dbg) return KDA_BT16_EINVAL;
-    }
-    if (need_outputs && !a->o) return KDA_BT16_EINVAL;
-    // The kernels use 8- and 16-byte vector accesses.
-    if (misaligned(a->q, 16) || misaligned(a->k, 16) || misaligned(a->v, 16) ||
-        misaligned(a->g, 16) || misaligned(a->beta, a->beta_dtype == KDA_BT16_DTYPE_BF16 ? 2 : 4) ||
-        misaligned(a->dt_bias, 16) ||
-        misaligned(a->h0, 16) || misaligned(a->ht, 16) || misaligned(a->o, 16) ||
-        misaligned(a->dbg_Aqk, 8) || misaligned(a->dbg_A_inv, 8) || misaligned(a->dbg_w, 16) ||
-        misaligned(a->dbg_u, 16) || misaligned(a->dbg_g, 16))
-        return KDA_BT16_EINVAL;
-    const size_t need = kda_bt16_workspace_bytes(a->B, a->T, a->H, a->K, a->V);
-    if (!a->workspace || a->workspace_bytes < need) return KDA_BT16_EWORKSPACE;
-    if ((reinterpret_cast<uintptr_t>(a->workspace) & 255u) != 0) return KDA_BT16_EWORKSPACE;
+bool gate_dtype_ok(int32_t t) { return t == KDA_BT16_DTYPE_F32 || t == KDA_BT16_DTYPE_BF16; }
 
-    p.q = static_cast<const uint16_t*>(a->q);
-    p.k = static_cast<const uint16_t*>(a->k);
-    p.v = static_cast<const uint16_t*>(a->v);
-    p.g = a->g;
-    p.beta = a->beta;
-    p.A_log = a->A_log;
-    p.dt_bias = a->dt_bias;
-    p.h0 = a->h0;
-    p.o = static_cast<uint16_t*>(a->o);
-    p.ht = a->ht;
-    p.ws = static_cast<uint8_t*>(a->workspace);
-    p.dbg_Aqk = static_cast<uint16_t*>(a->dbg_Aqk);
-    p.dbg_A_inv = static_cast<uint16_t*>(a->dbg_A_inv);
-    p.dbg_w = static_cast<uint16_t*>(a->dbg_w);
-    p.dbg_u = static_cast<uint16_t*>(a->dbg_u);
-    p.dbg_g = a->dbg_g;
-    p.B = a->B;
-    p.T = a->T;
-    p.H = a->H;
-    p.NT = (a->T + kda::BT - 1) / kda::BT;
-    p.scale = a->scale;
-    p.lower_bound = a->lower_bound;
-    p.g_bf16 = a->g_dtype == KDA_BT16_DTYPE_BF16;
-    p.beta_bf16 = a->beta_dtype == KDA_BT16_DTYPE_BF16;
-    p.use_gate = use_gate;
-    p.use_l2norm = (a->flags & KDA_BT16_USE_QK_L2NORM) != 0;
-    p.use_beta_sigmoid = (a->flags & KDA_BT16_USE_BETA_SIGMOID) != 0;
-    p.h0_v_first = p.ht_v_first = (a->flags & KDA_BT16_STATE_V_FIRST) != 0;
-    p.HV = a->H;
-    p.o_fp32 = 0;
-    return KDA_BT16_OK;
-}
+int64_t chunks_of(int64_t T) { return (T + kda::BT - 1) / kda::BT; }
 
-// The token recurrence: HV a multiple of H, no workspace, no debug outputs,
-// o in bf16 or fp32.
-int to_params_recurrent(const KdaBt16Args* a, Params& p) {
+// Sequences of the batch: B rows, or N packed sequences with cu_seqlens.
+int64_t sequences(const KdaBt16Args* a) { return a->cu_seqlens ? a->N : a->B; }
+
+// Record slots per value head with cu_seqlens: sequence n's chunks sit at
+// floor(cu_seqlens[n] / 16) + n + c, all below floor(T / 16) + N.
+int64_t varlen_slots(const KdaBt16Args* a) { return (int64_t)a->T / kda::BT + a->N; }
+
+// Checks shared by every entry point and the common part of Params.
+int check_common(const KdaBt16Args* a, Params& p) {
     if (a == nullptr) return KDA_BT16_EINVAL;
     if (a->abi_version != KDA_BT16_ABI_VERSION) return KDA_BT16_EABI;
     if (a->B <= 0 || a->T <= 0 || a->H <= 0 || a->HV <= 0 || a->K <= 0 || a->V <= 0)
         return KDA_BT16_EINVAL;
     if (a->K != kda::DK || a->V != kda::DK || a->HV % a->H != 0) return KDA_BT16_EUNSUPPORTED;
-    if ((int64_t)a->B * a->HV > 0x7fffffffLL) return KDA_BT16_EUNSUPPORTED;
-    if ((a->g_dtype != KDA_BT16_DTYPE_F32 && a->g_dtype != KDA_BT16_DTYPE_BF16) ||
-        (a->beta_dtype != KDA_BT16_DTYPE_F32 && a->beta_dtype != KDA_BT16_DTYPE_BF16))
-        return KDA_BT16_EINVAL;
+    if (!gate_dtype_ok(a->g_dtype) || !gate_dtype_ok(a->beta_dtype)) return KDA_BT16_EINVAL;
+    if (a->cu_seqlens) {
+        // Packed sequences: one batch row; 32- or 64-bit offsets.
+        if (a->B != 1 || a->N <= 0) return KDA_BT16_EINVAL;
+        if (a->cu_seqlens_dtype == KDA_BT16_DTYPE_I32) {
+            if (misaligned(a->cu_seqlens, 4)) return KDA_BT16_EINVAL;
+        } else if (a->cu_seqlens_dtype == KDA_BT16_DTYPE_I64) {
+            if (misaligned(a->cu_seqlens, 8)) return KDA_BT16_EINVAL;
+        } else {
+            return KDA_BT16_EINVAL;
+        }
+    }
     const bool use_gate = (a->flags & KDA_BT16_USE_GATE) != 0;
     if (use_gate && !(a->lower_bound > -11.0f && a->lower_bound < 0.0f)) return KDA_BT16_ERANGE;
-    if (!a->q || !a->k || !a->v || !a->g || !a->beta || !a->o) return KDA_BT16_EINVAL;
-    if (use_gate && !a->A_log) return KDA_BT16_EINVAL;
-    if (a->dbg_Aqk || a->dbg_A_inv || a->dbg_w || a->dbg_u || a->dbg_g) return KDA_BT16_EINVAL;
-    // 16-byte state rows; 2-byte q/k/v elements read in pairs.
-    if (misaligned(a->q, 4) || misaligned(a->k, 4) || misaligned(a->v, 2) ||
-        misaligned(a->g, a->g_dtype == KDA_BT16_DTYPE_BF16 ? 2 : 4) ||
-        misaligned(a->beta, a->beta_dtype == KDA_BT16_DTYPE_BF16 ? 2 : 4) ||
-        misaligned(a->dt_bias, 4) || misaligned(a->h0, 16) || misaligned(a->ht, 16) ||
-        misaligned(a->o, (a->flags & KDA_BT16_O_FP32) ? 4 : 2))
-        return KDA_BT16_EINVAL;
 
     p = Params{};
     p.q = static_cast<const uint16_t*>(a->q);
@@ -125,6 +64,7 @@ int to_params_recurrent(const KdaBt16Args* a, Params& p) {
     p.T = a->T;
     p.H = a->H;
     p.HV = a->HV;
+    p.NT = (int)chunks_of(a->T);
     p.scale = a->scale;
     p.lower_bound = a->lower_bound;
     p.g_bf16 = a->g_dtype == KDA_BT16_DTYPE_BF16;
@@ -132,7 +72,71 @@ int to_params_recurrent(const KdaBt16Args* a, Params& p) {
     p.use_gate = use_gate;
     p.use_l2norm = (a->flags & KDA_BT16_USE_QK_L2NORM) != 0;
     p.use_beta_sigmoid = (a->flags & KDA_BT16_USE_BETA_SIGMOID) != 0;
+    p.g_log = (a->flags & KDA_BT16_G_LOG_DECAY) != 0;
     p.h0_v_first = p.ht_v_first = (a->flags & KDA_BT16_STATE_V_FIRST) != 0;
+    p.cu_seqlens = a->cu_seqlens;
+    p.cu_i64 = a->cu_seqlens_dtype == KDA_BT16_DTYPE_I64;
+    p.N = a->cu_seqlens ? a->N : 0;
+    return KDA_BT16_OK;
+}
+
+// The chunked entries (stage 1, stage 2, both).
+int to_params(const KdaBt16Args* a, Params& p, bool need_inputs, bool need_outputs) {
+    int rc = check_common(a, p);
+    if (rc != KDA_BT16_OK) return rc;
+    if (a->flags & KDA_BT16_O_FP32) return KDA_BT16_EUNSUPPORTED;
+    // Grid sizes are 32-bit: stage 1 has one work-group per record slot,
+    // stage 2 eight per (sequence, value head).  Stage 2 addresses one
+    // sequence-head's records through a buffer descriptor with a 32-bit size
+    // (at most ceil(T / 16) * REC_BYTES bytes).
+    const int64_t slots = a->cu_seqlens ? varlen_slots(a) : (int64_t)a->B * chunks_of(a->T);
+    if ((int64_t)a->HV * slots > I32_MAX || sequences(a) * a->HV * 8 > I32_MAX ||
+        chunks_of(a->T) * kda::REC_BYTES > I32_MAX)
+        return KDA_BT16_EUNSUPPORTED;
+    p.NS = a->cu_seqlens ? (int)varlen_slots(a) : 0;
+    if (need_inputs) {
+        if (!a->q || !a->k || !a->v || !a->g || !a->beta) return KDA_BT16_EINVAL;
+        if (p.use_gate && !a->A_log) return KDA_BT16_EINVAL;
+        const bool any_dbg = a->dbg_Aqk || a->dbg_A_inv || a->dbg_w || a->dbg_u || a->dbg_g;
+        const bool all_dbg = a->dbg_Aqk && a->dbg_A_inv && a->dbg_w && a->dbg_u && a->dbg_g;
+        if (any_dbg && !all_dbg) return KDA_BT16_EINVAL;
+    }
+    if (need_outputs && !a->o) return KDA_BT16_EINVAL;
+    // The kernels use 8- and 16-byte vector accesses.
+    if (misaligned(a->q, 16) || misaligned(a->k, 16) || misaligned(a->v, 16) ||
+        misaligned(a->g, 16) || misaligned(a->beta, a->beta_dtype == KDA_BT16_DTYPE_BF16 ? 2 : 4) ||
+        misaligned(a->dt_bias, 16) ||
+        misaligned(a->h0, 16) || misaligned(a->ht, 16) || misaligned(a->o, 16) ||
+        misaligned(a->dbg_Aqk, 8) || misaligned(a->dbg_A_inv, 8) || misaligned(a->dbg_w, 16) ||
+        misaligned(a->dbg_u, 16) || misaligned(a->dbg_g, 16))
+        return KDA_BT16_EINVAL;
+    const size_t need = kda_bt16_workspace_bytes_args(a);
+    if (!a->workspace || a->workspace_bytes < need) return KDA_BT16_EWORKSPACE;
+    if ((reinterpret_cast<uintptr_t>(a->workspace) & 255u) != 0) return KDA_BT16_EWORKSPACE;
+    p.ws = static_cast<uint8_t*>(a->workspace);
+    p.dbg_Aqk = static_cast<uint16_t*>(a->dbg_Aqk);
+    p.dbg_A_inv = static_cast<uint16_t*>(a->dbg_A_inv);
+    p.dbg_w = static_cast<uint16_t*>(a->dbg_w);
+    p.dbg_u = static_cast<uint16_t*>(a->dbg_u);
+    p.dbg_g = a->dbg_g;
+    return KDA_BT16_OK;
+}
+
+// The token recurrence: no workspace, no debug outputs, o in bf16 or fp32.
+int to_params_recurrent(const KdaBt16Args* a, Params& p) {
+    int rc = check_common(a, p);
+    if (rc != KDA_BT16_OK) return rc;
+    if (sequences(a) * a->HV > I32_MAX) return KDA_BT16_EUNSUPPORTED;
+    if (!a->q || !a->k || !a->v || !a->g || !a->beta || !a->o) return KDA_BT16_EINVAL;
+    if (p.use_gate && !a->A_log) return KDA_BT16_EINVAL;
+    if (a->dbg_Aqk || a->dbg_A_inv || a->dbg_w || a->dbg_u || a->dbg_g) return KDA_BT16_EINVAL;
+    // 16-byte state rows; 2-byte q/k/v elements read in pairs.
+    if (misaligned(a->q, 4) || misaligned(a->k, 4) || misaligned(a->v, 2) ||
+        misaligned(a->g, a->g_dtype == KDA_BT16_DTYPE_BF16 ? 2 : 4) ||
+        misaligned(a->beta, a->beta_dtype == KDA_BT16_DTYPE_BF16 ? 2 : 4) ||
+        misaligned(a->dt_bias, 4) || misaligned(a->h0, 16) || misaligned(a->ht, 16) ||
+        misaligned(a->o, (a->flags & KDA_BT16_O_FP32) ? 4 : 2))
+        return KDA_BT16_EINVAL;
     p.o_fp32 = (a->flags & KDA_BT16_O_FP32) != 0;
     return KDA_BT16_OK;
 }
@@ -141,10 +145,16 @@ int to_params_recurrent(const KdaBt16Args* a, Params& p) {
 
 extern "C" {
 
-size_t kda_bt16_workspace_bytes(int32_t B, int32_t T, int32_t H, int32_t K, int32_t V) {
-    if (B <= 0 || T <= 0 || H <= 0 || K != kda::DK || V != kda::DK) return 0;
-    const size_t nt = (size_t)(T + kda::BT - 1) / kda::BT;
-    return (size_t)B * (size_t)H * nt * (size_t)kda::REC_BYTES;
+size_t kda_bt16_workspace_bytes(int32_t B, int32_t T, int32_t HV, int32_t K, int32_t V) {
+    if (B <= 0 || T <= 0 || HV <= 0 || K != kda::DK || V != kda::DK) return 0;
+    return (size_t)B * (size_t)HV * (size_t)chunks_of(T) * (size_t)kda::REC_BYTES;
+}
+
+size_t kda_bt16_workspace_bytes_args(const KdaBt16Args* a) {
+    if (a == nullptr || a->T <= 0 || a->HV <= 0 || a->K != kda::DK || a->V != kda::DK) return 0;
+    if (!a->cu_seqlens) return kda_bt16_workspace_bytes(a->B, a->T, a->HV, a->K, a->V);
+    if (a->N <= 0) return 0;
+    return (size_t)a->HV * (size_t)varlen_slots(a) * (size_t)kda::REC_BYTES;
 }
 
 int kda_bt16_k1_hip(const KdaBt16Args* args, void* stream) {
@@ -185,11 +195,13 @@ int kda_recurrent_fwd_hip(const KdaBt16Args* args, void* stream) {
 const char* kda_bt16_strerror(int code) {
     switch (code) {
         case KDA_BT16_OK: return "ok";
-        case KDA_BT16_EINVAL: return "invalid argument (null pointer, non-positive size or bad dtype tag)";
+        case KDA_BT16_EINVAL:
+            return "invalid argument (null pointer, non-positive size, bad dtype tag, "
+                   "misaligned tensor, or cu_seqlens with B != 1 or N <= 0)";
         case KDA_BT16_EUNSUPPORTED:
-            return "unsupported geometry (needs K=V=128, HV == H (HV a multiple of H for the "
-                   "recurrence) and T <= 1973776) or flag";
-        case KDA_BT16_EWORKSPACE: return "workspace missing, misaligned or smaller than kda_bt16_workspace_bytes()";
+            return "unsupported geometry (needs K=V=128, HV a multiple of H, T <= 1973776 and "
+                   "32-bit grids) or flag";
+        case KDA_BT16_EWORKSPACE: return "workspace missing, misaligned or smaller than kda_bt16_workspace_bytes_args()";
         case KDA_BT16_ELAUNCH: return "HIP kernel launch failed";
         case KDA_BT16_EABI: return "abi_version mismatch";
         case KDA_BT16_ERANGE: return "lower_bound must be in (-11, 0) with the in-kernel gate";

@@ -1,9 +1,13 @@
 // Shared device helpers and the chunk-record layout exchanged by the two
 // stages of the KDA BT=16 forward on gfx950.
 //
-// Record layout.  Stage 1 writes one record per (batch*head, chunk) and
-// stage 2 reads them head by head, chunk after chunk.  Records of one head
-// are contiguous: record index = (b*H + h) * NT + chunk.  Every operand is
+// Record layout.  Stage 1 writes one record per (sequence, value head,
+// chunk) and stage 2 reads them sequence-head by sequence-head, chunk after
+// chunk.  The records of one (sequence, value head) are contiguous:
+//   fixed length: record index = (b*HV + hv) * NT + chunk;
+//   varlen:       record index = hv * NS + floor(bos_n / 16) + n + chunk,
+//                 NS = floor(T / 16) + N (slot map of SeqMap below).
+// Every operand is
 // stored in the register order in which stage 2 feeds it to the matrix
 // cores, so each lane reads its slice with 16-byte loads and no shuffles.
 //
@@ -72,16 +76,60 @@ struct Params {
     uint16_t* dbg_w;
     uint16_t* dbg_u;
     float* dbg_g;
-    int B, T, H, NT;
+    // Value heads: v, g, beta, A_log, dt_bias, the states and o use HV heads,
+    // q and k use H, HV a multiple of H (value head hv reads q/k head
+    // hv / (HV / H), kernels.py:88).
+    int B, T, H, HV, NT;
     float scale, lower_bound;
     int g_bf16, beta_bf16;
     int use_gate, use_l2norm, use_beta_sigmoid;
+    int g_log;  // without use_gate: g is the per-token natural-log decay
     int h0_v_first, ht_v_first;  // layouts of h0 / ht: [V, K] if set, else [K, V]
-    // Token recurrence only: value heads (v, g, beta, A_log, dt_bias, states
-    // and o use HV heads; q and k use H, HV a multiple of H) and o in fp32.
-    int HV;
-    int o_fp32;
+    int o_fp32;                  // token recurrence only: o in fp32
+    // Varlen: N sequences packed along T (B == 1), sequence n holding tokens
+    // [cu_seqlens[n], cu_seqlens[n+1]); states are [N, HV, ...].  NS is the
+    // number of record slots per value head.  Null cu_seqlens: fixed length.
+    const void* cu_seqlens;
+    int cu_i64;
+    int N, NS;
 };
+
+// Bounds of sequence n of a varlen batch, clamped into [0, T] so that a
+// malformed cu_seqlens never leads outside the tensors.
+__device__ __forceinline__ int cu_at(const Params& p, int i) {
+    const int64_t x = p.cu_i64 ? static_cast<const int64_t*>(p.cu_seqlens)[i]
+                               : (int64_t) static_cast<const int32_t*>(p.cu_seqlens)[i];
+    return (int)(x < 0 ? 0 : (x > p.T ? p.T : x));
+}
+
+// One (sequence or batch row, value head) of the work: its first token in
+// the flattened [B*T] token dimension, its length, its chunk count and the
+// index of its first record.
+struct SeqSpan {
+    int64_t tok0;
+    int len, nt;
+    int64_t rec0;
+};
+
+// bh = (batch row or sequence) * HV + hv.
+__device__ __forceinline__ SeqSpan seq_span(const Params& p, int bh) {
+    SeqSpan s;
+    if (p.cu_seqlens) {
+        const int n = bh / p.HV, hv = bh - n * p.HV;
+        const int bos = cu_at(p, n);
+        const int eos = max(bos, cu_at(p, n + 1));
+        s.tok0 = bos;
+        s.len = eos - bos;
+        s.nt = (s.len + BT - 1) / BT;
+        s.rec0 = (int64_t)hv * p.NS + bos / BT + n;
+    } else {
+        s.tok0 = (int64_t)(bh / p.HV) * p.T;
+        s.len = p.T;
+        s.nt = p.NT;
+        s.rec0 = (int64_t)bh * p.NT;
+    }
+    return s;
+}
 
 // bf16 <-> fp32.  fp32 -> bf16 rounds to nearest even (the hardware
 // conversion on gfx950), matching torch's .to(torch.bfloat16).

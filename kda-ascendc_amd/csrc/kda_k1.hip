@@ -71,6 +71,26 @@ __device__ __forceinline__ u32x2 pack4(f32x4 v) { return pack4(v.x, v.y, v.z, v.
 // Three waves per SIMD (at most 168 VGPRs; the compiler spills two 8-byte
 // values): each wave spends most of its life waiting on its loads, and a
 // third wave per SIMD hides more of that than the two that 172 VGPRs allow.
+// Varlen: the sequence n whose record slots hold slot x, i.e. the largest n
+// with floor(cu_seqlens[n] / 16) + n <= x (strictly increasing in n for a
+// non-decreasing cu_seqlens).  A 64-way search: each round every lane tests
+// one candidate and the ballot's population count is the number of
+// candidates at or below x.  Any cu_seqlens gives an n in [0, N).
+__device__ __forceinline__ int find_sequence(const Params& p, int x, int lane) {
+    int lo = 0, cnt = p.N;
+    while (cnt > 1) {
+        const int step = (cnt + 63) >> 6;
+        const int idx = lo + lane * step;
+        const bool below = idx < lo + cnt && cu_at(p, idx) / BT + idx <= x;
+        const int m = __popcll(__ballot(below));
+        if (m == 0) break;
+        const int next = lo + (m - 1) * step;
+        cnt = min(step, lo + cnt - next);
+        lo = next;
+    }
+    return lo;
+}
+
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k1_kernel(Params p) {
     __shared__ __attribute__((aligned(16))) uint16_t s_T[BT * LROW];  // transpose tile
     __shared__ __attribute__((aligned(16))) float s_L[BT * BT];
@@ -80,29 +100,45 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k1
     const int r = lane & 15;
     const int q4 = lane >> 4;
     const int colbase = 4 * q4;
-    const int NT = p.NT, H = p.H, T = p.T;
-    const int c = blockIdx.x % NT;
-    const int bh = blockIdx.x / NT;
-    const int b = bh / H, h = bh - (bh / H) * H;
+    const int H = p.H, HV = p.HV;
+    int hv, c;
+    SeqSpan sp;
+    if (p.cu_seqlens) {
+        // Slot x of value head hv belongs to the sequence n with the largest
+        // floor(bos_n / 16) + n <= x; slots past its last chunk are gaps.
+        hv = blockIdx.x / p.NS;
+        const int x = blockIdx.x - hv * p.NS;
+        const int n = find_sequence(p, x, lane);
+        sp = seq_span(p, n * HV + hv);
+        c = (int)((int64_t)x - (sp.rec0 - (int64_t)hv * p.NS));
+        if (c < 0 || c >= sp.nt) return;  // wave-uniform: no barrier passed yet
+    } else {
+        c = blockIdx.x % p.NT;
+        const int bh = blockIdx.x / p.NT;
+        hv = bh - (bh / HV) * HV;
+        sp = seq_span(p, bh);
+    }
+    const int h = hv / (HV / H);  // the q/k head of this value head
     const int t0 = c * BT;
-    const int nvalid = min(BT, T - t0);
+    const int nvalid = min(BT, sp.len - t0);
     const bool valid = r < nvalid;
-    const int64_t tok = (int64_t)b * T + t0 + r;  // token of this lane's row
-    const int64_t rowoff = (tok * H + h) * DK;    // element offset of that row
+    const int64_t tok = sp.tok0 + t0 + r;        // token of this lane's row
+    const int64_t rowoff = (tok * H + h) * DK;    // q/k element offset of that row
+    const int64_t vrowoff = (tok * HV + hv) * DK; // v/g element offset of that row
 
     // ---- loads (kernels.py:97-106); padded rows read as zero -------------
     Row32 qp, kp, vp;
     load_row(p.q + rowoff, valid, colbase, qp);
     load_row(p.k + rowoff, valid, colbase, kp);
-    load_row(p.v + rowoff, valid, colbase, vp);
+    load_row(p.v + vrowoff, valid, colbase, vp);
     float G[32];
     if (p.g_bf16) {
         Row32 gp;
-        load_row(static_cast<const uint16_t*>(p.g) + rowoff, valid, colbase, gp);
+        load_row(static_cast<const uint16_t*>(p.g) + vrowoff, valid, colbase, gp);
 #pragma unroll
         for (int j = 0; j < 32; ++j) G[j] = elem(gp, j);
     } else {
-        const float* gsrc = static_cast<const float*>(p.g) + rowoff;
+        const float* gsrc = static_cast<const float*>(p.g) + vrowoff;
 #pragma unroll
         for (int kt = 0; kt < 8; ++kt) {
             f32x4 a = {0.f, 0.f, 0.f, 0.f};
@@ -113,7 +149,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k1
     }
     float beta = 0.f;
     if (valid) {
-        const int64_t bi = tok * H + h;
+        const int64_t bi = tok * HV + hv;
         beta = p.beta_bf16 ? bf2f(static_cast<const uint16_t*>(p.beta)[bi])
                            : static_cast<const float*>(p.beta)[bi];
     }
@@ -144,8 +180,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k1
 
     // ---- gate and chunk-local log2 cumsum (kernels.py:115-124) -----------
     if (p.use_gate) {
-        const float ea = expf(p.A_log[h]);
-        const float* bias = p.dt_bias ? p.dt_bias + h * DK : nullptr;
+        const float ea = expf(p.A_log[hv]);
+        const float* bias = p.dt_bias ? p.dt_bias + hv * DK : nullptr;
 #pragma unroll
         for (int kt = 0; kt < 8; ++kt) {
             f32x4 bb = {0.f, 0.f, 0.f, 0.f};
@@ -158,6 +194,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k1
                 G[4 * kt + i] = row_scan16(gate) * RCP_LN2;
             }
         }
+    } else if (p.g_log) {
+        // g is the per-token natural-log decay: the same cumsum-then-scale
+        // as the in-kernel gate, on g itself.
+#pragma unroll
+        for (int j = 0; j < 32; ++j) G[j] = row_scan16(valid ? G[j] : 0.f) * RCP_LN2;
     }
 
     // ---- mid-row recentring, grams on matrix cores (kernels.py:129-155) ---
@@ -181,7 +222,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k1
     // This chunk's record.  Its stores are non-temporal: the records are
     // written once here and read once by stage 2, and left dirty in L2 they
     // slow stage 2's own stores by the write-backs they force.
-    uint8_t* rec = p.ws + ((int64_t)bh * NT + c) * REC_BYTES;
+    uint8_t* rec = p.ws + (sp.rec0 + c) * REC_BYTES;
 
     f32x4 aqk, L;
 #pragma unroll
@@ -248,7 +289,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k1
                 for (int i = 0; i < 4; ++i) {
                     const int row = 4 * q4 + i;
                     if (row < nvalid) {
-                        const int64_t o = (((int64_t)b * T + t0 + row) * H + h) * DK + 16 * vt + r;
+                        const int64_t o = ((sp.tok0 + t0 + row) * HV + hv) * DK + 16 * vt + r;
                         p.dbg_u[o] = (uint16_t)(i == 0 ? ub.x : i == 1 ? (ub.x >> 16)
                                                 : i == 2 ? ub.y : (ub.y >> 16));
                     }
@@ -335,13 +376,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k1
 
     // ---- optional reference-layout intermediates (kernels.py:125,153,178-184)
     if (p.dbg_w && valid) {
-        const int64_t bt16 = (tok * H + h) * BT + 4 * q4;
+        const int64_t bt16 = (tok * HV + hv) * BT + 4 * q4;
         *reinterpret_cast<u32x2*>(p.dbg_Aqk + bt16) = aqk_bf;
         *reinterpret_cast<u32x2*>(p.dbg_A_inv + bt16) = ainv_bf;
 #pragma unroll
         for (int kt = 0; kt < 8; ++kt) {
-            *reinterpret_cast<u32x2*>(p.dbg_w + rowoff + 16 * kt + colbase) = wpk[kt] ^ 0x80008000u;
-            *reinterpret_cast<f32x4*>(p.dbg_g + rowoff + 16 * kt + colbase) =
+            *reinterpret_cast<u32x2*>(p.dbg_w + vrowoff + 16 * kt + colbase) = wpk[kt] ^ 0x80008000u;
+            *reinterpret_cast<f32x4*>(p.dbg_g + vrowoff + 16 * kt + colbase) =
                 f32x4{G[4 * kt + 0], G[4 * kt + 1], G[4 * kt + 2], G[4 * kt + 3]};
         }
     }
@@ -350,7 +391,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k1
 }  // namespace
 
 hipError_t launch_k1(const Params& p, hipStream_t stream) {
-    const int64_t grid = (int64_t)p.B * p.H * p.NT;
+    const int64_t grid = p.cu_seqlens ? (int64_t)p.HV * p.NS : (int64_t)p.B * p.HV * p.NT;
     hipLaunchKernelGGL(k1_kernel, dim3((unsigned)grid), dim3(64), 0, stream, p);
     return hipGetLastError();
 }

@@ -222,13 +222,13 @@ __device__ __forceinline__ u32x2 quad_transpose(uint32_t p0, uint32_t p1, int j)
 
 // Constants of the chunk loop.
 struct Ctx {
-    __amdgpu_buffer_rsrc_t rs;  // copy: this head's records, NT * REC_BYTES bytes
+    __amdgpu_buffer_rsrc_t rs;  // copy: this sequence-head's records, NT * REC_BYTES bytes
     uint32_t voff16;            // copy: lane * 16
     uint32_t u_off;             // copy: REC_U + 1024 * (vt / 2)
-    uint16_t* obase;            // output: o[b, 0, h, 16*vt + 4*((lane%16)/4)]
+    uint16_t* obase;            // output: o[first token, hv, 16*vt + 4*((lane%16)/4)]
     int64_t orow_stride;        // output: elements between consecutive tokens of o
     float scale;
-    int NT, T, lane, q4, vt;
+    int NT, T, lane, q4, vt;    // NT chunks over T tokens (this sequence's)
 };
 
 // State wave, chunk c in ring slot S (a template argument, so every LDS
@@ -452,9 +452,9 @@ __device__ __forceinline__ void copy_round(const Ctx& cx, int c) {
     }
 }
 
-__device__ __forceinline__ void copy_wave(const Params& p, Ctx& cx, int bh) {
+__device__ __forceinline__ void copy_wave(const Params& p, Ctx& cx, const SeqSpan& sp) {
     const int NT = cx.NT;
-    cx.rs = __builtin_amdgcn_make_buffer_rsrc(p.ws + (int64_t)bh * NT * REC_BYTES, (short)0,
+    cx.rs = __builtin_amdgcn_make_buffer_rsrc(p.ws + sp.rec0 * REC_BYTES, (short)0,
                                               NT * REC_BYTES, BUF_DWORD3);
     cx.voff16 = cx.lane * 16;
     cx.u_off = REC_U + 1024 * (cx.vt >> 1);
@@ -470,21 +470,18 @@ __device__ __forceinline__ void copy_wave(const Params& p, Ctx& cx, int bh) {
     copy_barrier();  // the output wave's last chunk
 }
 
-__device__ __forceinline__ void output_wave(const Params& p, Ctx& cx, int b, int h) {
+__device__ __forceinline__ void output_wave(const Params& p, Ctx& cx, const SeqSpan& sp, int hv) {
     const int x = cx.lane & 15;
-    cx.obase = p.o + ((int64_t)b * cx.T * p.H + h) * DK + 16 * cx.vt + 4 * (x >> 2);
-    cx.orow_stride = (int64_t)p.H * DK;
+    cx.obase = p.o + (sp.tok0 * p.HV + hv) * DK + 16 * cx.vt + 4 * (x >> 2);
+    cx.orow_stride = (int64_t)p.HV * DK;
     chunk_barrier();
     chunk_barrier();
     for (int c = 0; c < cx.NT; c += RING) output_round<0>(cx, c);
 }
 
-__device__ __forceinline__ void state_wave(const Params& p, const Ctx& cx, int bh) {
-    const int lane = cx.lane, q4 = cx.q4, vt = cx.vt;
-    const int v = 16 * vt + (lane & 15);
-    // S^T tiles: St[kt][i] = S[v][16*kt + 4*q4 + i].
-    f32x4 St[8];
-    const int64_t sbase = (int64_t)bh * DK * DK;
+// S^T tiles of this lane: St[kt][i] = S[v][16*kt + 4*q4 + i], v = 16*vt + lane%16.
+__device__ __forceinline__ void load_state(const Params& p, int64_t sbase, int v, int q4,
+                                           f32x4 (&St)[8]) {
 #pragma unroll
     for (int kt = 0; kt < 8; ++kt) {
         St[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -498,6 +495,29 @@ __device__ __forceinline__ void state_wave(const Params& p, const Ctx& cx, int b
             }
         }
     }
+}
+
+__device__ __forceinline__ void store_state(const Params& p, int64_t sbase, int v, int q4,
+                                            const f32x4 (&St)[8]) {
+    if (!p.ht) return;
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) {
+        const int k0 = 16 * kt + 4 * q4;
+        if (p.ht_v_first) {
+            *reinterpret_cast<f32x4*>(p.ht + sbase + (int64_t)v * DK + k0) = St[kt];
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) p.ht[sbase + (int64_t)(k0 + i) * DK + v] = St[kt][i];
+        }
+    }
+}
+
+__device__ __forceinline__ void state_wave(const Params& p, const Ctx& cx, int bh) {
+    const int lane = cx.lane, q4 = cx.q4, vt = cx.vt;
+    const int v = 16 * vt + (lane & 15);
+    const int64_t sbase = (int64_t)bh * DK * DK;
+    f32x4 St[8];
+    load_state(p, sbase, v, q4, St);
     chunk_barrier();  // chunks 0 and 1 are in the ring
     StateOps op[2];
     read_state_ops_a(ring, lane, vt, op[0]);
@@ -513,19 +533,7 @@ __device__ __forceinline__ void state_wave(const Params& p, const Ctx& cx, int b
     for (; c + RING < cx.NT; c += RING) state_round_full<1, RING>(cx, St, op, vn);
     state_round_tail<1 % RING, RING>(cx, c, St, op, vn);
     chunk_barrier();  // the output wave's last chunk
-
-    if (p.ht) {
-#pragma unroll
-        for (int kt = 0; kt < 8; ++kt) {
-            const int k0 = 16 * kt + 4 * q4;
-            if (p.ht_v_first) {
-                *reinterpret_cast<f32x4*>(p.ht + sbase + (int64_t)v * DK + k0) = St[kt];
-            } else {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) p.ht[sbase + (int64_t)(k0 + i) * DK + v] = St[kt][i];
-            }
-        }
-    }
+    store_state(p, sbase, v, q4, St);
 }
 
 enum Role { STATE = 0, OUTPUT = 1, COPY = 2 };
@@ -538,40 +546,52 @@ enum Role { STATE = 0, OUTPUT = 1, COPY = 2 };
 __global__ __launch_bounds__(192) void k2_kernel(Params p) {
     const int lane = threadIdx.x & 63;
     const int role = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int nbh = p.B * p.H;
+    const int nbh = (p.cu_seqlens ? p.N : p.B) * p.HV;
 
     // Work-group -> (head, value tile), XCD aware: consecutive work-group ids
     // go to different XCDs round-robin, so the 8 tiles of one head get ids
     // of one residue class mod 8 and share that XCD's L2 for the records.
     const int wg = blockIdx.x;
     const int lin = (wg & 7) * nbh + (wg >> 3);
-    const int bh = lin >> 3;
-    const int b = bh / p.H, h = bh - b * p.H;
+    const int bh = lin >> 3;  // (batch row or sequence) * HV + value head
+    const int hv = bh - (bh / p.HV) * p.HV;
+    const SeqSpan sp = seq_span(p, bh);
 
     Ctx cx;
     cx.scale = p.scale;
-    cx.NT = p.NT;
-    cx.T = p.T;
+    cx.NT = sp.nt;
+    cx.T = sp.len;
     cx.lane = lane;
     cx.q4 = lane >> 4;
     cx.vt = lin & 7;
 
+    if (sp.nt == 0) {
+        // An empty sequence: its final state is its initial state.  Every
+        // role sees the same count, so no wave reaches a barrier.
+        if (role == STATE) {
+            f32x4 St[8];
+            const int v = 16 * cx.vt + (lane & 15);
+            load_state(p, (int64_t)bh * DK * DK, v, cx.q4, St);
+            store_state(p, (int64_t)bh * DK * DK, v, cx.q4, St);
+        }
+        __builtin_amdgcn_endpgm();
+    }
     if (role == STATE) {
         state_wave(p, cx, bh);
         __builtin_amdgcn_endpgm();
     }
     if (role == OUTPUT) {
-        output_wave(p, cx, b, h);
+        output_wave(p, cx, sp, hv);
         __builtin_amdgcn_endpgm();
     }
-    copy_wave(p, cx, bh);
+    copy_wave(p, cx, sp);
     __builtin_amdgcn_endpgm();
 }
 
 }  // namespace
 
 hipError_t launch_k2(const Params& p, hipStream_t stream) {
-    const int64_t grid = (int64_t)p.B * p.H * 8;
+    const int64_t grid = (int64_t)(p.cu_seqlens ? p.N : p.B) * p.HV * 8;
     hipLaunchKernelGGL(k2_kernel, dim3((unsigned)grid), dim3(192), 0, stream, p);
     return hipGetLastError();
 }

@@ -7,7 +7,9 @@
 //   S     = S + v_new k^_t^T
 //   o_t   = scale * S q^_t
 // alpha_t = exp(lb * sigmoid(exp(A_log) * (g_t + dt_bias))) with the in-kernel
-// gate, else exp(g_t) (g the per-token log decay).  This is the recurrence the
+// gate; else exp(g_t) when g is the per-token log decay (g_log), else
+// 2^(G_t - G_{t-1}) with G the chunk-local log2 cumsum the chunked path takes
+// (G_{-1} = 0 at every 16-token chunk start of a sequence).  This is the recurrence the
 // chunked path is the WY form of (kernels.py:53-302 computes it chunk-wise);
 // the reference's tests use FLA's fused_recurrent_kda for it
 // (/root/reference/tests/test_kda_bt16.py:26-38), and its roadmap lists the
@@ -21,7 +23,8 @@
 // for itself (lane l: elements 2l, 2l+1; the l2 norms by a wave-wide
 // butterfly sum) into its own LDS area and read back as broadcasts.
 // Grouped value heads (GVA): value head hv reads q/k head hv / (HV / H)
-// (kernels.py:88).
+// (kernels.py:88).  Varlen: one work-group per (sequence, value head), over
+// the sequence's tokens, with states [N, HV, ...].
 #include "kda_common.h"
 
 namespace kda {
@@ -42,10 +45,11 @@ __device__ __forceinline__ float wave_sum(float x) {
 __device__ __forceinline__ float sigmoid_precise(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 __global__ __launch_bounds__(128) void recurrent_kernel(Params p) {
-    const int HV = p.HV, H = p.H, T = p.T;
-    const int bhv = blockIdx.x;  // b * HV + hv
-    const int b = bhv / HV, hv = bhv - b * HV;
+    const int HV = p.HV, H = p.H;
+    const int bhv = blockIdx.x;  // (batch row or sequence) * HV + hv
+    const int hv = bhv - (bhv / HV) * HV;
     const int h = hv / (HV / H);
+    const SeqSpan sp = seq_span(p, bhv);
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int vrow = 64 * w + lane;  // this lane's row of S
     const int k0 = 2 * lane;         // this lane's two elements of the token vectors
@@ -77,9 +81,10 @@ __global__ __launch_bounds__(128) void recurrent_kernel(Params p) {
         dtb1 = p.dt_bias[hv * DK + k0 + 1];
     }
 
-    for (int t = 0; t < T; ++t) {
-        const int64_t rq = ((int64_t)b * T + t) * H + h;   // q/k row
-        const int64_t rv = ((int64_t)b * T + t) * HV + hv; // v/g/beta/o row
+    float gp0 = 0.0f, gp1 = 0.0f;  // G_{t-1} of the cumsum form
+    for (int t = 0; t < sp.len; ++t) {
+        const int64_t rq = (sp.tok0 + t) * H + h;   // q/k row
+        const int64_t rv = (sp.tok0 + t) * HV + hv; // v/g/beta/o row
 
         float q0 = bf2f(p.q[rq * DK + k0]), q1 = bf2f(p.q[rq * DK + k0 + 1]);
         float c0 = bf2f(p.k[rq * DK + k0]), c1 = bf2f(p.k[rq * DK + k0 + 1]);
@@ -95,9 +100,15 @@ __global__ __launch_bounds__(128) void recurrent_kernel(Params p) {
         if (p.use_gate) {
             a0 = expf(p.lower_bound * sigmoid_precise(ea * (g0 + dtb0)));
             a1 = expf(p.lower_bound * sigmoid_precise(ea * (g1 + dtb1)));
-        } else {
+        } else if (p.g_log) {
             a0 = expf(g0);
             a1 = expf(g1);
+        } else {
+            if (t % BT == 0) gp0 = gp1 = 0.0f;
+            a0 = exp2f(g0 - gp0);
+            a1 = exp2f(g1 - gp1);
+            gp0 = g0;
+            gp1 = g1;
         }
         vec[w][0][k0] = a0; vec[w][0][k0 + 1] = a1;
         vec[w][1][k0] = c0; vec[w][1][k0 + 1] = c1;
@@ -150,7 +161,7 @@ __global__ __launch_bounds__(128) void recurrent_kernel(Params p) {
 }  // namespace
 
 hipError_t launch_recurrent(const Params& p, hipStream_t stream) {
-    const int64_t grid = (int64_t)p.B * p.HV;
+    const int64_t grid = (int64_t)(p.cu_seqlens ? p.N : p.B) * p.HV;
     hipLaunchKernelGGL(recurrent_kernel, dim3((unsigned)grid), dim3(128), 0, stream, p);
     return hipGetLastError();
 }

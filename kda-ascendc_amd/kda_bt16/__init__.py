@@ -7,9 +7,14 @@ Triton kernels the reference also exports are replaced by
 HIP library); ``kda_bt16_kernel_fused`` raises NotImplementedError.
 
 Beyond the reference: ``kda_recurrent_fwd`` (token-by-token recurrence in
-fp32, the decode step and an on-GPU gold) and ``kda_decode_step``.
+fp32, the decode step and an on-GPU gold) and ``kda_decode_step``; FLA's
+``chunk_kda`` / ``fused_recurrent_kda`` calling convention (``kda_bt16.fla``)
+and a per-function backend dispatch that registers these kernels
+(``kda_bt16.dispatch``).
 """
 
+from . import dispatch
+from .fla import chunk_kda, fused_recurrent_kda
 from .kernels import (
     kda_bt16_debug,
     kda_bt16_fwd,
@@ -26,5 +31,8 @@ __all__ = [
     "kda_bt16_stage_launchers",
     "kda_recurrent_fwd",
     "kda_decode_step",
+    "chunk_kda",
+    "fused_recurrent_kda",
+    "dispatch",
 ]
 __version__ = "0.1.0"

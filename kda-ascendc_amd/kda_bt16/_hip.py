@@ -12,19 +12,23 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libkda_bt16_hip.so"
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 USE_GATE = 1 << 0
 USE_QK_L2NORM = 1 << 1
 USE_BETA_SIGMOID = 1 << 2
 STATE_V_FIRST = 1 << 3
 O_FP32 = 1 << 4  # token recurrence only
+G_LOG_DECAY = 1 << 5  # without USE_GATE: g is the per-token natural-log decay
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
+DTYPE_I32 = 2
+DTYPE_I64 = 3
 
 EXPORTED_SYMBOLS = (
     "kda_bt16_workspace_bytes",
+    "kda_bt16_workspace_bytes_args",
     "kda_bt16_fwd_hip",
     "kda_bt16_k1_hip",
     "kda_bt16_k2_hip",
@@ -67,6 +71,9 @@ class KdaBt16Args(ctypes.Structure):
         ("dbg_w", ctypes.c_void_p),
         ("dbg_u", ctypes.c_void_p),
         ("dbg_g", ctypes.c_void_p),
+        ("cu_seqlens", ctypes.c_void_p),
+        ("cu_seqlens_dtype", ctypes.c_int32),
+        ("N", ctypes.c_int32),
     ]
 
 
@@ -98,6 +105,8 @@ def lib() -> ctypes.CDLL:
         h = ctypes.CDLL(str(LIB_PATH))
         h.kda_bt16_workspace_bytes.restype = ctypes.c_size_t
         h.kda_bt16_workspace_bytes.argtypes = [ctypes.c_int32] * 5
+        h.kda_bt16_workspace_bytes_args.restype = ctypes.c_size_t
+        h.kda_bt16_workspace_bytes_args.argtypes = [ctypes.POINTER(KdaBt16Args)]
         for name in ("kda_bt16_fwd_hip", "kda_bt16_k1_hip", "kda_bt16_k2_hip",
                      "kda_recurrent_fwd_hip"):
             fn = getattr(h, name)
@@ -114,8 +123,14 @@ def lib() -> ctypes.CDLL:
         return _lib
 
 
-def workspace_bytes(B: int, T: int, H: int, K: int, V: int) -> int:
-    return int(lib().kda_bt16_workspace_bytes(B, T, H, K, V))
+def workspace_bytes(B: int, T: int, HV: int, K: int, V: int) -> int:
+    """Fixed-length workspace bytes (``kda_bt16_workspace_bytes``)."""
+    return int(lib().kda_bt16_workspace_bytes(B, T, HV, K, V))
+
+
+def workspace_bytes_args(args: KdaBt16Args) -> int:
+    """Workspace bytes for any arguments, varlen included."""
+    return int(lib().kda_bt16_workspace_bytes_args(ctypes.byref(args)))
 
 
 def call(name: str, args: KdaBt16Args, stream: int) -> None:

@@ -18,7 +18,14 @@ Differences from the reference, all supersets of its contract:
   ``[K, V]`` state directly instead of transposing at the boundary
   (kernels.py:499-510); the values are identical;
 * ``use_fused_kernel=True`` is accepted and runs the same two-stage path
-  (the reference's own test requires the two to agree, tests/test_kda_bt16.py:174-200).
+  (the reference's own test requires the two to agree, tests/test_kda_bt16.py:174-200);
+* ``HV`` may be any multiple of ``H`` (grouped value heads: value head hv
+  reads q/k head hv // (HV // H), the indexing of kernels.py:88, which the
+  reference's validation does not yet admit, kernels.py:729-730);
+* ``cu_seqlens`` (keyword, default None) packs N variable-length sequences
+  along T with B == 1, FLA's varlen convention; the states are then
+  ``[N, HV, ...]`` (the reference lists varlen as a limitation,
+  README.md:420-421).
 """
 
 from __future__ import annotations
@@ -50,13 +57,15 @@ def _validate_kda_inputs(
     A_log: torch.Tensor | None,
     dt_bias: torch.Tensor | None,
     state_v_first: bool,
-    allow_gva: bool = False,
+    cu_seqlens: torch.Tensor | None = None,
 ) -> tuple[int, int, int, int, int, int]:
-    """Input contract of kernels.py:609-749, same order and messages.
+    """Input contract of kernels.py:609-749, same order and messages, with
+    two widenings: HV may be any multiple of H (grouped value heads; the
+    reference requires HV == H, kernels.py:729-730), and ``cu_seqlens``
+    packs N sequences along T (FLA's varlen convention and messages: B must
+    be 1 and the states have N rows).
 
-    ``allow_gva`` (token recurrence only) accepts HV a multiple of H instead
-    of HV == H.  Returns ``(B, T, H, K, HV, V)``; raises ``ValueError`` /
-    ``TypeError``.
+    Returns ``(B, T, H, K, HV, V)``; raises ``ValueError`` / ``TypeError``.
     """
     if q.ndim != 4:
         raise ValueError(f"q must be 4D [B, T, H, D], got {q.ndim}D with shape {q.shape}")
@@ -113,6 +122,28 @@ def _validate_kda_inputs(
     if not all(x.device == q.device for x in [k, v, g, beta]):
         raise ValueError(f"All tensors must be on same device as q ({q.device})")
 
+    S = B
+    if cu_seqlens is not None:
+        if cu_seqlens.ndim != 1 or cu_seqlens.numel() < 2:
+            raise ValueError(f"cu_seqlens must be 1D with at least 2 entries, got shape {tuple(cu_seqlens.shape)}")
+        if cu_seqlens.dtype not in (torch.int32, torch.int64):
+            raise TypeError(f"cu_seqlens must be int32 or int64, got {cu_seqlens.dtype}")
+        if not cu_seqlens.is_contiguous():
+            raise ValueError("cu_seqlens must be contiguous")
+        if cu_seqlens.device != q.device:
+            raise ValueError(f"cu_seqlens device {cu_seqlens.device} must match q ({q.device})")
+        if B != 1:
+            raise ValueError(
+                f"The batch size is expected to be 1 rather than {B} when using `cu_seqlens`. "
+                "Please flatten variable-length inputs before processing."
+            )
+        S = cu_seqlens.numel() - 1
+        if initial_state is not None and initial_state.shape[0] != S:
+            raise ValueError(
+                "The number of initial states is expected to be equal to the number of input "
+                f"sequences, i.e., {S} rather than {initial_state.shape[0]}."
+            )
+
     if initial_state is not None:
         if not initial_state.is_contiguous():
             raise ValueError("initial_state must be contiguous")
@@ -120,7 +151,7 @@ def _validate_kda_inputs(
             raise TypeError(f"initial_state must be float32, got {initial_state.dtype}")
         if initial_state.device != q.device:
             raise ValueError(f"initial_state device {initial_state.device} must match q ({q.device})")
-        expected_shape = (B, HV, V, K) if state_v_first else (B, HV, K, V)
+        expected_shape = (S, HV, V, K) if state_v_first else (S, HV, K, V)
         if initial_state.shape != expected_shape:
             raise ValueError(
                 f"initial_state.shape {initial_state.shape} must be {expected_shape} "
@@ -149,11 +180,8 @@ def _validate_kda_inputs(
 
     if K != 128 or V != 128:
         raise ValueError(f"prototype targets K=V=128, got K={K}, V={V}")
-    if allow_gva:
-        if HV % H != 0:
-            raise ValueError(f"HV must be a multiple of H (grouped value heads), got HV={HV}, H={H}")
-    elif HV != H:
-        raise ValueError(f"prototype targets MHA (HV == H), got HV={HV}, H={H}")
+    if HV % H != 0:
+        raise ValueError(f"HV must be a multiple of H (grouped value heads), got HV={HV}, H={H}")
 
     if use_gate_in_kernel:
         if not safe_gate:
@@ -196,7 +224,7 @@ def _dtype_tag(t: torch.Tensor) -> int:
 
 def _make_args(
     q, k, v, g, beta, scale, lower_bound, A_log, dt_bias, h0, o, ht, ws, ws_bytes,
-    flags, dbg=None,
+    flags, dbg=None, cu_seqlens=None,
 ) -> _hip.KdaBt16Args:
     B, T, H, K = q.shape
     HV, V = v.shape[2], v.shape[-1]
@@ -222,11 +250,18 @@ def _make_args(
         a.dbg_w = dbg["w"].data_ptr()
         a.dbg_u = dbg["u"].data_ptr()
         a.dbg_g = dbg["g"].data_ptr()
+    if cu_seqlens is not None:
+        a.cu_seqlens = cu_seqlens.data_ptr()
+        a.cu_seqlens_dtype = _hip.DTYPE_I64 if cu_seqlens.dtype == torch.int64 else _hip.DTYPE_I32
+        a.N = cu_seqlens.numel() - 1
     return a
 
 
-def _flags(use_gate: bool, use_l2norm: bool, use_beta_sigmoid: bool, state_v_first: bool) -> int:
+def _flags(use_gate: bool, use_l2norm: bool, use_beta_sigmoid: bool, state_v_first: bool,
+           g_log: bool = False) -> int:
     f = 0
+    if g_log and not use_gate:
+        f |= _hip.G_LOG_DECAY
     if use_gate:
         f |= _hip.USE_GATE
     if use_l2norm:
@@ -257,6 +292,8 @@ def _run(
     return_intermediates: bool,
     use_fused: bool = False,
     reuse_workspace: bool = False,
+    cu_seqlens: torch.Tensor | None = None,
+    g_log: bool = False,
 ):
     """Host driver, the counterpart of kernels.py:475-606: allocate outputs,
     lease the workspace, launch stage 1 and stage 2 through the C ABI."""
@@ -266,9 +303,10 @@ def _run(
         _aligned(x) for x in (q, k, v, g, initial_state, dt_bias))
     B, T, H, K = q.shape
     HV, V = v.shape[2], v.shape[-1]
+    S = B if cu_seqlens is None else cu_seqlens.numel() - 1
     dev = q.device
 
-    cache_key = (dev, B, T, H, HV, K, V, k.dtype, return_intermediates)
+    cache_key = (dev, B, T, H, HV, K, V, S, k.dtype, return_intermediates)
     cache = _WORKSPACE_CACHE.get(cache_key) if reuse_workspace else None
 
     def alloc(name, shape, dtype):
@@ -284,7 +322,7 @@ def _run(
     o = alloc("o", (B, T, HV, V), k.dtype)
     ht = None
     if output_final_state:
-        ht = alloc("ht", (B, HV, V, K) if state_v_first else (B, HV, K, V), torch.float32)
+        ht = alloc("ht", (S, HV, V, K) if state_v_first else (S, HV, K, V), torch.float32)
 
     dbg = None
     if return_intermediates:
@@ -298,15 +336,16 @@ def _run(
 
     with torch.cuda.device(dev):
         stream = torch.cuda.current_stream(dev).cuda_stream
-        ws_bytes = _hip.workspace_bytes(B, T, H, K, V)
-        ws = workspace.lease(dev, stream, ws_bytes)
         args = _make_args(
             q, k, v, g, beta, scale, lower_bound if use_gate_in_kernel else None,
-            A_log, dt_bias, initial_state, o, ht, ws, ws_bytes,
+            A_log, dt_bias, initial_state, o, ht, None, 0,
             _flags(use_gate_in_kernel, use_qk_l2norm_in_kernel, use_beta_sigmoid_in_kernel,
-                   state_v_first),
-            dbg,
+                   state_v_first, g_log),
+            dbg, cu_seqlens,
         )
+        ws_bytes = _hip.workspace_bytes_args(args)
+        ws = workspace.lease(dev, stream, ws_bytes)
+        args.workspace, args.workspace_bytes = ws.data_ptr(), ws_bytes
         _hip.call("kda_bt16_fwd_hip", args, stream)
 
     if return_intermediates:
@@ -333,19 +372,23 @@ def kda_bt16_fwd(
     state_v_first: bool = True,
     use_fused_kernel: bool = False,
     reuse_workspace: bool = False,
+    *,
+    cu_seqlens: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor | None]:
     """KDA forward (reference: kernels.py:752-810).
 
     Args:
         q/k: ``[B, T, H, K]``, bf16, ``K == 128``.
-        v: ``[B, T, HV, V]``, bf16, ``HV == H``, ``V == 128``.
+        v: ``[B, T, HV, V]``, bf16, ``HV`` a multiple of ``H``, ``V == 128``.
         g: ``[B, T, HV, K]`` fp32 or bf16: the raw gate if
             ``use_gate_in_kernel``, else the precomputed chunk-local cumsum
             in the log2 domain.
         beta: ``[B, T, HV]`` fp32 or bf16; raw logits if
             ``use_beta_sigmoid_in_kernel``.
         initial_state: fp32 ``[B, HV, V, K]`` (``state_v_first=True``) or
-            ``[B, HV, K, V]``.
+            ``[B, HV, K, V]``; ``N`` rows instead of ``B`` with ``cu_seqlens``.
+        cu_seqlens: optional int32/int64 ``[N + 1]`` offsets of N sequences
+            packed along T (B must be 1).
 
     Returns:
         ``o`` of shape ``[B, T, HV, V]`` (bf16) and, if
@@ -355,7 +398,7 @@ def kda_bt16_fwd(
     B, T, H, K, HV, V = _validate_kda_inputs(
         q, k, v, g, beta, initial_state,
         use_gate_in_kernel, safe_gate, lower_bound,
-        A_log, dt_bias, state_v_first,
+        A_log, dt_bias, state_v_first, cu_seqlens,
     )
     if scale is None:
         scale = K ** -0.5
@@ -366,6 +409,7 @@ def kda_bt16_fwd(
         return_intermediates=False,
         use_fused=use_fused_kernel,
         reuse_workspace=reuse_workspace,
+        cu_seqlens=cu_seqlens,
     )
 
 
@@ -386,6 +430,8 @@ def kda_bt16_debug(
     A_log: torch.Tensor | None = None,
     dt_bias: torch.Tensor | None = None,
     state_v_first: bool = True,
+    *,
+    cu_seqlens: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor | None, dict]:
     """Like :func:`kda_bt16_fwd`, and also return the stage-1 intermediates
     ``{Aqk, A_inv, w, u, g}`` in the reference's layouts (kernels.py:813-850):
@@ -394,7 +440,7 @@ def kda_bt16_debug(
     B, T, H, K, HV, V = _validate_kda_inputs(
         q, k, v, g, beta, initial_state,
         use_gate_in_kernel, safe_gate, lower_bound,
-        A_log, dt_bias, state_v_first,
+        A_log, dt_bias, state_v_first, cu_seqlens,
     )
     if scale is None:
         scale = K ** -0.5
@@ -405,13 +451,15 @@ def kda_bt16_debug(
         return_intermediates=True,
         use_fused=False,
         reuse_workspace=False,
+        cu_seqlens=cu_seqlens,
     )
 
 
 def kda_bt16_stage_launchers(
     q, k, v, g, beta, scale=None, initial_state=None, output_final_state=False,
     use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True, use_beta_sigmoid_in_kernel=True,
-    lower_bound=-5.0, A_log=None, dt_bias=None, state_v_first=True,
+    lower_bound=-5.0, A_log=None, dt_bias=None, state_v_first=True, cu_seqlens=None,
+    g_log=False,
 ):
     """Return ``(k1, k2, o, ht)``: zero-argument callables that launch only
     stage 1 or only stage 2 on the current stream, over buffers allocated
@@ -419,26 +467,29 @@ def kda_bt16_stage_launchers(
     raw Triton kernels for the same purpose."""
     B, T, H, K, HV, V = _validate_kda_inputs(
         q, k, v, g, beta, initial_state, use_gate_in_kernel, True, lower_bound,
-        A_log, dt_bias, state_v_first,
+        A_log, dt_bias, state_v_first, cu_seqlens,
     )
     _require_gpu(q)
     if scale is None:
         scale = K ** -0.5
     dev = q.device
+    S = B if cu_seqlens is None else cu_seqlens.numel() - 1
     o = torch.empty((B, T, HV, V), dtype=torch.bfloat16, device=dev)
     ht = None
     if output_final_state:
-        ht = torch.empty((B, HV, V, K) if state_v_first else (B, HV, K, V),
+        ht = torch.empty((S, HV, V, K) if state_v_first else (S, HV, K, V),
                          dtype=torch.float32, device=dev)
-    ws_bytes = _hip.workspace_bytes(B, T, H, K, V)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     args = _make_args(
         q, k, v, g, beta, scale, lower_bound if use_gate_in_kernel else None,
-        A_log, dt_bias, initial_state, o, ht, ws, ws_bytes,
+        A_log, dt_bias, initial_state, o, ht, None, 0,
         _flags(use_gate_in_kernel, use_qk_l2norm_in_kernel, use_beta_sigmoid_in_kernel,
-               state_v_first),
+               state_v_first, g_log),
+        None, cu_seqlens,
     )
-    keep = (q, k, v, g, beta, A_log, dt_bias, initial_state, ws)
+    ws_bytes = _hip.workspace_bytes_args(args)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    args.workspace, args.workspace_bytes = ws.data_ptr(), ws_bytes
+    keep = (q, k, v, g, beta, A_log, dt_bias, initial_state, ws, cu_seqlens)
 
     def k1():
         _ = keep
@@ -469,6 +520,7 @@ def kda_recurrent_fwd(
     state_v_first: bool = True,
     output_dtype: torch.dtype = torch.bfloat16,
     inplace_final_state: bool = False,
+    cu_seqlens: torch.Tensor | None = None,
 ):
     """Token-by-token KDA recurrence on the GPU, fp32 state: the decode
     step (T == 1) and the fused-recurrent forward for any T.
@@ -480,8 +532,6 @@ def kda_recurrent_fwd(
 
     * without ``use_gate_in_kernel``, ``g`` is the per-token log decay
       (``alpha_t = exp(g_t)``), not a chunk-local cumsum;
-    * v, g, beta, A_log, dt_bias and the states may have ``HV`` heads, a
-      multiple of q/k's ``H`` (grouped value heads, ``kernels.py:88``);
     * ``output_dtype`` is bf16 or fp32 (fp32 makes this an on-GPU gold);
     * ``inplace_final_state`` writes the final state into ``initial_state``
       and returns it as ``ht`` (a decode step that allocates no state).
@@ -490,8 +540,9 @@ def kda_recurrent_fwd(
     """
     B, T, H, K, HV, V = _validate_kda_inputs(
         q, k, v, g, beta, initial_state, use_gate_in_kernel, True, lower_bound,
-        A_log, dt_bias, state_v_first, allow_gva=True,
+        A_log, dt_bias, state_v_first, cu_seqlens,
     )
+    S = B if cu_seqlens is None else cu_seqlens.numel() - 1
     if output_dtype not in (torch.bfloat16, torch.float32):
         raise TypeError(f"output_dtype must be bfloat16 or float32, got {output_dtype}")
     if inplace_final_state and initial_state is None:
@@ -510,15 +561,15 @@ def kda_recurrent_fwd(
     if inplace_final_state:
         ht = initial_state
     elif output_final_state:
-        ht = torch.empty((B, HV, V, K) if state_v_first else (B, HV, K, V),
+        ht = torch.empty((S, HV, V, K) if state_v_first else (S, HV, K, V),
                          dtype=torch.float32, device=dev)
     flags = _flags(use_gate_in_kernel, use_qk_l2norm_in_kernel, use_beta_sigmoid_in_kernel,
-                   state_v_first)
+                   state_v_first, g_log=True)
     if output_dtype == torch.float32:
         flags |= _hip.O_FP32
     args = _make_args(
         q, k, v, g, beta, scale, lower_bound if use_gate_in_kernel else None,
-        A_log, dt_bias, h0, o, ht, None, 0, flags,
+        A_log, dt_bias, h0, o, ht, None, 0, flags, None, cu_seqlens,
     )
     _hip.call("kda_recurrent_fwd_hip", args, torch.cuda.current_stream(dev).cuda_stream)
     return o, ht

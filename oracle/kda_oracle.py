@@ -70,17 +70,27 @@ def _unchunk(x: torch.Tensor, T: int) -> torch.Tensor:
 
 def k1_reference(
     q, k, v, g, beta, scale, *, A_log=None, dt_bias=None, lower_bound=-5.0,
-    use_gate=True, use_l2norm=True, use_beta_sigmoid=True, mode="kernel",
+    use_gate=True, use_l2norm=True, use_beta_sigmoid=True, mode="kernel", gate_log=False,
 ) -> dict:
-    """Stage-1 intermediates, chunked as [B, H, NT, 16, ...].
+    """Stage-1 intermediates, chunked as [B, HV, NT, 16, ...].
 
     Follows kernels.py:97-184.  Returns q_hat, k_hat, v, beta, G (fp32 log2
     cumsum), Aqk (stored bf16 in kernel mode), A_inv (fp32 and bf16), w, u,
     nvalid (valid rows per chunk).
+
+    Beyond the reference: grouped value heads (v, g, beta, A_log, dt_bias
+    with HV heads, value head hv using q/k head hv // (HV // H), the
+    indexing of kernels.py:88), and ``gate_log``: without ``use_gate``, g is
+    the per-token natural-log decay and G its chunk-local cumsum times
+    RCP_LN2, the cumsum-then-scale order of the in-kernel gate.
     """
     exact = mode == "exact"
     dt = torch.float64 if exact else torch.float32
-    B, T, H, K = q.shape
+    H = q.shape[2]
+    HV = v.shape[2]
+    q = q.repeat_interleave(HV // H, dim=2)
+    k = k.repeat_interleave(HV // H, dim=2)
+    B, T, H, K = q.shape  # H is now the value-head count
     NT = -(-T // BT)
     rows = torch.arange(NT * BT).reshape(NT, BT)
     valid = (rows < T)  # [NT, 16]
@@ -111,6 +121,8 @@ def k1_reference(
         gate = lower_bound * torch.sigmoid(ea * s)
         gate = torch.where(vmask, gate, torch.zeros((), dtype=dt))
         G = torch.cumsum(gate, dim=3) * RCP_LN2
+    elif gate_log:
+        G = torch.cumsum(torch.where(vmask, gc, torch.zeros((), dtype=dt)), dim=3) * RCP_LN2
     else:
         G = gc
 
@@ -203,7 +215,7 @@ def k2_reference(st: dict, scale, *, h0=None, state_v_first=True, mode="kernel",
 def chunked_reference(
     q, k, v, g, beta, scale=None, *, A_log=None, dt_bias=None, lower_bound=-5.0,
     initial_state=None, state_v_first=True, use_gate=True, use_l2norm=True,
-    use_beta_sigmoid=True, mode="kernel",
+    use_beta_sigmoid=True, mode="kernel", gate_log=False,
 ):
     """The reference's chunked forward on the CPU.
 
@@ -217,6 +229,7 @@ def chunked_reference(
     st = k1_reference(
         q, k, v, g, beta, scale, A_log=A_log, dt_bias=dt_bias, lower_bound=lower_bound,
         use_gate=use_gate, use_l2norm=use_l2norm, use_beta_sigmoid=use_beta_sigmoid, mode=mode,
+        gate_log=gate_log,
     )
     o, ht = k2_reference(
         st, scale, h0=initial_state, state_v_first=state_v_first, mode=mode,
@@ -296,6 +309,35 @@ def recurrent_gold(
         o[:, :, t] = scale * (S @ qf[:, :, t, :, None])[..., 0]
     ht = S if state_v_first else S.transpose(-1, -2).contiguous()
     return o.movedim(1, 2).contiguous(), ht
+
+
+def per_sequence(fn, q, k, v, g, beta, cu_seqlens, *args, initial_state=None,
+                 state_v_first=True, **kwargs):
+    """Varlen by definition: sequence n (tokens cu_seqlens[n] to
+    cu_seqlens[n+1] of the single batch row) runs on its own with state
+    initial_state[n], and the outputs are concatenated along T (o) and
+    stacked (final states).  ``fn`` is :func:`chunked_reference` or
+    :func:`recurrent_gold`; an empty sequence passes its state through.
+    Returns (o, ht)."""
+    cu = [int(x) for x in cu_seqlens]
+    HV = v.shape[2]
+    K, V = q.shape[-1], v.shape[-1]
+    outs, states = [], []
+    for n in range(len(cu) - 1):
+        a, b = cu[n], cu[n + 1]
+        h0 = None if initial_state is None else initial_state[n:n + 1]
+        if b == a:
+            if h0 is None:
+                shape = (1, HV, V, K) if state_v_first else (1, HV, K, V)
+                states.append(torch.zeros(shape))
+            else:
+                states.append(h0.clone())
+            continue
+        res = fn(q[:, a:b], k[:, a:b], v[:, a:b], g[:, a:b], beta[:, a:b], *args,
+                 initial_state=h0, state_v_first=state_v_first, **kwargs)
+        outs.append(res[0])
+        states.append(res[1])
+    return torch.cat(outs, dim=1), torch.cat(states, dim=0)
 
 
 def make_inputs(B, T, H, *, seed=42, g_std=1.0, h0_std=0.0, K=128, storage=torch.bfloat16,

@@ -57,6 +57,29 @@ def test_workspace_bytes():
     assert ws(2, 1037, 4, 128, 128) == 2 * 4 * 65 * 17408
     assert ws(1, 16, 1, 64, 128) == 0
     assert ws(0, 16, 1, 128, 128) == 0
+    # by arguments: value heads count, and varlen takes HV * (T // 16 + N) slots
+    assert _hip.workspace_bytes_args(_args(B=2, T=1037, H=2, HV=4)) == 2 * 4 * 65 * 17408
+    fake = 1 << 40
+    a = _args(T=1000, H=2, HV=4, cu_seqlens=fake, cu_seqlens_dtype=_hip.DTYPE_I64, N=7)
+    assert _hip.workspace_bytes_args(a) == 4 * (1000 // 16 + 7) * 17408
+    assert _hip.workspace_bytes_args(_args(cu_seqlens=fake, N=0)) == 0
+
+
+def test_varlen_argument_checks():
+    fake = 1 << 40  # never dereferenced: argument checks fail first
+    vl = dict(cu_seqlens=fake, cu_seqlens_dtype=_hip.DTYPE_I64, N=3)
+    for fn in ("kda_bt16_fwd_hip", "kda_recurrent_fwd_hip"):
+        f = getattr(_hip.lib(), fn)
+        assert f(ctypes.byref(_args(B=2, **vl)), None) == -1  # packed sequences need B == 1
+        assert f(ctypes.byref(_args(**{**vl, "N": 0})), None) == -1
+        assert f(ctypes.byref(_args(**{**vl, "cu_seqlens_dtype": 0})), None) == -1
+        assert f(ctypes.byref(_args(**{**vl, "cu_seqlens": fake + 4})), None) == -1
+        assert f(ctypes.byref(_args(**{**vl, "cu_seqlens": fake + 4,
+                                       "cu_seqlens_dtype": _hip.DTYPE_I32})), None) == -1  # no tensors
+    # workspace sized for the fixed-length layout is too small for varlen
+    full = dict(q=fake, k=fake, v=fake, g=fake, beta=fake, o=fake, workspace=fake)
+    a = _args(T=64, **full, **vl, workspace_bytes=4 * 17408)
+    assert _hip.lib().kda_bt16_fwd_hip(ctypes.byref(a), None) == -3
 
 
 def test_strerror_codes():
@@ -83,7 +106,7 @@ def test_argument_checks_return_codes_without_launching(fn):
     assert f(None, None) == -1
     assert f(ctypes.byref(_args(abi_version=99)), None) == -5
     assert f(ctypes.byref(_args(K=64)), None) == -2
-    assert f(ctypes.byref(_args(HV=2)), None) == -2
+    assert f(ctypes.byref(_args(H=2, HV=3)), None) == -2  # HV not a multiple of H
     assert f(ctypes.byref(_args(T=1973776 + 1)), None) == -2  # 32-bit per-head record size
     assert f(ctypes.byref(_args(T=0)), None) == -1
     assert f(ctypes.byref(_args(g_dtype=7)), None) == -1

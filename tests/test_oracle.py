@@ -14,6 +14,7 @@ from kda_oracle import (
     chunked_reference,
     k1_reference,
     make_inputs,
+    per_sequence,
     recurrent_gold,
 )
 from kda_testlib import GOLDEN_CASES, assert_close_rel, load_golden, maxdiff
@@ -236,3 +237,90 @@ def test_recurrent_grouped_value_heads_map_to_query_head():
             dtype=torch.float64)
         assert maxdiff(o[:, :, hv:hv + 1], o1) < 1e-12, hv
         assert maxdiff(ht[:, hv:hv + 1], ht1) < 1e-12, hv
+
+
+def test_exact_chunked_log_decay_equals_recurrence():
+    """Chunked restatement with per-token log decay (cumsum formed inside)
+    against the token recurrence with alpha = exp(g), fp64, partial chunks
+    and a non-zero state."""
+    inp = make_inputs(1, 37, 2, seed=21, h0_std=0.05)
+    g_log = -torch.rand(1, 37, 2, 128, dtype=torch.float64) * 0.4
+    kw = dict(use_gate=False, gate_log=True, initial_state=inp["h0"])
+    o_c, ht_c, _ = chunked_reference(inp["q"], inp["k"], inp["v"], g_log, inp["beta"].float(),
+                                     0.1, mode="exact", **kw)
+    o_g, ht_g = recurrent_gold(inp["q"], inp["k"], inp["v"], g_log, inp["beta"].float(), 0.1,
+                               dtype=torch.float64, **kw)
+    assert maxdiff(o_c, o_g) < 1e-8 and maxdiff(ht_c, ht_g) < 1e-7
+
+
+@pytest.mark.parametrize("state_v_first", [True, False])
+def test_exact_chunked_grouped_value_heads(state_v_first):
+    """Chunked restatement with HV = 2H against the token recurrence (itself
+    pinned against single-head runs), fp64."""
+    H, HV, T = 2, 4, 29
+    gen = torch.Generator().manual_seed(23)
+    q = torch.randn(1, T, H, 128, generator=gen).bfloat16()
+    k = torch.randn(1, T, H, 128, generator=gen).bfloat16()
+    v = torch.randn(1, T, HV, 128, generator=gen).bfloat16()
+    g = torch.randn(1, T, HV, 128, generator=gen)
+    beta = torch.randn(1, T, HV, generator=gen)
+    A_log = torch.log(torch.rand(HV, generator=gen) * 15 + 1)
+    dt_bias = torch.randn(HV * 128, generator=gen) * 0.1
+    h0 = torch.randn(1, HV, 128, 128, generator=gen) * 0.05
+    kw = dict(A_log=A_log, dt_bias=dt_bias, initial_state=h0, state_v_first=state_v_first)
+    o_c, ht_c, _ = chunked_reference(q, k, v, g, beta, 0.1, mode="exact", **kw)
+    o_g, ht_g = recurrent_gold(q, k, v, g, beta, 0.1, dtype=torch.float64, **kw)
+    assert o_c.shape == (1, T, HV, 128)
+    assert maxdiff(o_c, o_g) < 1e-8 and maxdiff(ht_c, ht_g) < 1e-7
+
+
+def _packed_recurrence(q, k, v, g, beta, cu, h0, scale):
+    """One token loop over the packed row, resetting the state to h0[n] at
+    each sequence start and saving it at each end (fp64, in-kernel gate
+    off, alpha = exp(g), no l2norm or sigmoid)."""
+    T, HV = v.shape[1], v.shape[2]
+    rep = HV // q.shape[2]
+    qf = q[0].double().repeat_interleave(rep, dim=1)
+    kf = k[0].double().repeat_interleave(rep, dim=1)
+    vf, gf, bf = v[0].double(), g[0].double(), beta[0].double()
+    o = torch.zeros(T, HV, 128, dtype=torch.float64)
+    hts = []
+    starts = {int(cu[n]): n for n in range(len(cu) - 1) if int(cu[n + 1]) > int(cu[n])}
+    n_of = torch.zeros(T, dtype=torch.long)
+    for n in range(len(cu) - 1):
+        n_of[int(cu[n]):int(cu[n + 1])] = n
+    S = None
+    for t in range(T):
+        if t in starts:
+            S = h0[starts[t]].double().clone()
+        S = S * torch.exp(gf[t])[:, None, :]
+        pred = (S @ kf[t][:, :, None])[..., 0]
+        vn = bf[t][:, None] * (vf[t] - pred)
+        S = S + vn[:, :, None] * kf[t][:, None, :]
+        o[t] = scale * (S @ qf[t][:, :, None])[..., 0]
+        if t + 1 == int(cu[n_of[t] + 1]):
+            hts.append((int(n_of[t]), S.clone()))
+    ht = h0.double().clone()
+    for n, s in hts:
+        ht[n] = s
+    return o[None], ht
+
+
+def test_per_sequence_equals_packed_loop_with_resets():
+    """Varlen by slicing (per_sequence) against one packed token loop with
+    state resets, including an empty sequence and GVA."""
+    cu = torch.tensor([0, 7, 7, 30, 33])
+    T, H, HV = 33, 1, 2
+    gen = torch.Generator().manual_seed(29)
+    q = torch.randn(1, T, H, 128, generator=gen).bfloat16() * 0.08
+    k = torch.randn(1, T, H, 128, generator=gen).bfloat16() * 0.08
+    v = torch.randn(1, T, HV, 128, generator=gen).bfloat16()
+    g = -torch.rand(1, T, HV, 128, generator=gen, dtype=torch.float64) * 0.3
+    beta = torch.rand(1, T, HV, generator=gen, dtype=torch.float64)
+    h0 = torch.randn(4, HV, 128, 128, generator=gen, dtype=torch.float64) * 0.05
+    o_a, ht_a = per_sequence(recurrent_gold, q, k, v, g, beta, cu, 0.1, initial_state=h0,
+                             use_gate=False, gate_log=True, use_l2norm=False,
+                             use_beta_sigmoid=False, dtype=torch.float64)
+    o_b, ht_b = _packed_recurrence(q, k, v, g, beta, cu, h0, 0.1)
+    assert maxdiff(o_a, o_b) < 1e-12 and maxdiff(ht_a, ht_b) < 1e-12
+    assert torch.equal(ht_a[1], h0[1])  # the empty sequence passes its state through

@@ -98,13 +98,39 @@ def test_state_and_gate_parameter_errors():
         kda_bt16_fwd(q, k, v, g, beta, use_gate_in_kernel=True)
 
 
-def test_mha_only():
+def test_grouped_value_heads():
+    """HV a multiple of H is accepted (the reference rejects HV != H,
+    kernels.py:729-730); anything else is refused."""
     q, k, v, g, beta = _inputs()
     v2 = torch.randn(B, T, 2 * H, D, dtype=torch.bfloat16)
     g2 = torch.randn(B, T, 2 * H, D)
     b2 = torch.randn(B, T, 2 * H)
-    with pytest.raises(ValueError, match="prototype targets MHA"):
+    with pytest.raises(ValueError, match="ROCm GPU"):
         kda_bt16_fwd(q, k, v2, g2, b2)
+    v3 = torch.randn(B, T, 3, D, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="HV must be a multiple of H"):
+        kda_bt16_fwd(q, k, v3, torch.randn(B, T, 3, D), torch.randn(B, T, 3))
+
+
+def test_varlen_contract():
+    """cu_seqlens: FLA's varlen convention and messages."""
+    q, k, v, g, beta = _inputs()
+    cu = torch.tensor([0, 5, 32], dtype=torch.int64)
+    with pytest.raises(ValueError, match="ROCm GPU"):
+        kda_bt16_fwd(q, k, v, g, beta, cu_seqlens=cu)
+    with pytest.raises(ValueError, match="ROCm GPU"):
+        kda_bt16_fwd(q, k, v, g, beta, cu_seqlens=cu.int(),
+                     initial_state=torch.zeros(2, H, D, D))
+    with pytest.raises(ValueError, match="The batch size is expected to be 1"):
+        kda_bt16_fwd(*(torch.cat([x, x]) for x in (q, k, v, g, beta)), cu_seqlens=cu)
+    with pytest.raises(ValueError, match="number of initial states"):
+        kda_bt16_fwd(q, k, v, g, beta, cu_seqlens=cu, initial_state=torch.zeros(1, H, D, D))
+    with pytest.raises(TypeError, match="cu_seqlens must be int32 or int64"):
+        kda_bt16_fwd(q, k, v, g, beta, cu_seqlens=cu.float())
+    with pytest.raises(ValueError, match="cu_seqlens must be 1D"):
+        kda_bt16_fwd(q, k, v, g, beta, cu_seqlens=cu[:1])
+    with pytest.raises(ValueError, match="number of initial states"):
+        kda_recurrent_fwd(q, k, v, g, beta, cu_seqlens=cu, initial_state=torch.zeros(3, H, D, D))
 
 
 def test_valid_cpu_inputs_are_refused_before_launch():
