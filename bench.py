@@ -9,7 +9,15 @@ Prints ONE JSON line with the throughput (tokens/s), the roofline of the
 dominant kernel measured with HIP events on the launch stream, and the CPU
 restatement of the reference chunked path timed on this host.
 
-  python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+  python bench.py [--gpus 1] [--steps 200] [--warmup 50] [--no-cpu-baseline]
+
+Two more workloads, each printing its own line in the same format (not the
+headline metric):
+  --workload varlen   the same 8192 tokens and 32 heads as 16 packed
+                      sequences of uneven lengths (cu_seqlens), both stages;
+  --workload decode   one decode step (T = 1, state updated in place) for
+                      B = 128 sequences of 32 heads: the token recurrence,
+                      bound by reading and writing the fp32 states.
 """
 
 from __future__ import annotations
@@ -29,7 +37,7 @@ import torch
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "kda-ascendc_amd"))
 
-from kda_bt16 import kda_bt16_fwd, kda_bt16_stage_launchers  # noqa: E402
+from kda_bt16 import kda_bt16_fwd, kda_bt16_stage_launchers, kda_decode_step  # noqa: E402
 
 METRIC = "KDA fwd tokens/sec and ms at B=1 T=8192 H=32 bf16; % HBM/MFMA roofline"
 B, T, H, D = 1, 8192, 32, 128
@@ -55,19 +63,20 @@ def make_inputs(seed: int = 42):
     return q, k, v, g, beta, A_log, dt_bias
 
 
-def algorithmic_bytes():
+def algorithmic_bytes(n_states: int = B):
     """Algorithmic HBM bytes of one forward, split by the kernel that moves
     them: stage 1 reads q, k, v (2 B), g (2 B), beta (2 B) per token-head
     element plus A_log/dt_bias; stage 2 writes o (2 B) and the fp32 final
-    state.  Total = 1282 B per token-head + states."""
+    state of each of ``n_states`` sequences.  Total = 1282 B per token-head
+    + states."""
     nth = B * T * H
     k1 = nth * (3 * D * 2 + D * 2 + 2) + H * (4 + 4 * D)
-    k2 = nth * D * 2 + B * H * D * D * 4
+    k2 = nth * D * 2 + n_states * H * D * D * 4
     return k1, k2
 
 
-def matmul_flops():
-    nch = B * H * math.ceil(T / 16)
+def matmul_flops(n_chunks: int | None = None):
+    nch = B * H * math.ceil(T / 16) if n_chunks is None else H * n_chunks
     k1 = nch * 4 * (2 * 16 * 16 * D)
     k2 = nch * (3 * (2 * 16 * D * D) + 2 * 16 * 16 * D)
     return k1, k2
@@ -145,15 +154,148 @@ def cpu_baseline(inputs, min_seconds: float = 10.0, max_reps: int = 30) -> dict:
     }
 
 
+VARLEN_N = 16
+
+
+def varlen_offsets(seed: int = 7) -> list[int]:
+    """16 sequences over the 8192 tokens, lengths uneven (16 cut points drawn
+    uniformly, so most lengths are not multiples of 16)."""
+    gen = torch.Generator().manual_seed(seed)
+    cuts = sorted(set(torch.randint(1, T, (VARLEN_N - 1,), generator=gen).tolist()))
+    while len(cuts) < VARLEN_N - 1:  # distinct cut points
+        cuts = sorted(set(cuts + torch.randint(1, T, (1,), generator=gen).tolist()))
+    return [0] + cuts + [T]
+
+
+def _kernel_roofline(k1_ms, k2_ms, wall_ms, by, fl):
+    by1, by2 = by
+    fl1, fl2 = fl
+    kern = {
+        "k1": {"ms": k1_ms, "alg_bytes": by1, "alg_gbs": by1 / k1_ms / 1e6,
+               "tflops": fl1 / k1_ms / 1e9},
+        "k2": {"ms": k2_ms, "alg_bytes": by2, "alg_gbs": by2 / k2_ms / 1e6,
+               "tflops": fl2 / k2_ms / 1e9},
+    }
+    dom = "k1" if k1_ms >= k2_ms else "k2"
+    return kern, dom
+
+
+def run_varlen(args, dev, inputs_cpu) -> dict:
+    q, k, v, g, beta, A_log, dt_bias = (x.to(dev) for x in inputs_cpu)
+    offs = varlen_offsets()
+    cu = torch.tensor(offs, dtype=torch.int64, device=dev)
+    kw = dict(scale=SCALE, output_final_state=True, use_qk_l2norm_in_kernel=True,
+              use_gate_in_kernel=True, use_beta_sigmoid_in_kernel=True,
+              lower_bound=LOWER_BOUND, A_log=A_log, dt_bias=dt_bias)
+
+    def step():
+        return kda_bt16_fwd(q, k, v, g, beta, cu_seqlens=cu, **kw)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    k1, k2, _, _ = kda_bt16_stage_launchers(q, k, v, g, beta, output_final_state=True,
+                                            A_log=A_log, dt_bias=dt_bias,
+                                            lower_bound=LOWER_BOUND, cu_seqlens=cu)
+    k1(); k2()
+    reps = max(args.steps, 10)
+    k1_ms, k2_ms = time_events(k1, reps), time_events(k2, reps)
+    lens = [b - a for a, b in zip(offs[:-1], offs[1:])]
+    n_chunks = sum(math.ceil(n / 16) for n in lens)
+    by = algorithmic_bytes(VARLEN_N)
+    kern, dom = _kernel_roofline(k1_ms, k2_ms, wall_ms, by, matmul_flops(n_chunks))
+    achieved = kern[dom]["alg_gbs"]
+    return {
+        "metric": "KDA varlen fwd tokens/sec, 8192 tokens in 16 packed sequences, H=32 bf16",
+        "value": round(T / (wall_ms / 1e3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"kda_bt16_fwd cu_seqlens, {VARLEN_N} sequences over T={T}, "
+                               f"H={H}, lengths {lens}", "seq_len": T, "heads": H,
+                   "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 2),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None,
+                     "kernels": {n: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
+                                     for kk, vv in d.items()} for n, d in kern.items()}},
+    }
+
+
+DEC_B = 128
+
+
+def run_decode(args, dev) -> dict:
+    """One decode step for DEC_B sequences x H heads, the state updated in
+    place (kda_decode_step).  Algorithmic bytes per (sequence, head): the
+    fp32 state read and written (2 x 64 KiB), q, k, v, o (4 x 256 B), g
+    (512 B fp32), beta (4 B)."""
+    gen = torch.Generator().manual_seed(11)
+    q = torch.randn(DEC_B, 1, H, D, generator=gen).bfloat16().to(dev)
+    k = torch.randn(DEC_B, 1, H, D, generator=gen).bfloat16().to(dev)
+    v = torch.randn(DEC_B, 1, H, D, generator=gen).bfloat16().to(dev)
+    g = torch.randn(DEC_B, 1, H, D, generator=gen).to(dev)
+    beta = torch.randn(DEC_B, 1, H, generator=gen).to(dev)
+    A_log = torch.log(torch.rand(H, generator=gen) * 15.0 + 1.0).to(dev)
+    dt_bias = (torch.randn(H * D, generator=gen) * 0.1).to(dev)
+    state = (torch.randn(DEC_B, H, D, D, generator=gen) * 0.05).to(dev)
+    kw = dict(scale=SCALE, use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True,
+              use_beta_sigmoid_in_kernel=True, lower_bound=LOWER_BOUND, A_log=A_log,
+              dt_bias=dt_bias)
+
+    def step():
+        return kda_decode_step(q, k, v, g, beta, state, **kw)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    ev_ms = time_events(step, max(args.steps, 10))
+    per = 2 * D * D * 4 + 4 * D * 2 + D * 4 + 4
+    alg = DEC_B * H * per
+    achieved = alg / ev_ms / 1e6
+    return {
+        "metric": "KDA decode step tokens/sec, B=128 sequences x H=32, fp32 state in place",
+        "value": round(DEC_B / (wall_ms / 1e3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"kda_decode_step B={DEC_B} T=1 H={H} K=V={D}, V-first fp32 "
+                               "state updated in place, all in-kernel flags",
+                   "global_batch": DEC_B, "seq_len": 1, "heads": H,
+                   "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "kernel": "recurrent", "achieved": round(achieved, 2),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None,
+                     "kernel_ms": round(ev_ms, 5), "alg_bytes": alg},
+    }
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # 200 forwards are ~60 ms of timed work; 50 warmups bring the GPU to its
+    # steady clocks first (20 steps after 5 warmups read ~6% slow).
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 256 MiB device copy (3 launches), the reference "
                          "kernel for scaling rocprof FETCH_SIZE / WRITE_SIZE to bytes")
+    ap.add_argument("--workload", choices=("headline", "varlen", "decode"), default="headline")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the forward shards over (batch, head) with no "
@@ -166,7 +308,20 @@ def main() -> None:
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.copy_calibration:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+    if args.workload == "decode":
+        print(json.dumps(run_decode(args, dev)), flush=True)
+        return
     inputs_cpu = make_inputs()
+    if args.workload == "varlen":
+        print(json.dumps(run_varlen(args, dev, inputs_cpu)), flush=True)
+        return
     q, k, v, g, beta, A_log, dt_bias = (x.to(dev) for x in inputs_cpu)
     kw = dict(scale=SCALE, output_final_state=True, use_qk_l2norm_in_kernel=True,
               use_gate_in_kernel=True, use_beta_sigmoid_in_kernel=True,
@@ -186,7 +341,7 @@ def main() -> None:
     wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
     # per-call latency distribution with HIP events
     lat = []
-    for _ in range(max(args.steps, 5)):
+    for _ in range(min(max(args.steps, 5), 50)):
         lat.append(time_events(step, 1))
     lat.sort()
 
@@ -256,12 +411,6 @@ def main() -> None:
                        "p80": round(lat[(4 * len(lat)) // 5], 4)},
         "roofline": roofline,
     }
-    if args.copy_calibration:
-        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(inputs_cpu)
     print(json.dumps(result), flush=True)

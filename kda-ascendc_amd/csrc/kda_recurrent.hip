@@ -22,6 +22,15 @@
 // Each token's decay, k^ and q^ (128 values each) are formed by every wave
 // for itself (lane l: elements 2l, 2l+1; the l2 norms by a wave-wide
 // butterfly sum) into its own LDS area and read back as broadcasts.
+// A V-first state ([V, K], row v contiguous) is moved between HBM and the
+// lanes' rows through LDS: the work-group reads and writes it with
+// coalesced 16-byte accesses (each wave instruction covers 1 KiB of
+// consecutive memory), and each lane reads or writes its row in LDS, rows
+// padded to 132 floats so that the 16-byte row accesses of 16 consecutive
+// lanes fall in distinct banks.  Read directly, lane v's 16-byte pieces of
+// row v sit 512 bytes apart across the wave and every load instruction
+// touches 64 cache lines.  A K-first state ([K, V]) is already coalesced
+// for this lane-per-row layout (lane v reads S[k][v] for each k).
 // Grouped value heads (GVA): value head hv reads q/k head hv / (HV / H)
 // (kernels.py:88).  Varlen: one work-group per (sequence, value head), over
 // the sequence's tokens, with states [N, HV, ...].
@@ -44,7 +53,10 @@ __device__ __forceinline__ float wave_sum(float x) {
 
 __device__ __forceinline__ float sigmoid_precise(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-__global__ __launch_bounds__(128) void recurrent_kernel(Params p) {
+constexpr int SROW = DK + 4;  // padded LDS row of the state, in floats
+constexpr int NTHREADS = 128;
+
+__global__ __launch_bounds__(NTHREADS) void recurrent_kernel(Params p) {
     const int HV = p.HV, H = p.H;
     const int bhv = blockIdx.x;  // (batch row or sequence) * HV + hv
     const int hv = bhv - (bhv / HV) * HV;
@@ -56,6 +68,8 @@ __global__ __launch_bounds__(128) void recurrent_kernel(Params p) {
 
     // Per wave: [0] decay, [1] k^, [2] q^ of the current token.
     __shared__ __attribute__((aligned(16))) float vec[2][3][DK];
+    // A V-first state on its way in or out.
+    __shared__ __attribute__((aligned(16))) float stage[DK * SROW];
 
     float S[DK];
     const int64_t sbase = (int64_t)bhv * DK * DK;
@@ -63,9 +77,17 @@ __global__ __launch_bounds__(128) void recurrent_kernel(Params p) {
     for (int k = 0; k < DK; ++k) S[k] = 0.0f;
     if (p.h0) {
         if (p.h0_v_first) {
+            // pass i: thread x moves floats 4 * (128 i + x) .. + 3
+#pragma unroll 8
+            for (int i = 0; i < DK * DK / (4 * NTHREADS); ++i) {
+                const int e = 4 * (i * NTHREADS + (int)threadIdx.x);
+                const f32x4 r = *reinterpret_cast<const f32x4*>(p.h0 + sbase + e);
+                *reinterpret_cast<f32x4*>(stage + (e >> 7) * SROW + (e & (DK - 1))) = r;
+            }
+            __syncthreads();
 #pragma unroll
             for (int k = 0; k < DK; k += 4) {
-                const f32x4 r = *reinterpret_cast<const f32x4*>(p.h0 + sbase + (int64_t)vrow * DK + k);
+                const f32x4 r = *reinterpret_cast<const f32x4*>(stage + vrow * SROW + k);
                 S[k] = r[0]; S[k + 1] = r[1]; S[k + 2] = r[2]; S[k + 3] = r[3];
             }
         } else {
@@ -147,10 +169,19 @@ __global__ __launch_bounds__(128) void recurrent_kernel(Params p) {
 
     if (p.ht) {
         if (p.ht_v_first) {
+            // Other lanes may still be reading their rows of a staged h0.
+            __syncthreads();
 #pragma unroll
             for (int k = 0; k < DK; k += 4)
-                *reinterpret_cast<f32x4*>(p.ht + sbase + (int64_t)vrow * DK + k) =
+                *reinterpret_cast<f32x4*>(stage + vrow * SROW + k) =
                     f32x4{S[k], S[k + 1], S[k + 2], S[k + 3]};
+            __syncthreads();
+#pragma unroll 8
+            for (int i = 0; i < DK * DK / (4 * NTHREADS); ++i) {
+                const int e = 4 * (i * NTHREADS + (int)threadIdx.x);
+                *reinterpret_cast<f32x4*>(p.ht + sbase + e) =
+                    *reinterpret_cast<const f32x4*>(stage + (e >> 7) * SROW + (e & (DK - 1)));
+            }
         } else {
 #pragma unroll
             for (int k = 0; k < DK; ++k) p.ht[sbase + (int64_t)k * DK + vrow] = S[k];
@@ -162,7 +193,7 @@ __global__ __launch_bounds__(128) void recurrent_kernel(Params p) {
 
 hipError_t launch_recurrent(const Params& p, hipStream_t stream) {
     const int64_t grid = (int64_t)(p.cu_seqlens ? p.N : p.B) * p.HV;
-    hipLaunchKernelGGL(recurrent_kernel, dim3((unsigned)grid), dim3(128), 0, stream, p);
+    hipLaunchKernelGGL(recurrent_kernel, dim3((unsigned)grid), dim3(NTHREADS), 0, stream, p);
     return hipGetLastError();
 }
 
