@@ -53,7 +53,7 @@
 extern "C" {
 #endif
 
-#define KDA_BT16_ABI_VERSION 2
+#define KDA_BT16_ABI_VERSION 3
 
 /* Flags: the reference's tl.constexpr switches (kernels.py:78-82, 208-212).
  * USE_INITIAL_STATE / STORE_FINAL_STATE / HAS_BIAS / STORE_A_INV follow from
@@ -158,6 +158,39 @@ int kda_bt16_k2_hip(const KdaBt16Args* args, void* stream);
  *     debug pointers must be NULL);
  *   - h0 and ht may be the same buffer (the state updated in place). */
 int kda_recurrent_fwd_hip(const KdaBt16Args* args, void* stream);
+
+/* Backward of the chunked forward (no counterpart in the reference, which is
+ * forward-only, README.md:420; its training graph is FLA's chunk_kda_bwd,
+ * docs/KDA_ANALYSIS.md:134-165).  Gradients of sum(o * dO) + sum(ht * dht)
+ * with respect to every input, for the same arguments as the forward:
+ * recompute (stage 1, stage 2 storing the per-chunk states), the reverse
+ * state-gradient chain, the per-chunk gradients, and the gate-parameter
+ * sums.  Asynchronous on `stream`; allocates nothing. */
+typedef struct KdaBt16BwdArgs {
+    const KdaBt16Args* fwd; /* the forward's arguments: inputs, sizes, flags,
+                               cu_seqlens; its o, ht, workspace and debug
+                               pointers are ignored (debug must be NULL) */
+    const void* dout;       /* dO [B, T, HV, 128] bf16, required */
+    const float* dht;       /* optional gradient of ht (state layout of the flags) */
+    void* dq;               /* [B, T, H, 128] bf16, required */
+    void* dk;               /* [B, T, H, 128] bf16, required */
+    void* dv;               /* [B, T, HV, 128] bf16, required */
+    void* dg;               /* shape and element type of g, required */
+    void* dbeta;            /* shape and element type of beta, required */
+    float* dA_log;          /* optional [HV]; only with USE_GATE */
+    float* ddt_bias;        /* optional [HV * 128]; only with USE_GATE and dt_bias */
+    float* dh0;             /* optional gradient of the initial state (its layout) */
+    void* workspace;        /* kda_bt16_bwd_workspace_bytes() bytes, 256-byte aligned */
+    size_t workspace_bytes;
+} KdaBt16BwdArgs;
+
+/* Workspace of kda_bt16_bwd_hip: per 16-token record slot, the 17 KiB
+ * record, bf16 h and dh (32 KiB each), v_new and dv_new (4 KiB each) and the
+ * gate partial sums (528 B): ~89.5 KiB (1.43 GiB at B=1 T=8192 H=32).
+ * Returns 0 for an unsupported geometry. */
+size_t kda_bt16_bwd_workspace_bytes(const KdaBt16Args* fwd);
+
+int kda_bt16_bwd_hip(const KdaBt16BwdArgs* args, void* stream);
 
 /* Static message for an error code. */
 const char* kda_bt16_strerror(int code);

@@ -141,6 +141,38 @@ int to_params_recurrent(const KdaBt16Args* a, Params& p) {
     return KDA_BT16_OK;
 }
 
+// Record slots of a geometry (every value head): B * HV * NT, or HV * NS.
+int64_t record_slots(const KdaBt16Args* a) {
+    return a->cu_seqlens ? (int64_t)a->HV * varlen_slots(a)
+                         : (int64_t)a->B * a->HV * chunks_of(a->T);
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Backward workspace regions, in order.
+struct BwdLayout {
+    size_t rec, h, vn, dh, dvn, part, total;
+};
+
+BwdLayout bwd_layout(int64_t R) {
+    BwdLayout L;
+    size_t off = 0;
+    L.rec = off;
+    off = align256(off + (size_t)R * kda::REC_BYTES);
+    L.h = off;
+    off = align256(off + (size_t)R * kda::TR_H_ELEMS * 2);
+    L.vn = off;
+    off = align256(off + (size_t)R * kda::TR_VN_ELEMS * 2);
+    L.dh = off;
+    off = align256(off + (size_t)R * kda::TR_H_ELEMS * 2);
+    L.dvn = off;
+    off = align256(off + (size_t)R * kda::TR_VN_ELEMS * 2);
+    L.part = off;
+    off = align256(off + (size_t)R * kda::PART_STRIDE * 4);
+    L.total = off;
+    return L;
+}
+
 }  // namespace
 
 extern "C" {
@@ -189,6 +221,69 @@ int kda_recurrent_fwd_hip(const KdaBt16Args* args, void* stream) {
     if (rc != KDA_BT16_OK) return rc;
     if (kda::launch_recurrent(p, static_cast<hipStream_t>(stream)) != hipSuccess)
         return KDA_BT16_ELAUNCH;
+    return KDA_BT16_OK;
+}
+
+size_t kda_bt16_bwd_workspace_bytes(const KdaBt16Args* a) {
+    if (kda_bt16_workspace_bytes_args(a) == 0) return 0;
+    return bwd_layout(record_slots(a)).total;
+}
+
+int kda_bt16_bwd_hip(const KdaBt16BwdArgs* b, void* stream) {
+    if (b == nullptr || b->fwd == nullptr) return KDA_BT16_EINVAL;
+    const KdaBt16Args* a = b->fwd;
+    Params p;
+    int rc = check_common(a, p);
+    if (rc != KDA_BT16_OK) return rc;
+    if (a->flags & KDA_BT16_O_FP32) return KDA_BT16_EUNSUPPORTED;
+    const int64_t slots = a->cu_seqlens ? varlen_slots(a) : (int64_t)a->B * chunks_of(a->T);
+    if ((int64_t)a->HV * slots > I32_MAX || sequences(a) * a->HV * 8 > I32_MAX ||
+        chunks_of(a->T) * kda::REC_BYTES > I32_MAX)
+        return KDA_BT16_EUNSUPPORTED;
+    p.NS = a->cu_seqlens ? (int)varlen_slots(a) : 0;
+    if (!a->q || !a->k || !a->v || !a->g || !a->beta) return KDA_BT16_EINVAL;
+    if (p.use_gate && !a->A_log) return KDA_BT16_EINVAL;
+    if (a->dbg_Aqk || a->dbg_A_inv || a->dbg_w || a->dbg_u || a->dbg_g) return KDA_BT16_EINVAL;
+    if (!b->dout || !b->dq || !b->dk || !b->dv || !b->dg || !b->dbeta) return KDA_BT16_EINVAL;
+    if ((b->dA_log || b->ddt_bias) && !p.use_gate) return KDA_BT16_EINVAL;
+    if (b->ddt_bias && !a->dt_bias) return KDA_BT16_EINVAL;
+    const uintptr_t bsz = a->beta_dtype == KDA_BT16_DTYPE_BF16 ? 2 : 4;
+    if (misaligned(a->q, 16) || misaligned(a->k, 16) || misaligned(a->v, 16) ||
+        misaligned(a->g, 16) || misaligned(a->beta, bsz) || misaligned(a->dt_bias, 16) ||
+        misaligned(a->h0, 16) || misaligned(b->dout, 16) || misaligned(b->dht, 16) ||
+        misaligned(b->dq, 16) || misaligned(b->dk, 16) || misaligned(b->dv, 16) ||
+        misaligned(b->dg, 16) || misaligned(b->dbeta, bsz) || misaligned(b->dh0, 16) ||
+        misaligned(b->dA_log, 4) || misaligned(b->ddt_bias, 4))
+        return KDA_BT16_EINVAL;
+    const BwdLayout L = bwd_layout(record_slots(a));
+    if (!b->workspace || b->workspace_bytes < L.total) return KDA_BT16_EWORKSPACE;
+    if ((reinterpret_cast<uintptr_t>(b->workspace) & 255u) != 0) return KDA_BT16_EWORKSPACE;
+    uint8_t* ws = static_cast<uint8_t*>(b->workspace);
+    p.ws = ws + L.rec;
+    p.tr_h = reinterpret_cast<uint16_t*>(ws + L.h);
+    p.tr_vn = reinterpret_cast<uint16_t*>(ws + L.vn);
+    p.tr_dh = reinterpret_cast<uint16_t*>(ws + L.dh);
+    p.tr_dvn = reinterpret_cast<uint16_t*>(ws + L.dvn);
+    p.tr_part = (b->dA_log || b->ddt_bias) ? reinterpret_cast<float*>(ws + L.part) : nullptr;
+    p.o = nullptr;
+    p.ht = nullptr;
+    p.dout = static_cast<const uint16_t*>(b->dout);
+    p.dht = b->dht;
+    p.dq = static_cast<uint16_t*>(b->dq);
+    p.dk = static_cast<uint16_t*>(b->dk);
+    p.dv = static_cast<uint16_t*>(b->dv);
+    p.dg = b->dg;
+    p.dbeta = b->dbeta;
+    p.dA_log = b->dA_log;
+    p.ddt_bias = b->ddt_bias;
+    p.dh0 = b->dh0;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (kda::launch_k1(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
+    if (kda::launch_k2_train(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
+    if (kda::launch_k1_bwd_records(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
+    if (kda::launch_bwd_state(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
+    if (kda::launch_bwd_chunk(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
+    if (p.tr_part && kda::launch_bwd_gate_reduce(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
     return KDA_BT16_OK;
 }
 

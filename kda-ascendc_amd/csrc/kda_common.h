@@ -49,6 +49,33 @@ constexpr int REC_U = 13312;
 constexpr int REC_SHARED = 13312;  // bytes every value tile reads
 constexpr int REC_BYTES = 17408;
 
+// Backward record (kda_bt16_bwd_hip): what the reverse state chain feeds
+// its matrix cores, written by stage 1 in place of the forward record once
+// the recompute has consumed that.  Same slot indexing.
+//   offset  bytes  content
+//   0       4096   kg     bf16, F order, [j][lane][8] (k-tiles 2j, 2j+1):
+//                         the A operand of dv_new += kg @ dh
+//   4096    8192   upd    bf16, [kt][lane][8]: items 0..3 = scale*qg[4*q4+i][16*kt+r]
+//                         (bf16(scale * q^ * 2^G)), items 4..7 = -w[4*q4+i][16*kt+r]:
+//                         the A operand of dh[kt] += [scale*qg | -w]^T @ [dO ; dv_new]
+//   12288   512    AqkT   bf16, [lane][i] = Aqk[4*q4+i][r]: the A operand of Aqk^T @ dO
+//   12800   512    decay  fp32, as REC_DECAY
+constexpr int BREC_KG = 0;
+constexpr int BREC_UPD = 4096;
+constexpr int BREC_AQKT = 12288;
+constexpr int BREC_DECAY = 12800;
+constexpr int BREC_BYTES = 13312;
+static_assert(BREC_BYTES <= REC_BYTES && BREC_DECAY == REC_DECAY, "backward record fits a slot");
+
+// Training buffers per record slot (bf16, natural row-major layouts):
+// the state at the chunk's start h = bf16(S)^T [K][V], v_new [16][V], the
+// gradient of the state after the chunk dh [K][V] and dv_new [16][V]; and
+// per-chunk partial sums of the gate-parameter gradients: ddt_bias[128] then
+// dA_log at index 128.
+constexpr int TR_H_ELEMS = DK * DK;
+constexpr int TR_VN_ELEMS = BT * DK;
+constexpr int PART_STRIDE = 132;
+
 // RCP_LN2 and the l2norm epsilon, kernels.py:38-39.
 constexpr float RCP_LN2 = 1.4426950216f;
 constexpr float L2_EPS = 1e-6f;
@@ -92,6 +119,27 @@ struct Params {
     const void* cu_seqlens;
     int cu_i64;
     int N, NS;
+    // Backward only (kda_bt16_bwd_hip).  Training buffers indexed by record
+    // slot (layouts above), the incoming gradients dO [B,T,HV,V] bf16 and
+    // dht (state layout of ht, optional), and the outputs: dq, dk, dv bf16 in
+    // the shapes of q, k, v; dg and dbeta in the element types of g and beta;
+    // dA_log [HV], ddt_bias [HV*128] and dh0 (state layout of h0), each
+    // optional as its input is.
+    uint16_t* tr_h;
+    uint16_t* tr_vn;
+    uint16_t* tr_dh;
+    uint16_t* tr_dvn;
+    float* tr_part;
+    const uint16_t* dout;
+    const float* dht;
+    uint16_t* dq;
+    uint16_t* dk;
+    uint16_t* dv;
+    void* dg;
+    void* dbeta;
+    float* dA_log;
+    float* ddt_bias;
+    float* dh0;
 };
 
 // Bounds of sequence n of a varlen batch, clamped into [0, T] so that a
@@ -129,6 +177,26 @@ __device__ __forceinline__ SeqSpan seq_span(const Params& p, int bh) {
         s.rec0 = (int64_t)bh * p.NT;
     }
     return s;
+}
+
+// Varlen: the sequence n whose record slots hold slot x, i.e. the largest n
+// with floor(cu_seqlens[n] / 16) + n <= x (strictly increasing in n for a
+// non-decreasing cu_seqlens).  A 64-way search: each round every lane tests
+// one candidate and the ballot's population count is the number of
+// candidates at or below x.  Any cu_seqlens gives an n in [0, N).
+__device__ __forceinline__ int find_sequence(const Params& p, int x, int lane) {
+    int lo = 0, cnt = p.N;
+    while (cnt > 1) {
+        const int step = (cnt + 63) >> 6;
+        const int idx = lo + lane * step;
+        const bool below = idx < lo + cnt && cu_at(p, idx) / BT + idx <= x;
+        const int m = __popcll(__ballot(below));
+        if (m == 0) break;
+        const int next = lo + (m - 1) * step;
+        cnt = min(step, lo + cnt - next);
+        lo = next;
+    }
+    return lo;
 }
 
 // bf16 <-> fp32.  fp32 -> bf16 rounds to nearest even (the hardware
@@ -198,6 +266,37 @@ __device__ __forceinline__ f32x4 mfma_bf16_16x16x32(bf16x8 a, bf16x8 b, f32x4 c)
 }
 
 __device__ __forceinline__ i16x4 as_i16x4(u32x2 v) { return __builtin_bit_cast(i16x4, v); }
+
+// 4x4 transpose of 16-bit values across the 4 lanes of a quad.  Lane j
+// enters with p0 = (M[0][j], M[1][j]) and p1 = (M[2][j], M[3][j]) and leaves
+// with (M[j][0], M[j][1]) and (M[j][2], M[j][3]).  Two DPP exchanges:
+// lanes j and j^2 swap the 2x2 blocks off the diagonal, then lanes j and
+// j^1 swap 16-bit halves.  Applied to a 16x16 accumulator tile (lane
+// (x, q4) holding rows 4*q4 .. +3 of column x), it leaves lane (x, q4) with
+// row 4*q4 + x%4, columns 4*(x/4) .. +3: one 8-byte row-major store per
+// lane.  Applied to such row pieces, it gives back the tile layout.
+__device__ __forceinline__ u32x2 quad_transpose(uint32_t p0, uint32_t p1, int j) {
+    constexpr int QP_XOR2 = 2 | (3 << 2) | (0 << 4) | (1 << 6);  // quad_perm [2,3,0,1]
+    constexpr int QP_XOR1 = 1 | (0 << 2) | (3 << 4) | (2 << 6);  // quad_perm [1,0,3,2]
+    const bool lo2 = (j & 2) == 0;
+    // after this, the lane holds rows {r, r+1} (r = 0 for j < 2, else 2)
+    // for columns {j & 1, (j & 1) + 2} as (a: column j&1, b: column (j&1)+2)
+    const uint32_t send2 = lo2 ? p1 : p0;
+    const uint32_t recv2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)send2, QP_XOR2, 0xf, 0xf, false);
+    const uint32_t a = lo2 ? p0 : recv2;
+    const uint32_t bb = lo2 ? recv2 : p1;
+    // lane with j even keeps the low halves (its row), sends the high halves
+    const bool even = (j & 1) == 0;
+    const uint32_t send1 = even ? __builtin_amdgcn_perm(bb, a, 0x07060302u)   // (a.hi, b.hi)
+                                : __builtin_amdgcn_perm(bb, a, 0x05040100u);  // (a.lo, b.lo)
+    const uint32_t recv1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)send1, QP_XOR1, 0xf, 0xf, false);
+    // even lane: (a.lo, recv.lo), (b.lo, recv.hi); odd lane: (recv.lo, a.hi), (recv.hi, b.hi)
+    const uint32_t w0 = even ? __builtin_amdgcn_perm(recv1, a, 0x05040100u)
+                             : __builtin_amdgcn_perm(a, recv1, 0x07060100u);
+    const uint32_t w1 = even ? __builtin_amdgcn_perm(recv1, bb, 0x07060100u)
+                             : __builtin_amdgcn_perm(bb, recv1, 0x07060302u);
+    return u32x2{w0, w1};
+}
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 }  // namespace kda
@@ -207,4 +306,10 @@ namespace kda {
 hipError_t launch_k1(const Params& p, hipStream_t stream);
 hipError_t launch_k2(const Params& p, hipStream_t stream);
 hipError_t launch_recurrent(const Params& p, hipStream_t stream);
+// Backward (kda_bt16_bwd.hip, and the training variants of the stages).
+hipError_t launch_k1_bwd_records(const Params& p, hipStream_t stream);
+hipError_t launch_k2_train(const Params& p, hipStream_t stream);
+hipError_t launch_bwd_state(const Params& p, hipStream_t stream);
+hipError_t launch_bwd_chunk(const Params& p, hipStream_t stream);
+hipError_t launch_bwd_gate_reduce(const Params& p, hipStream_t stream);
 }  // namespace kda

@@ -71,26 +71,10 @@ __device__ __forceinline__ u32x2 pack4(f32x4 v) { return pack4(v.x, v.y, v.z, v.
 // Three waves per SIMD (at most 168 VGPRs; the compiler spills two 8-byte
 // values): each wave spends most of its life waiting on its loads, and a
 // third wave per SIMD hides more of that than the two that 172 VGPRs allow.
-// Varlen: the sequence n whose record slots hold slot x, i.e. the largest n
-// with floor(cu_seqlens[n] / 16) + n <= x (strictly increasing in n for a
-// non-decreasing cu_seqlens).  A 64-way search: each round every lane tests
-// one candidate and the ballot's population count is the number of
-// candidates at or below x.  Any cu_seqlens gives an n in [0, N).
-__device__ __forceinline__ int find_sequence(const Params& p, int x, int lane) {
-    int lo = 0, cnt = p.N;
-    while (cnt > 1) {
-        const int step = (cnt + 63) >> 6;
-        const int idx = lo + lane * step;
-        const bool below = idx < lo + cnt && cu_at(p, idx) / BT + idx <= x;
-        const int m = __popcll(__ballot(below));
-        if (m == 0) break;
-        const int next = lo + (m - 1) * step;
-        cnt = min(step, lo + cnt - next);
-        lo = next;
-    }
-    return lo;
-}
-
+//
+// BWD = true writes the backward record (kda_common.h) instead: the same
+// chunk quantities in the operand orders of the reverse state chain.
+template <bool BWD>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k1_kernel(Params p) {
     __shared__ __attribute__((aligned(16))) uint16_t s_T[BT * LROW];  // transpose tile
     __shared__ __attribute__((aligned(16))) float s_L[BT * BT];
@@ -232,7 +216,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k1
         L[i] = (r > s) ? acc_kk[i] * beta : 0.f;
     }
     const u32x2 aqk_bf = pack4(aqk);
-    __builtin_nontemporal_store(aqk_bf, reinterpret_cast<u32x2*>(rec + REC_AQK + lane * 8));
+    if constexpr (!BWD)
+        __builtin_nontemporal_store(aqk_bf, reinterpret_cast<u32x2*>(rec + REC_AQK + lane * 8));
 
     // ---- (I + L)^-1 by forward substitution (kernels.py:157-167) ---------
     // Lane r solves column s = r: a[t] = A_inv[t][s], with a[s] = 1,
@@ -265,6 +250,86 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k1
     for (int i = 0; i < 4; ++i) ainv[i] = s_X[(4 * q4 + i) * (BT + 1) + r];
     const u32x2 ainv_bf = pack4(ainv);  // A = bf16(A_inv), kernels.py:170
     const i16x4 A_op = as_i16x4(ainv_bf);
+    const i16x4 A_neg = as_i16x4(ainv_bf ^ 0x80008000u);
+
+    if constexpr (BWD) {
+        // ---- backward record ---------------------------------------------
+        // Aqk^T as an A operand: lane (r, q4) takes Aqk[4*q4 + i][r], the
+        // transpose of what it holds, through s_L (free after the solve).
+        *reinterpret_cast<f32x4*>(s_L + r * BT + 4 * q4) = aqk;
+        __syncthreads();
+        {
+            f32x4 at;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) at[i] = s_L[(4 * q4 + i) * BT + r];
+            __builtin_nontemporal_store(pack4(at),
+                                        reinterpret_cast<u32x2*>(rec + BREC_AQKT + lane * 8));
+        }
+        // -w in T order straight from the matrix cores: (-A) @ kb tile kt
+        // lands as -w[4*q4 + i][16*kt + r].  bf16(scale * q^ * 2^G) goes
+        // through the LDS tile to T order.
+        u32x2 wT[8], qsF[8];
+#pragma unroll
+        for (int kt = 0; kt < 8; ++kt) {
+            float kb[4], qs[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float e = fast_exp2(G[4 * kt + i]);
+                kb[i] = round_bf(elem(kp, 4 * kt + i) * beta) * e;
+                qs[i] = p.scale * (elem(qp, 4 * kt + i) * e);
+            }
+            lds_put(s_T, r, colbase, kt, pack4(kb[0], kb[1], kb[2], kb[3]));
+            qsF[kt] = pack4(qs[0], qs[1], qs[2], qs[3]);
+        }
+        __syncthreads();
+        {
+            i16x4 kbT[8];
+            load_lds_T(s_T, r, q4, kbT);
+#pragma unroll
+            for (int kt = 0; kt < 8; ++kt) {
+                const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+                wT[kt] = pack4(mfma_bf16_16x16x16(A_neg, kbT[kt], zero));
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kt = 0; kt < 8; ++kt) lds_put(s_T, r, colbase, kt, qsF[kt]);
+        __syncthreads();
+        {
+            i16x4 qsT[8];
+            load_lds_T(s_T, r, q4, qsT);
+#pragma unroll
+            for (int kt = 0; kt < 8; ++kt) {
+                const u32x2 qv = __builtin_bit_cast(u32x2, qsT[kt]);
+                __builtin_nontemporal_store(
+                    u32x4{qv.x, qv.y, wT[kt].x, wT[kt].y},
+                    reinterpret_cast<u32x4*>(rec + BREC_UPD + kt * 1024 + lane * 16));
+            }
+        }
+        // kg = bf16(k^ * 2^(G_last - G)) in F order (the A operand of
+        // kg @ dh), and the decay 2^G_last.
+        u32x2 kgF[8];
+#pragma unroll
+        for (int kt = 0; kt < 8; ++kt) {
+            float kg[4], gl[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                gl[i] = shfl(G[4 * kt + i], row0 | last);
+                kg[i] = elem(kp, 4 * kt + i) * fast_exp2(gl[i] - G[4 * kt + i]);
+            }
+            kgF[kt] = pack4(kg[0], kg[1], kg[2], kg[3]);
+            if (r == 0)
+                __builtin_nontemporal_store(
+                    f32x4{fast_exp2(gl[0]), fast_exp2(gl[1]), fast_exp2(gl[2]), fast_exp2(gl[3])},
+                    reinterpret_cast<f32x4*>(rec + BREC_DECAY + kt * 64 + q4 * 16));
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            __builtin_nontemporal_store(
+                u32x4{kgF[2 * j].x, kgF[2 * j].y, kgF[2 * j + 1].x, kgF[2 * j + 1].y},
+                reinterpret_cast<u32x4*>(rec + BREC_KG + j * 1024 + lane * 16));
+        return;
+    }
 
     // ---- u = A @ bf16(v * beta) (kernels.py:173-174) ----------------------
     // One 16x16x16 tile per 16 value columns; u lands as
@@ -330,7 +395,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k1
     {
         i16x4 kbT[8];
         load_lds_T(s_T, r, q4, kbT);
-        const i16x4 A_neg = as_i16x4(ainv_bf ^ 0x80008000u);
 #pragma unroll
         for (int kt = 0; kt < 8; ++kt) {
             const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
@@ -392,7 +456,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k1
 
 hipError_t launch_k1(const Params& p, hipStream_t stream) {
     const int64_t grid = p.cu_seqlens ? (int64_t)p.HV * p.NS : (int64_t)p.B * p.HV * p.NT;
-    hipLaunchKernelGGL(k1_kernel, dim3((unsigned)grid), dim3(64), 0, stream, p);
+    hipLaunchKernelGGL(k1_kernel<false>, dim3((unsigned)grid), dim3(64), 0, stream, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_k1_bwd_records(const Params& p, hipStream_t stream) {
+    const int64_t grid = p.cu_seqlens ? (int64_t)p.HV * p.NS : (int64_t)p.B * p.HV * p.NT;
+    hipLaunchKernelGGL(k1_kernel<true>, dim3((unsigned)grid), dim3(64), 0, stream, p);
     return hipGetLastError();
 }
 

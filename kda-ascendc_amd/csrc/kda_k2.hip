@@ -192,34 +192,6 @@ __device__ __forceinline__ void chunk_barrier_nodrain() {
 // wait for its loads in flight.
 __device__ __forceinline__ void copy_barrier() { asm volatile("s_barrier"); }
 
-// 4x4 transpose of 16-bit values across the 4 lanes of a quad.  Lane j
-// enters with p0 = (M[0][j], M[1][j]) and p1 = (M[2][j], M[3][j]) and leaves
-// with (M[j][0], M[j][1]) and (M[j][2], M[j][3]).  Two DPP exchanges:
-// lanes j and j^2 swap the 2x2 blocks off the diagonal, then lanes j and
-// j^1 swap 16-bit halves.
-__device__ __forceinline__ u32x2 quad_transpose(uint32_t p0, uint32_t p1, int j) {
-    constexpr int QP_XOR2 = 2 | (3 << 2) | (0 << 4) | (1 << 6);  // quad_perm [2,3,0,1]
-    constexpr int QP_XOR1 = 1 | (0 << 2) | (3 << 4) | (2 << 6);  // quad_perm [1,0,3,2]
-    const bool lo2 = (j & 2) == 0;
-    // after this, the lane holds rows {r, r+1} (r = 0 for j < 2, else 2)
-    // for columns {j & 1, (j & 1) + 2} as (a: column j&1, b: column (j&1)+2)
-    const uint32_t send2 = lo2 ? p1 : p0;
-    const uint32_t recv2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)send2, QP_XOR2, 0xf, 0xf, false);
-    const uint32_t a = lo2 ? p0 : recv2;
-    const uint32_t bb = lo2 ? recv2 : p1;
-    // lane with j even keeps the low halves (its row), sends the high halves
-    const bool even = (j & 1) == 0;
-    const uint32_t send1 = even ? __builtin_amdgcn_perm(bb, a, 0x07060302u)   // (a.hi, b.hi)
-                                : __builtin_amdgcn_perm(bb, a, 0x05040100u);  // (a.lo, b.lo)
-    const uint32_t recv1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)send1, QP_XOR1, 0xf, 0xf, false);
-    // even lane: (a.lo, recv.lo), (b.lo, recv.hi); odd lane: (recv.lo, a.hi), (recv.hi, b.hi)
-    const uint32_t w0 = even ? __builtin_amdgcn_perm(recv1, a, 0x05040100u)
-                             : __builtin_amdgcn_perm(a, recv1, 0x07060100u);
-    const uint32_t w1 = even ? __builtin_amdgcn_perm(recv1, bb, 0x07060100u)
-                             : __builtin_amdgcn_perm(bb, recv1, 0x07060302u);
-    return u32x2{w0, w1};
-}
-
 // Constants of the chunk loop.
 struct Ctx {
     __amdgpu_buffer_rsrc_t rs;  // copy: this sequence-head's records, NT * REC_BYTES bytes
@@ -227,6 +199,8 @@ struct Ctx {
     uint32_t u_off;             // copy: REC_U + 1024 * (vt / 2)
     uint16_t* obase;            // output: o[first token, hv, 16*vt + 4*((lane%16)/4)]
     int64_t orow_stride;        // output: elements between consecutive tokens of o
+    uint16_t* trh;              // training: h of the first record, column 16*vt + 4*((lane%16)/4)
+    uint16_t* trvn;             // training: v_new of the first record, same column
     float scale;
     int NT, T, lane, q4, vt;    // NT chunks over T tokens (this sequence's)
 };
@@ -368,10 +342,31 @@ __device__ __forceinline__ void state_step(const Ctx& cx, f32x4 (&St)[8], StateO
 
 // Output wave, chunk c (slot S) after the barrier that ends chunk c + 1:
 // o = scale * qg @ hc^T + Aqk @ v_new (kernels.py:268-279).
-template <int S>
+// TRAIN: instead of o, store the chunk's hc = bf16(S) as h = hc^T [K][V]
+// and v_new [16][V] (the backward's training buffers), each 16x16 tile
+// quad-transposed to one 8-byte row piece per lane.
+template <int S, bool TRAIN>
 __device__ __forceinline__ void output_step(const Ctx& cx, int c) {
     chunk_barrier();
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (TRAIN) {
+        const int j4 = cx.lane & 3;
+        uint16_t* hrec = cx.trh + (int64_t)c * TR_H_ELEMS;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const u32x4 hc = *reinterpret_cast<const u32x4*>(hc_buf[S % HANDOFF] + j * 1024 + cx.lane * 16);
+            const u32x2 t0 = quad_transpose(hc.x, hc.y, j4);
+            const u32x2 t1 = quad_transpose(hc.z, hc.w, j4);
+            const int k0 = 32 * j + 4 * cx.q4 + j4;  // row of k-tile 2j
+            __builtin_nontemporal_store(t0, reinterpret_cast<u32x2*>(hrec + (int64_t)k0 * DK));
+            __builtin_nontemporal_store(t1, reinterpret_cast<u32x2*>(hrec + (int64_t)(k0 + 16) * DK));
+        }
+        const u32x2 vn = *reinterpret_cast<const u32x2*>(vn_buf[S % HANDOFF] + cx.lane * 8);
+        const u32x2 vt = quad_transpose(vn.x, vn.y, j4);
+        __builtin_nontemporal_store(
+            vt, reinterpret_cast<u32x2*>(cx.trvn + (int64_t)c * TR_VN_ELEMS + (4 * cx.q4 + j4) * DK));
+        return;
+    }
     const uint8_t* slot = ring + S * SLOT;
     u32x4 hc[4], qg[4];
 #pragma unroll
@@ -436,11 +431,11 @@ __device__ __forceinline__ void state_round_tail(const Ctx& cx, int c, f32x4 (&S
     if constexpr (N > 1) state_round_tail<(S + 1) % RING, N - 1>(cx, c + 1, St, op, vn);
 }
 
-template <int S>
+template <int S, bool TRAIN>
 __device__ __forceinline__ void output_round(const Ctx& cx, int c) {
-    output_step<S>(cx, c);
+    output_step<S, TRAIN>(cx, c);
     if constexpr (S + 1 < RING) {
-        if (c + 1 < cx.NT) output_round<S + 1>(cx, c + 1);
+        if (c + 1 < cx.NT) output_round<S + 1, TRAIN>(cx, c + 1);
     }
 }
 
@@ -470,13 +465,20 @@ __device__ __forceinline__ void copy_wave(const Params& p, Ctx& cx, const SeqSpa
     copy_barrier();  // the output wave's last chunk
 }
 
+template <bool TRAIN>
 __device__ __forceinline__ void output_wave(const Params& p, Ctx& cx, const SeqSpan& sp, int hv) {
     const int x = cx.lane & 15;
-    cx.obase = p.o + (sp.tok0 * p.HV + hv) * DK + 16 * cx.vt + 4 * (x >> 2);
-    cx.orow_stride = (int64_t)p.HV * DK;
+    const int col = 16 * cx.vt + 4 * (x >> 2);
+    if constexpr (TRAIN) {
+        cx.trh = p.tr_h + sp.rec0 * TR_H_ELEMS + col;
+        cx.trvn = p.tr_vn + sp.rec0 * TR_VN_ELEMS + col;
+    } else {
+        cx.obase = p.o + (sp.tok0 * p.HV + hv) * DK + col;
+        cx.orow_stride = (int64_t)p.HV * DK;
+    }
     chunk_barrier();
     chunk_barrier();
-    for (int c = 0; c < cx.NT; c += RING) output_round<0>(cx, c);
+    for (int c = 0; c < cx.NT; c += RING) output_round<0, TRAIN>(cx, c);
 }
 
 // S^T tiles of this lane: St[kt][i] = S[v][16*kt + 4*q4 + i], v = 16*vt + lane%16.
@@ -543,6 +545,10 @@ enum Role { STATE = 0, OUTPUT = 1, COPY = 2 };
 // two chunks behind the state wave).  Each role ends its wave itself: with no join of
 // the roles' code paths, the compiler's wait analysis of one role never
 // sees another role's memory operations.
+//
+// TRAIN: the recompute of the backward; the output wave stores the
+// training buffers instead of o (output_step).
+template <bool TRAIN>
 __global__ __launch_bounds__(192) void k2_kernel(Params p) {
     const int lane = threadIdx.x & 63;
     const int role = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -581,7 +587,7 @@ __global__ __launch_bounds__(192) void k2_kernel(Params p) {
         __builtin_amdgcn_endpgm();
     }
     if (role == OUTPUT) {
-        output_wave(p, cx, sp, hv);
+        output_wave<TRAIN>(p, cx, sp, hv);
         __builtin_amdgcn_endpgm();
     }
     copy_wave(p, cx, sp);
@@ -592,7 +598,13 @@ __global__ __launch_bounds__(192) void k2_kernel(Params p) {
 
 hipError_t launch_k2(const Params& p, hipStream_t stream) {
     const int64_t grid = (int64_t)(p.cu_seqlens ? p.N : p.B) * p.HV * 8;
-    hipLaunchKernelGGL(k2_kernel, dim3((unsigned)grid), dim3(192), 0, stream, p);
+    hipLaunchKernelGGL(k2_kernel<false>, dim3((unsigned)grid), dim3(192), 0, stream, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_k2_train(const Params& p, hipStream_t stream) {
+    const int64_t grid = (int64_t)(p.cu_seqlens ? p.N : p.B) * p.HV * 8;
+    hipLaunchKernelGGL(k2_kernel<true>, dim3((unsigned)grid), dim3(192), 0, stream, p);
     return hipGetLastError();
 }
 

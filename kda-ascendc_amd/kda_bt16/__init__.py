@@ -6,7 +6,8 @@ Triton kernels the reference also exports are replaced by
 ``kda_bt16_stage_launchers`` (stage-1 / stage-2 launch closures over the
 HIP library); ``kda_bt16_kernel_fused`` raises NotImplementedError.
 
-Beyond the reference: ``kda_recurrent_fwd`` (token-by-token recurrence in
+Beyond the reference: the backward (``kda_bt16_bwd``, and autograd through
+``kda_bt16_fwd`` / ``chunk_kda``); ``kda_recurrent_fwd`` (token-by-token recurrence in
 fp32, the decode step and an on-GPU gold) and ``kda_decode_step``; FLA's
 ``chunk_kda`` / ``fused_recurrent_kda`` calling convention (``kda_bt16.fla``)
 and a per-function backend dispatch that registers these kernels
@@ -16,6 +17,7 @@ and a per-function backend dispatch that registers these kernels
 from . import dispatch
 from .fla import chunk_kda, fused_recurrent_kda
 from .kernels import (
+    kda_bt16_bwd,
     kda_bt16_debug,
     kda_bt16_fwd,
     kda_bt16_kernel_fused,
@@ -26,6 +28,7 @@ from .kernels import (
 
 __all__ = [
     "kda_bt16_fwd",
+    "kda_bt16_bwd",
     "kda_bt16_debug",
     "kda_bt16_kernel_fused",
     "kda_bt16_stage_launchers",

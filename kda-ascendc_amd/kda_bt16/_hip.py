@@ -12,7 +12,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libkda_bt16_hip.so"
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 USE_GATE = 1 << 0
 USE_QK_L2NORM = 1 << 1
@@ -33,6 +33,8 @@ EXPORTED_SYMBOLS = (
     "kda_bt16_k1_hip",
     "kda_bt16_k2_hip",
     "kda_recurrent_fwd_hip",
+    "kda_bt16_bwd_workspace_bytes",
+    "kda_bt16_bwd_hip",
     "kda_bt16_strerror",
     "kda_bt16_abi_version",
 )
@@ -77,6 +79,26 @@ class KdaBt16Args(ctypes.Structure):
     ]
 
 
+class KdaBt16BwdArgs(ctypes.Structure):
+    """Mirror of ``struct KdaBt16BwdArgs``."""
+
+    _fields_ = [
+        ("fwd", ctypes.POINTER(KdaBt16Args)),
+        ("dout", ctypes.c_void_p),
+        ("dht", ctypes.c_void_p),
+        ("dq", ctypes.c_void_p),
+        ("dk", ctypes.c_void_p),
+        ("dv", ctypes.c_void_p),
+        ("dg", ctypes.c_void_p),
+        ("dbeta", ctypes.c_void_p),
+        ("dA_log", ctypes.c_void_p),
+        ("ddt_bias", ctypes.c_void_p),
+        ("dh0", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
 class KdaHipError(RuntimeError):
     """A non-zero return code from the HIP library."""
 
@@ -112,6 +134,10 @@ def lib() -> ctypes.CDLL:
             fn = getattr(h, name)
             fn.restype = ctypes.c_int
             fn.argtypes = [ctypes.POINTER(KdaBt16Args), ctypes.c_void_p]
+        h.kda_bt16_bwd_workspace_bytes.restype = ctypes.c_size_t
+        h.kda_bt16_bwd_workspace_bytes.argtypes = [ctypes.POINTER(KdaBt16Args)]
+        h.kda_bt16_bwd_hip.restype = ctypes.c_int
+        h.kda_bt16_bwd_hip.argtypes = [ctypes.POINTER(KdaBt16BwdArgs), ctypes.c_void_p]
         h.kda_bt16_strerror.restype = ctypes.c_char_p
         h.kda_bt16_strerror.argtypes = [ctypes.c_int]
         h.kda_bt16_abi_version.restype = ctypes.c_int
@@ -133,7 +159,12 @@ def workspace_bytes_args(args: KdaBt16Args) -> int:
     return int(lib().kda_bt16_workspace_bytes_args(ctypes.byref(args)))
 
 
-def call(name: str, args: KdaBt16Args, stream: int) -> None:
+def bwd_workspace_bytes(args: KdaBt16Args) -> int:
+    """Backward workspace bytes (``kda_bt16_bwd_workspace_bytes``)."""
+    return int(lib().kda_bt16_bwd_workspace_bytes(ctypes.byref(args)))
+
+
+def call(name: str, args, stream: int) -> None:
     rc = getattr(lib(), name)(ctypes.byref(args), ctypes.c_void_p(stream))
     if rc != 0:
         raise KdaHipError(name, rc, lib().kda_bt16_strerror(rc).decode())

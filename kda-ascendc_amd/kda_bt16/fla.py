@@ -15,7 +15,9 @@ FLA conventions that differ from :func:`kda_bt16.kda_bt16_fwd`:
 * ``chunk_size`` is accepted for signature compatibility; the kernels use
   16-token chunks (results equal FLA's 64-token chunks to rounding, the
   reference's own check at 0.01, ``tests/test_kda_bt16.py:84-101``);
-* ``cu_seqlens`` packs sequences along T with B == 1.
+* ``cu_seqlens`` packs sequences along T with B == 1;
+* ``chunk_kda`` is differentiable (autograd runs the HIP backward);
+  ``fused_recurrent_kda`` is forward-only, like the token recurrence.
 
 What this backend serves is :func:`verify_chunk_kda` /
 :func:`verify_fused_recurrent_kda`'s bucket; outside it the functions raise
@@ -27,7 +29,7 @@ from __future__ import annotations
 
 import torch
 
-from .kernels import _run, _validate_kda_inputs, kda_recurrent_fwd
+from .kernels import _fwd_maybe_autograd, _validate_kda_inputs, kda_recurrent_fwd
 
 _LB_RANGE = (-11.0, 0.0)
 
@@ -36,7 +38,7 @@ def _lb_ok(lower_bound) -> bool:
     return lower_bound is not None and _LB_RANGE[0] < float(lower_bound) < _LB_RANGE[1]
 
 
-def _common_reason(q, k, v, g, beta) -> str | None:
+def _common_reason(q, k, v, g, beta, allow_grad: bool = False) -> str | None:
     for name, t in (("q", q), ("k", k), ("v", v)):
         if t.dtype != torch.bfloat16:
             return f"{name} must be bfloat16, got {t.dtype}"
@@ -46,7 +48,7 @@ def _common_reason(q, k, v, g, beta) -> str | None:
         return "needs HV a multiple of H"
     if g.dtype not in (torch.float32, torch.bfloat16) or beta.dtype not in (torch.float32, torch.bfloat16):
         return "g and beta must be float32 or bfloat16"
-    if torch.is_grad_enabled() and any(
+    if not allow_grad and torch.is_grad_enabled() and any(
             t is not None and t.requires_grad for t in (q, k, v, g, beta)):
         return "forward only: inputs require grad"
     return None
@@ -60,14 +62,15 @@ def verify_chunk_kda(q, k, v, g, beta, *, use_gate_in_kernel=False, safe_gate=Fa
                      lower_bound=None, A_log=None, return_intermediate_states=False,
                      cp_context=None, **_ignored) -> str | None:
     """``None`` if :func:`chunk_kda` serves this call, else the reason it
-    does not.  The bucket: bf16 q/k/v, K = V = 128, HV a multiple of H, no
-    autograd, no context parallelism or intermediate states, and a gate
+    does not.  The bucket: bf16 q/k/v, K = V = 128, HV a multiple of H
+    (autograd included: the backward kernels serve it), no context
+    parallelism or intermediate states, and a gate
     bounded below by ``lower_bound`` in (-11, 0): the in-kernel gate
     ``lower_bound * sigmoid(...)``, or a per-token log decay the caller
     guarantees to be >= lower_bound (FLA's ``safe_gate`` contract).  The
     unbounded softplus gate (``lower_bound=None``) is not served: a 16-token
     chunk's decay span would overflow fp32 (kernels.py:733-744)."""
-    reason = _common_reason(q, k, v, g, beta)
+    reason = _common_reason(q, k, v, g, beta, allow_grad=True)
     if reason:
         return reason
     if return_intermediate_states:
@@ -150,11 +153,11 @@ def chunk_kda(
     )
     if scale is None:
         scale = K ** -0.5
-    return _run(
+    return _fwd_maybe_autograd(
         q, k, v, g, beta, scale, initial_state, output_final_state,
         use_qk_l2norm_in_kernel, use_gate_in_kernel, use_beta_sigmoid_in_kernel,
         lower_bound, A_log, dt_bias, state_v_first,
-        return_intermediates=False, cu_seqlens=cu_seqlens, g_log=not use_gate_in_kernel,
+        cu_seqlens=cu_seqlens, g_log=not use_gate_in_kernel,
     )
 
 

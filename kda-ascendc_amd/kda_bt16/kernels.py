@@ -25,10 +25,16 @@ Differences from the reference, all supersets of its contract:
 * ``cu_seqlens`` (keyword, default None) packs N variable-length sequences
   along T with B == 1, FLA's varlen convention; the states are then
   ``[N, HV, ...]`` (the reference lists varlen as a limitation,
-  README.md:420-421).
+  README.md:420-421);
+* the forward is differentiable: when an input requires grad,
+  :func:`kda_bt16_fwd` records an autograd node whose backward runs the
+  HIP backward (:func:`kda_bt16_bwd`; the reference is forward-only,
+  README.md:420).
 """
 
 from __future__ import annotations
+
+import ctypes
 
 import torch
 
@@ -353,6 +359,165 @@ def _run(
     return o, ht
 
 
+def _bwd_run(
+    do: torch.Tensor,
+    dht: torch.Tensor | None,
+    q, k, v, g, beta, scale, initial_state, use_qk_l2norm_in_kernel, use_gate_in_kernel,
+    use_beta_sigmoid_in_kernel, lower_bound, A_log, dt_bias, state_v_first, cu_seqlens, g_log,
+    need_gate_grads: bool = True, need_dh0: bool = True,
+):
+    """Host driver of the backward: allocate the gradients, lease the
+    workspace, launch ``kda_bt16_bwd_hip`` on the current stream.
+
+    Returns ``(dq, dk, dv, dg, dbeta, dA_log, ddt_bias, dh0)``; dA_log /
+    ddt_bias are None without the in-kernel gate (or dt_bias), dh0 is None
+    without an initial state."""
+    _require_gpu(q)
+    q, k, v, g, initial_state, dt_bias = (
+        _aligned(x) for x in (q, k, v, g, initial_state, dt_bias))
+    dev = q.device
+    do = _aligned(do.to(torch.bfloat16).contiguous())
+    if dht is not None:
+        dht = _aligned(dht.to(torch.float32).contiguous())
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    dg = torch.empty_like(g)
+    dbeta = torch.empty_like(beta)
+    gate_grads = need_gate_grads and use_gate_in_kernel
+    dA_log = torch.empty_like(A_log) if gate_grads and A_log is not None else None
+    ddt_bias = torch.empty_like(dt_bias) if gate_grads and dt_bias is not None else None
+    dh0 = torch.empty_like(initial_state) if (need_dh0 and initial_state is not None) else None
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        fa = _make_args(
+            q, k, v, g, beta, scale, lower_bound if use_gate_in_kernel else None,
+            A_log, dt_bias, initial_state, None, None, None, 0,
+            _flags(use_gate_in_kernel, use_qk_l2norm_in_kernel, use_beta_sigmoid_in_kernel,
+                   state_v_first, g_log),
+            None, cu_seqlens,
+        )
+        ws_bytes = _hip.bwd_workspace_bytes(fa)
+        ws = workspace.lease(dev, stream, ws_bytes)
+        ba = _hip.KdaBt16BwdArgs()
+        ba.fwd = ctypes.pointer(fa)
+        ba.dout = do.data_ptr()
+        ba.dht = _ptr(dht)
+        ba.dq, ba.dk, ba.dv = dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
+        ba.dg, ba.dbeta = dg.data_ptr(), dbeta.data_ptr()
+        ba.dA_log = _ptr(dA_log)
+        ba.ddt_bias = _ptr(ddt_bias)
+        ba.dh0 = _ptr(dh0)
+        ba.workspace, ba.workspace_bytes = ws.data_ptr(), ws_bytes
+        _hip.call("kda_bt16_bwd_hip", ba, stream)
+    return dq, dk, dv, dg, dbeta, dA_log, ddt_bias, dh0
+
+
+class _KdaBt16Fn(torch.autograd.Function):
+    """Autograd node of the chunked forward: the forward is :func:`_run`;
+    the backward recomputes the chunk states and runs the backward kernels
+    (``csrc/kda_bwd.hip``) through ``kda_bt16_bwd_hip``."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, beta, A_log, dt_bias, initial_state, cu_seqlens, cfg):
+        (scale, output_final_state, l2, use_gate, bsig, lower_bound, svf, g_log, reuse) = cfg
+        o, ht = _run(
+            q, k, v, g, beta, scale, initial_state, output_final_state, l2, use_gate, bsig,
+            lower_bound, A_log, dt_bias, svf, return_intermediates=False,
+            reuse_workspace=reuse, cu_seqlens=cu_seqlens, g_log=g_log,
+        )
+        ctx.save_for_backward(q, k, v, g, beta, A_log, dt_bias, initial_state, cu_seqlens)
+        ctx.cfg = cfg
+        return o, ht
+
+    @staticmethod
+    def backward(ctx, do, dht):
+        q, k, v, g, beta, A_log, dt_bias, h0, cu = ctx.saved_tensors
+        (scale, _ofs, l2, use_gate, bsig, lower_bound, svf, g_log, _reuse) = ctx.cfg
+        if do is None:
+            do = torch.zeros(v.shape, dtype=torch.bfloat16, device=v.device)
+        need = ctx.needs_input_grad
+        dq, dk, dv, dg, dbeta, dA_log, ddt_bias, dh0 = _bwd_run(
+            do, dht, q, k, v, g, beta, scale, h0, l2, use_gate, bsig, lower_bound, A_log,
+            dt_bias, svf, cu, g_log, need_gate_grads=need[5] or need[6], need_dh0=need[7],
+        )
+        return (dq, dk, dv, dg, dbeta, dA_log if need[5] else None,
+                ddt_bias if need[6] else None, dh0 if need[7] else None, None, None)
+
+
+def _wants_grad(*ts) -> bool:
+    return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts)
+
+
+def _fwd_maybe_autograd(
+    q, k, v, g, beta, scale, initial_state, output_final_state, l2, use_gate, bsig,
+    lower_bound, A_log, dt_bias, svf, reuse_workspace=False, cu_seqlens=None, g_log=False,
+):
+    """:func:`_run`, through :class:`_KdaBt16Fn` when an input requires grad."""
+    if _wants_grad(q, k, v, g, beta, A_log, dt_bias, initial_state):
+        cfg = (scale, output_final_state, l2, use_gate, bsig, lower_bound, svf, g_log,
+               reuse_workspace)
+        return _KdaBt16Fn.apply(q, k, v, g, beta, A_log, dt_bias, initial_state, cu_seqlens, cfg)
+    return _run(
+        q, k, v, g, beta, scale, initial_state, output_final_state, l2, use_gate, bsig,
+        lower_bound, A_log, dt_bias, svf, return_intermediates=False,
+        reuse_workspace=reuse_workspace, cu_seqlens=cu_seqlens, g_log=g_log,
+    )
+
+
+def kda_bt16_bwd(
+    do: torch.Tensor,
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    g: torch.Tensor,
+    beta: torch.Tensor,
+    scale: float | None = None,
+    initial_state: torch.Tensor | None = None,
+    dht: torch.Tensor | None = None,
+    use_qk_l2norm_in_kernel: bool = False,
+    use_gate_in_kernel: bool = False,
+    use_beta_sigmoid_in_kernel: bool = False,
+    safe_gate: bool = True,
+    lower_bound: float = -5.0,
+    A_log: torch.Tensor | None = None,
+    dt_bias: torch.Tensor | None = None,
+    state_v_first: bool = True,
+    *,
+    cu_seqlens: torch.Tensor | None = None,
+    g_log: bool = False,
+) -> dict:
+    """Backward of :func:`kda_bt16_fwd` (no counterpart in the reference,
+    which is forward-only, README.md:420): the gradients of
+    ``sum(o * do) + sum(ht * dht)`` with respect to every input, for the
+    forward's arguments.  ``g_log`` selects FLA's per-token log decay for
+    ``g`` (as :func:`kda_bt16.fla.chunk_kda` uses it).
+
+    Returns a dict with ``dq, dk, dv`` (bf16), ``dg``, ``dbeta`` (the dtypes
+    of g and beta), ``dA_log``, ``ddt_bias`` (fp32, with the in-kernel gate)
+    and ``dh0`` (with an initial state, in its layout).  The same math runs
+    when :func:`kda_bt16_fwd`'s inputs require grad and autograd calls it.
+    """
+    B, T, H, K, HV, V = _validate_kda_inputs(
+        q, k, v, g, beta, initial_state, use_gate_in_kernel, safe_gate, lower_bound,
+        A_log, dt_bias, state_v_first, cu_seqlens,
+    )
+    S = B if cu_seqlens is None else cu_seqlens.numel() - 1
+    if do.shape != (B, T, HV, V):
+        raise ValueError(f"do.shape {tuple(do.shape)} must be [B={B}, T={T}, HV={HV}, V={V}]")
+    if dht is not None and dht.shape != ((S, HV, V, K) if state_v_first else (S, HV, K, V)):
+        raise ValueError(f"dht.shape {tuple(dht.shape)} must match the final state's")
+    if scale is None:
+        scale = K ** -0.5
+    dq, dk, dv, dg, dbeta, dA_log, ddt_bias, dh0 = _bwd_run(
+        do, dht, q, k, v, g, beta, scale, initial_state, use_qk_l2norm_in_kernel,
+        use_gate_in_kernel, use_beta_sigmoid_in_kernel, lower_bound, A_log, dt_bias,
+        state_v_first, cu_seqlens, g_log,
+    )
+    return {"dq": dq, "dk": dk, "dv": dv, "dg": dg, "dbeta": dbeta, "dA_log": dA_log,
+            "ddt_bias": ddt_bias, "dh0": dh0}
+
+
 def kda_bt16_fwd(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -402,14 +567,12 @@ def kda_bt16_fwd(
     )
     if scale is None:
         scale = K ** -0.5
-    return _run(
+    del use_fused_kernel  # one production path; see module docstring
+    return _fwd_maybe_autograd(
         q, k, v, g, beta, scale, initial_state, output_final_state,
         use_qk_l2norm_in_kernel, use_gate_in_kernel, use_beta_sigmoid_in_kernel,
         lower_bound, A_log, dt_bias, state_v_first,
-        return_intermediates=False,
-        use_fused=use_fused_kernel,
-        reuse_workspace=reuse_workspace,
-        cu_seqlens=cu_seqlens,
+        reuse_workspace=reuse_workspace, cu_seqlens=cu_seqlens,
     )
 
 

@@ -146,3 +146,52 @@ def test_o_fp32_is_refused_on_chunked_entries():
     fake = 1 << 40
     a = _args(q=fake, k=fake, v=fake, g=fake, beta=fake, o=fake, flags=_hip.O_FP32)
     assert _hip.lib().kda_bt16_fwd_hip(ctypes.byref(a), None) == -2
+
+
+def test_bwd_struct_layout_matches_header_field_order():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    body = re.search(r"typedef struct KdaBt16BwdArgs \{(.*?)\} KdaBt16BwdArgs;", text, re.S).group(1)
+    names = [re.findall(r"(\w+)\s*$", d.strip())[0] for d in body.split(";") if d.strip()]
+    assert names == [f for f, _ in _hip.KdaBt16BwdArgs._fields_]
+
+
+def test_bwd_workspace_bytes():
+    # per record slot: record, bf16 h and dh, v_new and dv_new, gate partials;
+    # each region 256-byte aligned
+    R = 32 * 512
+    per = [17408, 32768, 4096, 32768, 4096, 132 * 4]
+    assert _hip.bwd_workspace_bytes(_args(B=1, T=8192, H=32, HV=32)) == sum(
+        (R * x + 255) // 256 * 256 for x in per)
+    assert _hip.bwd_workspace_bytes(_args(K=64)) == 0
+
+
+def _bwd(fwd, **kw):
+    b = _hip.KdaBt16BwdArgs()
+    b.fwd = ctypes.pointer(fwd)
+    for name, val in kw.items():
+        setattr(b, name, val)
+    return b
+
+
+def test_bwd_argument_checks_return_codes_without_launching():
+    f = _hip.lib().kda_bt16_bwd_hip
+    fake = 1 << 40  # never dereferenced: the checks fail first
+    ins = dict(q=fake, k=fake, v=fake, g=fake, beta=fake)
+    grads = dict(dout=fake, dq=fake, dk=fake, dv=fake, dg=fake, dbeta=fake)
+    assert f(None, None) == -1
+    assert f(ctypes.byref(_bwd(_args(abi_version=99), **grads)), None) == -5
+    assert f(ctypes.byref(_bwd(_args(K=64, **ins), **grads)), None) == -2
+    assert f(ctypes.byref(_bwd(_args(**ins), **{**grads, "dq": None})), None) == -1
+    assert f(ctypes.byref(_bwd(_args(**ins, dbg_Aqk=fake), **grads)), None) == -1
+    # gate-parameter gradients need the in-kernel gate (and dt_bias for ddt_bias)
+    assert f(ctypes.byref(_bwd(_args(**ins), **grads, dA_log=fake)), None) == -1
+    gate = _args(**ins, flags=_hip.USE_GATE, A_log=fake)
+    assert f(ctypes.byref(_bwd(gate, **grads, ddt_bias=fake)), None) == -1
+    assert f(ctypes.byref(_bwd(_args(**ins), **{**grads, "dv": fake + 8})), None) == -1
+    # workspace missing, too small or misaligned
+    assert f(ctypes.byref(_bwd(_args(**ins), **grads)), None) == -3
+    assert f(ctypes.byref(_bwd(_args(**ins), **grads, workspace=fake, workspace_bytes=100)),
+             None) == -3
+    need = _hip.bwd_workspace_bytes(_args())
+    assert f(ctypes.byref(_bwd(_args(**ins), **grads, workspace=fake + 8,
+                               workspace_bytes=need)), None) == -3

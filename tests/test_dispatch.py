@@ -141,8 +141,11 @@ def test_verifier_bucket_reasons():
         "tensors are not on a ROCm GPU"
     assert "intermediate" in verify_chunk_kda(q, k, v, g, b, return_intermediate_states=True, **ok_gate)
     assert "context" in verify_chunk_kda(q, k, v, g, b, cp_context=object(), **ok_gate)
+    # autograd is served by chunk_kda (the backward kernels), not by the
+    # forward-only token recurrence
     qg = q.clone().requires_grad_(False).float().requires_grad_(True).bfloat16()
-    assert "grad" in verify_chunk_kda(qg, k, v, g, b, **ok_gate)
+    assert verify_chunk_kda(qg, k, v, g, b, **ok_gate) == "tensors are not on a ROCm GPU"
+    assert "grad" in verify_fused_recurrent_kda(qg, k, v, g, b)
     # the token recurrence takes an unbounded log decay
     assert verify_fused_recurrent_kda(q, k, v, g, b) == "tensors are not on a ROCm GPU"
 
