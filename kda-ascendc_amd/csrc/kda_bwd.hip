@@ -121,8 +121,8 @@ __global__ __launch_bounds__(64) void bwd_state_kernel(Params p) {
     if (sp.nt > 0) {
         const int col = 16 * vt + 4 * (x >> 2);
         const uint8_t* recs = p.ws + sp.rec0 * REC_BYTES;
-        uint16_t* dh_out = p.tr_dh + sp.rec0 * TR_H_ELEMS + col;
-        uint16_t* dvn_out = p.tr_dvn + sp.rec0 * TR_VN_ELEMS + col;
+        uint16_t* dh_out = p.tr_dh + sp.rec0 * TR_H_ELEMS + vt * TR_H_TILE + 4 * (x >> 2);
+        uint16_t* dvn_out = p.tr_dvn + sp.rec0 * TR_VN_ELEMS + vt * TR_VN_TILE + 4 * (x >> 2);
         // this lane's dO row piece: token 16*c + 4*q4 + j4, columns col..col+3
         const int64_t dstride = (int64_t)p.HV * DK;
         const uint16_t* dbase = p.dout + (sp.tok0 * p.HV + hv) * DK + col;
@@ -155,12 +155,12 @@ __global__ __launch_bounds__(64) void bwd_state_kernel(Params p) {
                 const u32x2 t0 = quad_transpose(hb[j].x, hb[j].y, j4);
                 const u32x2 t1 = quad_transpose(hb[j].z, hb[j].w, j4);
                 const int k0 = 32 * j + 4 * q4 + j4;
-                *reinterpret_cast<u32x2*>(dhc + (int64_t)k0 * DK) = t0;
-                *reinterpret_cast<u32x2*>(dhc + (int64_t)(k0 + 16) * DK) = t1;
+                *reinterpret_cast<u32x2*>(dhc + k0 * 16) = t0;
+                *reinterpret_cast<u32x2*>(dhc + (k0 + 16) * 16) = t1;
             }
             const u32x2 dvb = {pack2(dvn[0], dvn[1]), pack2(dvn[2], dvn[3])};
             const u32x2 dvt = quad_transpose(dvb.x, dvb.y, j4);
-            *reinterpret_cast<u32x2*>(dvn_out + (int64_t)c * TR_VN_ELEMS + (4 * q4 + j4) * DK) = dvt;
+            *reinterpret_cast<u32x2*>(dvn_out + (int64_t)c * TR_VN_ELEMS + (4 * q4 + j4) * 16) = dvt;
             // dh = 2^G_last * dh' + [scale qg | -w]^T [dO ; dv_new]
             const u32x4 bop = {dt.x, dt.y, dvb.x, dvb.y};
 #pragma unroll
@@ -181,10 +181,15 @@ __global__ __launch_bounds__(64) void bwd_state_kernel(Params p) {
 constexpr int CT = 256;    // threads: row i = t / 16 owns columns 8*(t % 16) .. +7
 constexpr int LD = DK + 4; // fp32 row stride of the [16][128] LDS matrices
 
+// The four waves split the small products on the fp32 16x16x4 matrix op,
+// operands read from these tiles: lane (n, k') of a wave supplies
+// A[n][4*s + k'] and B[4*s + k'][n] for slab s, and D[m][n] lands in lane
+// n + 16*(m/4) item m%4 (kda_common.h).
 struct ChunkSmem {
     float kp[BT][LD], km[BT][LD], qp[BT][LD], kb[BT][LD], vb[BT][LD];
     float dw[BT][LD], dvn[BT][LD], dqg[BT][LD], dkg[BT][LD], gsc[BT][LD];
     float el[DK], del[DK];
+    float partL[4][BT][BT + 1], partA[4][BT][BT + 1];
     float lraw[BT][BT + 1], ainv[BT][BT + 1], da[BT][BT + 1], m1[BT][BT + 1];
     float dlr[BT][BT + 1], daqm[BT][BT + 1];
     float red[CT / 64];
@@ -205,6 +210,21 @@ __device__ __forceinline__ void store8(uint16_t* dst, const float (&x)[8]) {
         u32x4{pack2(x[0], x[1]), pack2(x[2], x[3]), pack2(x[4], x[5]), pack2(x[6], x[7])};
 }
 
+__device__ __forceinline__ void lds_put8(float* dst, const float (&x)[8]) {
+    *reinterpret_cast<f32x4*>(dst) = f32x4{x[0], x[1], x[2], x[3]};
+    *reinterpret_cast<f32x4*>(dst + 4) = f32x4{x[4], x[5], x[6], x[7]};
+}
+
+__device__ __forceinline__ void lds_get8(const float* src, float (&x)[8]) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(src);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(src + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        x[j] = a[j];
+        x[4 + j] = b[j];
+    }
+}
+
 // Sum over the 16 threads of a row (lanes 16*m .. 16*m + 15 of a wave).
 __device__ __forceinline__ float row_sum16(float s) {
     s += __shfl_xor(s, 1);
@@ -214,12 +234,17 @@ __device__ __forceinline__ float row_sum16(float s) {
     return s;
 }
 
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + expf(-x)); }
+// One value head's row data of this thread (row i, columns c0 .. c0+7).
+struct HvRow {
+    float v[8], g[8], dvn[8], bias[8];
+    float beta;
+};
 
 __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
     __shared__ ChunkSmem sm;
     const int t = threadIdx.x;
     const int lane = t & 63, w = t >> 6;
+    const int x = lane & 15, q4 = lane >> 4;  // matrix-op lane coordinates
     const int i = t >> 4;          // row (and row of the 16x16 mapping)
     const int cb = t & 15;         // column of the 16x16 mapping
     const int c0 = 8 * cb;         // first of this thread's 8 columns
@@ -253,10 +278,51 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
     const bool valid = i < nvalid;
     const int64_t tok = sq.tok0 + c * BT + i;
 
+    auto load_hv = [&](int hv, HvRow& r) {
+        const SeqSpan sp = seq_span(p, seq * HV + hv);
+        const int64_t rec = sp.rec0 + c;
+        const int64_t vrow = (tok * HV + hv) * DK;
+        load8(p.v + vrow + c0, valid, r.v);
+        load8(p.tr_dvn + rec * TR_VN_ELEMS + (cb >> 1) * TR_VN_TILE + i * 16 + 8 * (cb & 1), valid,
+              r.dvn);
+        if (p.g_bf16) {
+            load8(static_cast<const uint16_t*>(p.g) + vrow + c0, valid, r.g);
+        } else {
+            f32x4 a = {0.f, 0.f, 0.f, 0.f}, b = a;
+            if (valid) {
+                a = *reinterpret_cast<const f32x4*>(static_cast<const float*>(p.g) + vrow + c0);
+                b = *reinterpret_cast<const f32x4*>(static_cast<const float*>(p.g) + vrow + c0 + 4);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                r.g[j] = a[j];
+                r.g[4 + j] = b[j];
+            }
+        }
+        f32x4 ba = {0.f, 0.f, 0.f, 0.f}, bb = ba;
+        if (p.use_gate && p.dt_bias) {
+            ba = *reinterpret_cast<const f32x4*>(p.dt_bias + hv * DK + c0);
+            bb = *reinterpret_cast<const f32x4*>(p.dt_bias + hv * DK + c0 + 4);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            r.bias[j] = ba[j];
+            r.bias[4 + j] = bb[j];
+        }
+        r.beta = 0.f;
+        if (valid) {
+            const int64_t bi = tok * HV + hv;
+            r.beta = p.beta_bf16 ? bf2f(static_cast<const uint16_t*>(p.beta)[bi])
+                                 : static_cast<const float*>(p.beta)[bi];
+        }
+    };
+
     // ---- q^, k^ (kernels.py:108-113), once per q/k head ------------------
     float qv[8], kv[8], qn[8], kn[8];
     load8(p.q + (tok * H + h) * DK + c0, valid, qv);
     load8(p.k + (tok * H + h) * DK + c0, valid, kv);
+    HvRow hr;
+    load_hv(h * rep, hr);
     float rq = 1.f, rk = 1.f;
     if (p.use_l2norm) {
         float sq2 = 0.f, sk2 = 0.f;
@@ -281,41 +347,25 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
 
     for (int gi = 0; gi < rep; ++gi) {
         const int hv = h * rep + gi;
+        if (gi > 0) load_hv(hv, hr);
         const SeqSpan sp = seq_span(p, seq * HV + hv);
         const int64_t rec = sp.rec0 + c;
         const int64_t vrow = (tok * HV + hv) * DK;  // v/g/dO element offset of row i
 
         // ---- phase 1: gates, cumsum, recentred operands ------------------
-        float vv[8], gr[8], dvn[8];
-        load8(p.v + vrow + c0, valid, vv);
-        load8(p.tr_dvn + rec * TR_VN_ELEMS + i * DK + c0, valid, dvn);
-        if (p.g_bf16) {
-            load8(static_cast<const uint16_t*>(p.g) + vrow + c0, valid, gr);
-        } else {
-            const float* gs = static_cast<const float*>(p.g) + vrow + c0;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) gr[j] = valid ? gs[j] : 0.f;
-        }
-        float beta = 0.f;
-        if (valid) {
-            const int64_t bi = tok * HV + hv;
-            beta = p.beta_bf16 ? bf2f(static_cast<const uint16_t*>(p.beta)[bi])
-                               : static_cast<const float*>(p.beta)[bi];
-        }
-        const float braw = beta;
-        if (p.use_beta_sigmoid) beta = valid ? sigmoidf_(braw) : 0.f;
+        float beta = hr.beta;
+        if (p.use_beta_sigmoid) beta = valid ? fast_sigmoid(hr.beta) : 0.f;
         const float ea = p.use_gate ? expf(p.A_log[hv]) : 0.f;
-        float bias[8];
+        {
+            float gv[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-            bias[j] = (p.use_gate && p.dt_bias) ? p.dt_bias[hv * DK + c0 + j] : 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            float gv;
-            if (p.use_gate) gv = p.lower_bound * sigmoidf_(ea * (gr[j] + bias[j]));
-            else gv = gr[j];
-            sm.gsc[i][c0 + j] = valid ? gv : 0.f;
-            sm.dvn[i][c0 + j] = dvn[j];
+            for (int j = 0; j < 8; ++j) {
+                const float gg = p.use_gate ? p.lower_bound * fast_sigmoid(ea * (hr.g[j] + hr.bias[j]))
+                                            : hr.g[j];
+                gv[j] = valid ? gg : 0.f;
+            }
+            lds_put8(&sm.gsc[i][c0], gv);
+            lds_put8(&sm.dvn[i][c0], hr.dvn);
         }
         __syncthreads();
         if ((p.use_gate || p.g_log) && t < DK) {
@@ -327,22 +377,30 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
             }
         }
         __syncthreads();
-        if (t < DK) sm.el[t] = exp2f(sm.gsc[last][t]);
+        if (t < DK) sm.el[t] = fast_exp2(sm.gsc[last][t]);
         float E[8], eq[8], ek[8], kgl[8];
+        {
+            float G[8], Gm[8], Gl[8], o1[8], o2[8], o3[8], o4[8], o5[8];
+            lds_get8(&sm.gsc[i][c0], G);
+            lds_get8(&sm.gsc[mid][c0], Gm);
+            lds_get8(&sm.gsc[last][c0], Gl);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float G = sm.gsc[i][c0 + j];
-            const float Gm = sm.gsc[mid][c0 + j];
-            const float Gl = sm.gsc[last][c0 + j];
-            E[j] = valid ? exp2f(G) : 0.f;
-            eq[j] = valid ? exp2f(G - Gm) : 0.f;
-            ek[j] = valid ? exp2f(Gm - G) : 0.f;
-            kgl[j] = valid ? exp2f(Gl - G) : 0.f;
-            sm.qp[i][c0 + j] = qn[j] * eq[j];
-            sm.kp[i][c0 + j] = kn[j] * eq[j];
-            sm.km[i][c0 + j] = kn[j] * ek[j];
-            sm.kb[i][c0 + j] = round_bf(round_bf(kn[j] * beta) * E[j]);
-            sm.vb[i][c0 + j] = round_bf(vv[j] * beta);
+            for (int j = 0; j < 8; ++j) {
+                E[j] = valid ? fast_exp2(G[j]) : 0.f;
+                eq[j] = valid ? fast_exp2(G[j] - Gm[j]) : 0.f;
+                ek[j] = valid ? fast_exp2(Gm[j] - G[j]) : 0.f;
+                kgl[j] = valid ? fast_exp2(Gl[j] - G[j]) : 0.f;
+                o1[j] = qn[j] * eq[j];
+                o2[j] = kn[j] * eq[j];
+                o3[j] = kn[j] * ek[j];
+                o4[j] = round_bf(round_bf(kn[j] * beta) * E[j]);
+                o5[j] = round_bf(hr.v[j] * beta);
+            }
+            lds_put8(&sm.qp[i][c0], o1);
+            lds_put8(&sm.kp[i][c0], o2);
+            lds_put8(&sm.km[i][c0], o3);
+            lds_put8(&sm.kb[i][c0], o4);
+            lds_put8(&sm.vb[i][c0], o5);
         }
 
         // ---- phase 2: products over V on the matrix cores ----------------
@@ -350,12 +408,14 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
         // dv_new / v_new and row 16*kt + x of h / dh', v columns
         // 32*jv + 8*q4 .. +7, as 16x16x32 operands.
         {
-            const int x = lane & 15, q4 = lane >> 4;
             const bool xv = x < nvalid;
             const uint16_t* hrec = p.tr_h + rec * TR_H_ELEMS;
             const uint16_t* dhrec = p.tr_dh + rec * TR_H_ELEMS;
-            const uint16_t* vnrec = p.tr_vn + rec * TR_VN_ELEMS + x * DK + 8 * q4;
-            const uint16_t* dvrec = p.tr_dvn + rec * TR_VN_ELEMS + x * DK + 8 * q4;
+            // blocked layouts: v = 32*jv + 8*q4 + e lies in value tile
+            // 2*jv + q4/2 at column 8*(q4%2) + e
+            const int64_t vnoff = (q4 >> 1) * TR_VN_TILE + x * 16 + 8 * (q4 & 1);
+            const uint16_t* vnrec = p.tr_vn + rec * TR_VN_ELEMS + vnoff;
+            const uint16_t* dvrec = p.tr_dvn + rec * TR_VN_ELEMS + vnoff;
             const uint16_t* dorow = p.dout + ((sq.tok0 + c * BT + x) * HV + hv) * DK + 8 * q4;
             f32x4 aq[2], aw[2], ak[2], adq = {0.f, 0.f, 0.f, 0.f};
             float pel[2] = {0.f, 0.f};
@@ -366,13 +426,14 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
                 u32x4 a_do = {0u, 0u, 0u, 0u}, a_dv = {0u, 0u, 0u, 0u}, a_vn = {0u, 0u, 0u, 0u};
                 if (xv) {
                     a_do = *reinterpret_cast<const u32x4*>(dorow + 32 * jv);
-                    a_dv = *reinterpret_cast<const u32x4*>(dvrec + 32 * jv);
-                    a_vn = *reinterpret_cast<const u32x4*>(vnrec + 32 * jv);
+                    a_dv = *reinterpret_cast<const u32x4*>(dvrec + 2 * jv * TR_VN_TILE);
+                    a_vn = *reinterpret_cast<const u32x4*>(vnrec + 2 * jv * TR_VN_TILE);
                 }
 #pragma unroll
                 for (int tt = 0; tt < 2; ++tt) {
                     const int kt = 2 * w + tt;
-                    const int64_t off = (int64_t)(16 * kt + x) * DK + 32 * jv + 8 * q4;
+                    const int64_t off = (2 * jv + (q4 >> 1)) * TR_H_TILE + (16 * kt + x) * 16 +
+                                        8 * (q4 & 1);
                     const u32x4 bh = *reinterpret_cast<const u32x4*>(hrec + off);
                     const u32x4 bd = *reinterpret_cast<const u32x4*>(dhrec + off);
                     aq[tt] = mfma_bf16_16x16x32(as_bf16x8(a_do), as_bf16x8(bh), aq[tt]);
@@ -398,10 +459,10 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
                     sm.dw[row][16 * kt + x] = -aw[tt][e];
                     sm.dkg[row][16 * kt + x] = ak[tt][e];
                 }
-                float s = pel[tt];
-                s += __shfl_xor(s, 16);
-                s += __shfl_xor(s, 32);
-                if (q4 == 0) sm.del[16 * kt + x] = s;
+                float s2 = pel[tt];
+                s2 += __shfl_xor(s2, 16);
+                s2 += __shfl_xor(s2, 32);
+                if (q4 == 0) sm.del[16 * kt + x] = s2;
             }
             if (w == 0) {
 #pragma unroll
@@ -413,23 +474,36 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
         }
         __syncthreads();
 
-        // ---- phase 3: L = beta tril_strict(kp km^T), A = (I + L)^-1 -------
+        // ---- phase 3: the grams Lraw = kp km^T and dA = dw kb^T + du vb^T,
+        // each wave over 32 of the 128 columns ------------------------------
         {
-            float s = 0.f;
-            for (int k = 0; k < DK; k += 4) {
-                const f32x4 a = *reinterpret_cast<const f32x4*>(&sm.kp[i][k]);
-                const f32x4 b = *reinterpret_cast<const f32x4*>(&sm.km[cb][k]);
-                s = fmaf(a[0], b[0], s);
-                s = fmaf(a[1], b[1], s);
-                s = fmaf(a[2], b[2], s);
-                s = fmaf(a[3], b[3], s);
+            f32x4 lr = {0.f, 0.f, 0.f, 0.f}, da = lr;
+#pragma unroll
+            for (int sl = 0; sl < 8; ++sl) {
+                const int col = 32 * w + 4 * sl + q4;
+                lr = mfma_f32_16x16x4(sm.kp[x][col], sm.km[x][col], lr);
+                da = mfma_f32_16x16x4(sm.dw[x][col], sm.kb[x][col], da);
+                da = mfma_f32_16x16x4(sm.dvn[x][col], sm.vb[x][col], da);
             }
-            sm.lraw[i][cb] = s;
-            sm.m1[i][cb] = (i > cb) ? beta * s : 0.f;  // L, read by the solve
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                sm.partL[w][4 * q4 + e][x] = lr[e];
+                sm.partA[w][4 * q4 + e][x] = da[e];
+            }
+        }
+        __syncthreads();
+        {
+            const float lraw = sm.partL[0][i][cb] + sm.partL[1][i][cb] + sm.partL[2][i][cb] +
+                               sm.partL[3][i][cb];
+            sm.lraw[i][cb] = lraw;
+            sm.m1[i][cb] = (i > cb) ? beta * lraw : 0.f;  // L, read by the solve
+            sm.da[i][cb] = sm.partA[0][i][cb] + sm.partA[1][i][cb] + sm.partA[2][i][cb] +
+                           sm.partA[3][i][cb];
         }
         __syncthreads();
         if (t < BT) {
-            // column s = t of A_inv: a[s] = 1, a[r > s] = -sum_{j<r} L[r][j] a[j]
+            // column s = t of A_inv = (I + L)^-1 (kernels.py:157-167):
+            // a[s] = 1, a[r > s] = -sum_{j<r} L[r][j] a[j]
             float a[BT];
 #pragma unroll
             for (int r = 0; r < BT; ++r) {
@@ -443,149 +517,194 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
         }
         __syncthreads();
 
-        // ---- phase 4: dA = dw kb^T + du vb^T; dkb = A^T dw, dvb = A^T du --
+        // ---- phase 4: dkb = A^T dw, dvb = A^T du (A = bf16(A_inv), the
+        // operand of w and u, kernels.py:170), dA A^T ------------------------
+        f32x4 dkbt[2], dvbt[2];
         {
-            float s = 0.f;
-            for (int k = 0; k < DK; k += 4) {
-                const f32x4 a = *reinterpret_cast<const f32x4*>(&sm.dw[i][k]);
-                const f32x4 b = *reinterpret_cast<const f32x4*>(&sm.kb[cb][k]);
-                const f32x4 a2 = *reinterpret_cast<const f32x4*>(&sm.dvn[i][k]);
-                const f32x4 b2 = *reinterpret_cast<const f32x4*>(&sm.vb[cb][k]);
+            float s2 = 0.f;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    s = fmaf(a[e], b[e], s);
-                    s = fmaf(a2[e], b2[e], s);
+            for (int m = 0; m < BT; ++m) s2 = fmaf(sm.da[i][m], sm.ainv[cb][m], s2);
+            sm.m1[i][cb] = s2;  // (dA A^T)[i][cb]; L is dead after the solve
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                const int col = 16 * (2 * w + tt) + x;
+                dkbt[tt] = dvbt[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int sl = 0; sl < 4; ++sl) {
+                    const int r = 4 * sl + q4;
+                    const float a = round_bf(sm.ainv[r][x]);
+                    dkbt[tt] = mfma_f32_16x16x4(a, sm.dw[r][col], dkbt[tt]);
+                    dvbt[tt] = mfma_f32_16x16x4(a, sm.dvn[r][col], dvbt[tt]);
                 }
-            }
-            sm.da[i][cb] = s;
-        }
-        float dkb[8], dvb[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) dkb[j] = dvb[j] = 0.f;
-        for (int r = i; r < BT; ++r) {
-            const float a = round_bf(sm.ainv[r][i]);  // the bf16 A of w, u (kernels.py:170)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                dkb[j] = fmaf(a, sm.dw[r][c0 + j], dkb[j]);
-                dvb[j] = fmaf(a, sm.dvn[r][c0 + j], dvb[j]);
             }
         }
         __syncthreads();
 
-        // ---- phase 5: dL = -A^T dA A^T (strictly lower), dLr = beta dL ----
-        {
-            float s = 0.f;
-#pragma unroll
-            for (int m = 0; m < BT; ++m) s = fmaf(sm.da[i][m], sm.ainv[cb][m], s);
-            sm.m1[i][cb] = s;  // (dA A^T)[i][cb]
-        }
-        __syncthreads();
+        // ---- phase 5: dL = -A^T dA A^T (strictly lower), dLr = beta dL; the
+        // dkb / dvb tiles replace kb / vb (read for the last time above) ----
         float dbl;
         {
-            float s = 0.f;
+            float s2 = 0.f;
 #pragma unroll
-            for (int m = 0; m < BT; ++m) s = fmaf(sm.ainv[m][i], sm.m1[m][cb], s);
-            const float dl = (i > cb) ? -s : 0.f;
+            for (int m = 0; m < BT; ++m) s2 = fmaf(sm.ainv[m][i], sm.m1[m][cb], s2);
+            const float dl = (i > cb) ? -s2 : 0.f;
             sm.dlr[i][cb] = beta * dl;
             dbl = row_sum16(dl * sm.lraw[i][cb]);
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                const int col = 16 * (2 * w + tt) + x;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    sm.kb[4 * q4 + e][col] = dkbt[tt][e];
+                    sm.vb[4 * q4 + e][col] = dvbt[tt][e];
+                }
+            }
         }
         __syncthreads();
 
-        // ---- phase 6: the row-wise gradients ------------------------------
-        float dkp[8], dqp[8], dkm[8];
+        // ---- phase 6: dkp = dLr km, dqp = dAqm km, dkm = dLr^T kp + dAqm^T qp
+        // on the matrix cores, each wave its two column tiles, written in
+        // place of kp / qp / km (only this wave reads those columns) --------
 #pragma unroll
-        for (int j = 0; j < 8; ++j) dkp[j] = dqp[j] = dkm[j] = 0.f;
-#pragma unroll 4
-        for (int b = 0; b < BT; ++b) {
-            const float l1 = sm.dlr[i][b], a1 = sm.daqm[i][b];
-            const float l2 = sm.dlr[b][i], a2 = sm.daqm[b][i];
+        for (int tt = 0; tt < 2; ++tt) {
+            const int col = 16 * (2 * w + tt) + x;
+            f32x4 dkp = {0.f, 0.f, 0.f, 0.f}, dqp = dkp, dkm = dkp;
+#pragma unroll
+            for (int sl = 0; sl < 4; ++sl) {
+                const int r = 4 * sl + q4;
+                const float kmv = sm.km[r][col];
+                dkp = mfma_f32_16x16x4(sm.dlr[x][r], kmv, dkp);
+                dqp = mfma_f32_16x16x4(sm.daqm[x][r], kmv, dqp);
+                dkm = mfma_f32_16x16x4(sm.dlr[r][x], sm.kp[r][col], dkm);
+                dkm = mfma_f32_16x16x4(sm.daqm[r][x], sm.qp[r][col], dkm);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                sm.kp[4 * q4 + e][col] = dkp[e];
+                sm.qp[4 * q4 + e][col] = dqp[e];
+                sm.km[4 * q4 + e][col] = dkm[e];
+            }
+        }
+        __syncthreads();
+
+        // ---- phase 7: the row-wise gradients ------------------------------
+        float dG[8];
+        {
+            float dkp[8], dqp[8], dkm[8], dkb[8], dvb[8], dqg[8], dkg[8], dv[8];
+            lds_get8(&sm.kp[i][c0], dkp);
+            lds_get8(&sm.qp[i][c0], dqp);
+            lds_get8(&sm.km[i][c0], dkm);
+            lds_get8(&sm.kb[i][c0], dkb);
+            lds_get8(&sm.vb[i][c0], dvb);
+            lds_get8(&sm.dqg[i][c0], dqg);
+            lds_get8(&sm.dkg[i][c0], dkg);
+            float dbeta = 0.f, kgkg[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float kmv = sm.km[b][c0 + j];
-                dkp[j] = fmaf(l1, kmv, dkp[j]);
-                dqp[j] = fmaf(a1, kmv, dqp[j]);
-                dkm[j] = fmaf(l2, sm.kp[b][c0 + j], dkm[j]);
-                dkm[j] = fmaf(a2, sm.qp[b][c0 + j], dkm[j]);
+                const float qp = qn[j] * eq[j], kp = kn[j] * eq[j], km = kn[j] * ek[j];
+                const float qg = qn[j] * E[j], kg = kn[j] * kgl[j];
+                const float kb = round_bf(round_bf(kn[j] * beta) * E[j]);
+                dQN[j] += dqg[j] * E[j] + dqp[j] * eq[j];
+                dKN[j] += dkb[j] * beta * E[j] + dkg[j] * kgl[j] + dkp[j] * eq[j] + dkm[j] * ek[j];
+                dbeta = fmaf(dkb[j], kn[j] * E[j], dbeta);
+                dbeta = fmaf(dvb[j], hr.v[j], dbeta);
+                dv[j] = dvb[j] * beta;
+                const float d = LN2 * (dkb[j] * kb + dqg[j] * qg - dkg[j] * kg + dqp[j] * qp +
+                                       dkp[j] * kp - dkm[j] * km);
+                dG[j] = valid ? d : 0.f;
+                kgkg[j] = valid ? dkg[j] * kg : 0.f;
             }
-        }
-        float dbeta = 0.f, dv[8], dG[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float dqg = sm.dqg[i][c0 + j];
-            const float dkg = sm.dkg[i][c0 + j];
-            const float qp = qn[j] * eq[j], kp = kn[j] * eq[j], km = kn[j] * ek[j];
-            const float qg = qn[j] * E[j], kg = kn[j] * kgl[j];
-            const float kb = sm.kb[i][c0 + j];
-            dQN[j] += dqg * E[j] + dqp[j] * eq[j];
-            dKN[j] += dkb[j] * beta * E[j] + dkg * kgl[j] + dkp[j] * eq[j] + dkm[j] * ek[j];
-            dbeta = fmaf(dkb[j], kn[j] * E[j], dbeta);
-            dbeta = fmaf(dvb[j], vv[j], dbeta);
-            dv[j] = dvb[j] * beta;
-            dG[j] = LN2 * (dkb[j] * kb + dqg * qg - dkg * kg + dqp[j] * qp + dkp[j] * kp -
-                           dkm[j] * km);
-        }
-        dbeta = row_sum16(dbeta) + dbl;
-        if (valid) {
-            store8(p.dv + vrow + c0, dv);
-            if (cb == 0) {
-                const float db = p.use_beta_sigmoid ? dbeta * beta * (1.f - beta) : dbeta;
-                const int64_t bi = tok * HV + hv;
-                if (p.beta_bf16) static_cast<uint16_t*>(p.dbeta)[bi] = f2bf(db);
-                else static_cast<float*>(p.dbeta)[bi] = db;
+            dbeta = row_sum16(dbeta) + dbl;
+            if (valid) {
+                store8(p.dv + vrow + c0, dv);
+                if (cb == 0) {
+                    const float db = p.use_beta_sigmoid ? dbeta * beta * (1.f - beta) : dbeta;
+                    const int64_t bi = tok * HV + hv;
+                    if (p.beta_bf16) static_cast<uint16_t*>(p.dbeta)[bi] = f2bf(db);
+                    else static_cast<float*>(p.dbeta)[bi] = db;
+                }
             }
-        }
-        __syncthreads();  // every read of gsc, dkg and the 16x16 scratch is done
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            sm.gsc[i][c0 + j] = valid ? dG[j] : 0.f;
-            sm.dkg[i][c0 + j] = valid ? sm.dkg[i][c0 + j] * kn[j] * kgl[j] : 0.f;
+            // gsc and dkg are read only by their owning thread since phase 1
+            lds_put8(&sm.gsc[i][c0], dG);
+            lds_put8(&sm.dkg[i][c0], kgkg);
         }
         __syncthreads();
 
-        // ---- phase 7: per column, the last row's dG, the reverse cumsum of
-        // dG into dgate, and the gate (kernels.py:115-124) ------------------
+        // ---- phase 8: the last row's dG (through kg and the state decay),
+        // then per row the reverse cumsum of dG into dgate and the gate
+        // (kernels.py:115-124) -------------------------------------------
         if (t < DK) {
-            const int k = t;
-            float s = 0.f;
+            float s2 = 0.f;
 #pragma unroll
-            for (int r = 0; r < BT; ++r) s += sm.dkg[r][k];
-            sm.gsc[last][k] += LN2 * (s + sm.el[k] * sm.del[k]);
-            const float bk = (p.use_gate && p.dt_bias) ? p.dt_bias[hv * DK + k] : 0.f;
-            float run = 0.f, pdt = 0.f, pal = 0.f;
-            for (int r = nvalid - 1; r >= 0; --r) {
-                run += sm.gsc[r][k];
-                const int64_t gidx = ((sq.tok0 + c * BT + r) * HV + hv) * DK + k;
-                float dg;
-                if (p.use_gate) {
-                    const float graw = p.g_bf16 ? bf2f(static_cast<const uint16_t*>(p.g)[gidx])
-                                                : static_cast<const float*>(p.g)[gidx];
-                    const float sarg = graw + bk;
-                    const float sg = sigmoidf_(ea * sarg);
-                    dg = RCP_LN2 * run * p.lower_bound * sg * (1.f - sg) * ea;
-                    pdt += dg;
-                    pal = fmaf(dg, sarg, pal);
-                } else if (p.g_log) {
-                    dg = RCP_LN2 * run;
-                } else {
-                    dg = sm.gsc[r][k];
-                }
-                if (p.g_bf16) static_cast<uint16_t*>(p.dg)[gidx] = f2bf(dg);
-                else static_cast<float*>(p.dg)[gidx] = dg;
-            }
-            if (gate_grads) {
-                p.tr_part[rec * PART_STRIDE + k] = pdt;
-                float a = pal;
-                a += __shfl_xor(a, 1);
-                a += __shfl_xor(a, 2);
-                a += __shfl_xor(a, 4);
-                a += __shfl_xor(a, 8);
-                a += __shfl_xor(a, 16);
-                a += __shfl_xor(a, 32);
-                if (lane == 0) sm.red[w] = a;
-            }
+            for (int r = 0; r < BT; ++r) s2 += sm.dkg[r][t];
+            sm.gsc[last][t] += LN2 * (s2 + sm.el[t] * sm.del[t]);
         }
         __syncthreads();
-        if (gate_grads && t == 0) p.tr_part[rec * PART_STRIDE + DK] = sm.red[0] + sm.red[1];
+        {
+            float dg[8], suf[8], own[8];
+            lds_get8(&sm.gsc[i][c0], own);  // dG with the last row's terms
+#pragma unroll
+            for (int j = 0; j < 8; ++j) suf[j] = 0.f;
+#pragma unroll
+            for (int r = 0; r < BT; ++r) {
+                if (r >= i && r < nvalid) {
+                    float row[8];
+                    lds_get8(&sm.gsc[r][c0], row);
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) suf[j] += row[j];
+                }
+            }
+            float pdt[8], pal[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                float d;
+                if (p.use_gate) {
+                    const float sarg = hr.g[j] + hr.bias[j];
+                    const float sg = fast_sigmoid(ea * sarg);
+                    d = RCP_LN2 * suf[j] * p.lower_bound * sg * (1.f - sg) * ea;
+                    pdt[j] = valid ? d : 0.f;
+                    pal[j] = valid ? d * sarg : 0.f;
+                } else if (p.g_log) {
+                    d = RCP_LN2 * suf[j];
+                } else {
+                    d = own[j];
+                }
+                dg[j] = d;
+            }
+            if (valid) {
+                if (p.g_bf16) {
+                    store8(static_cast<uint16_t*>(p.dg) + vrow + c0, dg);
+                } else {
+                    float* dst = static_cast<float*>(p.dg) + vrow + c0;
+                    *reinterpret_cast<f32x4*>(dst) = f32x4{dg[0], dg[1], dg[2], dg[3]};
+                    *reinterpret_cast<f32x4*>(dst + 4) = f32x4{dg[4], dg[5], dg[6], dg[7]};
+                }
+            }
+            if (gate_grads) {
+                // column sums for ddt_bias, dA_log's terms, through the dead
+                // dqg / dw tiles
+                lds_put8(&sm.dqg[i][c0], pdt);
+                lds_put8(&sm.dw[i][c0], pal);
+            }
+        }
+        if (gate_grads) {
+            __syncthreads();
+            if (t < DK) {
+                float sdt = 0.f, sal = 0.f;
+#pragma unroll
+                for (int r = 0; r < BT; ++r) {
+                    sdt += sm.dqg[r][t];
+                    sal += sm.dw[r][t];
+                }
+                p.tr_part[rec * PART_STRIDE + t] = sdt;
+#pragma unroll
+                for (int o = 1; o < 64; o <<= 1) sal += __shfl_xor(sal, o);
+                if (lane == 0) sm.red[w] = sal;
+            }
+            __syncthreads();
+            if (t == 0) p.tr_part[rec * PART_STRIDE + DK] = sm.red[0] + sm.red[1];
+        }
+        __syncthreads();
     }
 
     // ---- l2norm backward, dq / dk summed over the group -------------------
@@ -611,27 +730,41 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
 }
 
 // dA_log[hv] and ddt_bias[hv, :] summed over the chunk partials of value
-// head hv, in record order.
-__global__ __launch_bounds__(DK) void gate_reduce_kernel(Params p) {
-    const int hv = blockIdx.x, t = threadIdx.x;
+// head hv in a fixed order: thread group j (of RG) sums records j, j + RG,
+// ..., then the groups' sums are added in group order.
+constexpr int RG = 8;
+
+__global__ __launch_bounds__(RG * DK) void gate_reduce_kernel(Params p) {
+    __shared__ float s_acc[RG][DK + 1];
+    const int hv = blockIdx.x, t = threadIdx.x & (DK - 1), grp = threadIdx.x / DK;
+    // records of value head hv: nb runs of nr consecutive records
+    const int nb = p.cu_seqlens ? 1 : p.B;
+    const int nr = p.cu_seqlens ? p.NS : p.NT;
     float acc = 0.f, accA = 0.f;
-    if (p.cu_seqlens) {
-        const float* base = p.tr_part + (int64_t)hv * p.NS * PART_STRIDE;
-        for (int x = 0; x < p.NS; ++x) {
+    for (int b = 0; b < nb; ++b) {
+        const int64_t first = p.cu_seqlens ? (int64_t)hv * p.NS : (int64_t)(b * p.HV + hv) * p.NT;
+        const float* base = p.tr_part + first * PART_STRIDE;
+#pragma unroll 4
+        for (int x = grp; x < nr; x += RG) {
             acc += base[(int64_t)x * PART_STRIDE + t];
             if (t == 0) accA += base[(int64_t)x * PART_STRIDE + DK];
         }
-    } else {
-        for (int b = 0; b < p.B; ++b) {
-            const float* base = p.tr_part + (int64_t)(b * p.HV + hv) * p.NT * PART_STRIDE;
-            for (int c = 0; c < p.NT; ++c) {
-                acc += base[(int64_t)c * PART_STRIDE + t];
-                if (t == 0) accA += base[(int64_t)c * PART_STRIDE + DK];
-            }
+    }
+    s_acc[grp][t] = acc;
+    if (t == 0) s_acc[grp][DK] = accA;
+    __syncthreads();
+    if (grp == 0) {
+        float a = 0.f;
+#pragma unroll
+        for (int j = 0; j < RG; ++j) a += s_acc[j][t];
+        if (p.ddt_bias) p.ddt_bias[hv * DK + t] = a;
+        if (t == 0 && p.dA_log) {
+            float aa = 0.f;
+#pragma unroll
+            for (int j = 0; j < RG; ++j) aa += s_acc[j][DK];
+            p.dA_log[hv] = aa;
         }
     }
-    if (p.ddt_bias) p.ddt_bias[hv * DK + t] = acc;
-    if (p.dA_log && t == 0) p.dA_log[hv] = accA;
 }
 
 }  // namespace
@@ -649,7 +782,7 @@ hipError_t launch_bwd_chunk(const Params& p, hipStream_t stream) {
 }
 
 hipError_t launch_bwd_gate_reduce(const Params& p, hipStream_t stream) {
-    hipLaunchKernelGGL(gate_reduce_kernel, dim3((unsigned)p.HV), dim3(DK), 0, stream, p);
+    hipLaunchKernelGGL(gate_reduce_kernel, dim3((unsigned)p.HV), dim3(RG * DK), 0, stream, p);
     return hipGetLastError();
 }
 

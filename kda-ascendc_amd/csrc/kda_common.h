@@ -67,13 +67,17 @@ constexpr int BREC_DECAY = 12800;
 constexpr int BREC_BYTES = 13312;
 static_assert(BREC_BYTES <= REC_BYTES && BREC_DECAY == REC_DECAY, "backward record fits a slot");
 
-// Training buffers per record slot (bf16, natural row-major layouts):
-// the state at the chunk's start h = bf16(S)^T [K][V], v_new [16][V], the
-// gradient of the state after the chunk dh [K][V] and dv_new [16][V]; and
-// per-chunk partial sums of the gate-parameter gradients: ddt_bias[128] then
-// dA_log at index 128.
+// Training buffers per record slot, bf16, blocked by 16-column value tile
+// so that each stage-2 work-group (one value tile) writes whole cache lines:
+// the state at the chunk's start h = bf16(S)^T as [vt][k][16] (element
+// (k, v) at (v/16 * 128 + k) * 16 + v%16), the gradient of the state after
+// the chunk dh likewise, and v_new, dv_new as [vt][row][16] (element
+// (row, v) at (v/16 * 16 + row) * 16 + v%16).  Plus per-chunk partial sums
+// of the gate-parameter gradients: ddt_bias[128], then dA_log at index 128.
 constexpr int TR_H_ELEMS = DK * DK;
 constexpr int TR_VN_ELEMS = BT * DK;
+constexpr int TR_H_TILE = DK * 16;   // elements of one value tile of h
+constexpr int TR_VN_TILE = BT * 16;  // elements of one value tile of v_new
 constexpr int PART_STRIDE = 132;
 
 // RCP_LN2 and the l2norm epsilon, kernels.py:38-39.

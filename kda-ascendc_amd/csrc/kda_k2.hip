@@ -199,8 +199,8 @@ struct Ctx {
     uint32_t u_off;             // copy: REC_U + 1024 * (vt / 2)
     uint16_t* obase;            // output: o[first token, hv, 16*vt + 4*((lane%16)/4)]
     int64_t orow_stride;        // output: elements between consecutive tokens of o
-    uint16_t* trh;              // training: h of the first record, column 16*vt + 4*((lane%16)/4)
-    uint16_t* trvn;             // training: v_new of the first record, same column
+    uint16_t* trh;              // training: h of the first record, this tile, column 4*((lane%16)/4)
+    uint16_t* trvn;             // training: v_new of the first record, likewise
     float scale;
     int NT, T, lane, q4, vt;    // NT chunks over T tokens (this sequence's)
 };
@@ -342,8 +342,9 @@ __device__ __forceinline__ void state_step(const Ctx& cx, f32x4 (&St)[8], StateO
 
 // Output wave, chunk c (slot S) after the barrier that ends chunk c + 1:
 // o = scale * qg @ hc^T + Aqk @ v_new (kernels.py:268-279).
-// TRAIN: instead of o, store the chunk's hc = bf16(S) as h = hc^T [K][V]
-// and v_new [16][V] (the backward's training buffers), each 16x16 tile
+// TRAIN: instead of o, store the chunk's hc = bf16(S) as h = hc^T and
+// v_new into the backward's training buffers (blocked by value tile, so a
+// k-tile of this work-group is 512 contiguous bytes), each 16x16 tile
 // quad-transposed to one 8-byte row piece per lane.
 template <int S, bool TRAIN>
 __device__ __forceinline__ void output_step(const Ctx& cx, int c) {
@@ -358,13 +359,13 @@ __device__ __forceinline__ void output_step(const Ctx& cx, int c) {
             const u32x2 t0 = quad_transpose(hc.x, hc.y, j4);
             const u32x2 t1 = quad_transpose(hc.z, hc.w, j4);
             const int k0 = 32 * j + 4 * cx.q4 + j4;  // row of k-tile 2j
-            __builtin_nontemporal_store(t0, reinterpret_cast<u32x2*>(hrec + (int64_t)k0 * DK));
-            __builtin_nontemporal_store(t1, reinterpret_cast<u32x2*>(hrec + (int64_t)(k0 + 16) * DK));
+            __builtin_nontemporal_store(t0, reinterpret_cast<u32x2*>(hrec + k0 * 16));
+            __builtin_nontemporal_store(t1, reinterpret_cast<u32x2*>(hrec + (k0 + 16) * 16));
         }
         const u32x2 vn = *reinterpret_cast<const u32x2*>(vn_buf[S % HANDOFF] + cx.lane * 8);
         const u32x2 vt = quad_transpose(vn.x, vn.y, j4);
         __builtin_nontemporal_store(
-            vt, reinterpret_cast<u32x2*>(cx.trvn + (int64_t)c * TR_VN_ELEMS + (4 * cx.q4 + j4) * DK));
+            vt, reinterpret_cast<u32x2*>(cx.trvn + (int64_t)c * TR_VN_ELEMS + (4 * cx.q4 + j4) * 16));
         return;
     }
     const uint8_t* slot = ring + S * SLOT;
@@ -470,8 +471,8 @@ __device__ __forceinline__ void output_wave(const Params& p, Ctx& cx, const SeqS
     const int x = cx.lane & 15;
     const int col = 16 * cx.vt + 4 * (x >> 2);
     if constexpr (TRAIN) {
-        cx.trh = p.tr_h + sp.rec0 * TR_H_ELEMS + col;
-        cx.trvn = p.tr_vn + sp.rec0 * TR_VN_ELEMS + col;
+        cx.trh = p.tr_h + sp.rec0 * TR_H_ELEMS + cx.vt * TR_H_TILE + 4 * (x >> 2);
+        cx.trvn = p.tr_vn + sp.rec0 * TR_VN_ELEMS + cx.vt * TR_VN_TILE + 4 * (x >> 2);
     } else {
         cx.obase = p.o + (sp.tok0 * p.HV + hv) * DK + col;
         cx.orow_stride = (int64_t)p.HV * DK;
