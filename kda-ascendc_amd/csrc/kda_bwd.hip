@@ -8,10 +8,9 @@
 // recompute (stage 1, then stage 2 storing bf16 h and v_new per chunk, then
 // stage 1 again writing the backward records):
 //
-//   bwd_state_kernel  one wave per (sequence, value head, 16 value
-//                     columns), chunks in reverse order, the state gradient
-//                     dh [K, 16] resident in eight 16x16 fp32 accumulator
-//                     tiles (the forward stage 2's layout):
+//   k2_kernel<K2_BWD> (kda_k2.hip) the reverse recurrence of the state
+//                     gradient dh, stage 2's three-wave layout run over
+//                     the backward records in reverse chunk order:
 //                       dv_new = Aqk^T dO + kg dh'
 //                       dh     = 2^G_last * dh' + (scale qg)^T dO - w^T dv_new
 //                     storing bf16 dh' (the gradient of the state after the
@@ -37,142 +36,6 @@ namespace kda {
 namespace {
 
 constexpr float LN2 = 0.6931471805599453f;
-
-// ---------------------------------------------------------------------------
-// Reverse state chain.
-// ---------------------------------------------------------------------------
-
-// The operands of one chunk step (backward record, kda_common.h, and dO).
-struct BwdOps {
-    u32x4 kg[4];
-    u32x4 upd[8];
-    u32x2 aqkT;
-    f32x4 dec[8];
-    u32x2 dop;  // dO[4*q4 + i][16*vt + x] as the 16x16x16 B operand
-};
-
-__device__ __forceinline__ void load_bwd_ops(const uint8_t* rec, const uint16_t* drow, bool dvalid,
-                                             int lane, int q4, BwdOps& op) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-        op.kg[j] = *reinterpret_cast<const u32x4*>(rec + BREC_KG + j * 1024 + lane * 16);
-#pragma unroll
-    for (int kt = 0; kt < 8; ++kt)
-        op.upd[kt] = *reinterpret_cast<const u32x4*>(rec + BREC_UPD + kt * 1024 + lane * 16);
-    op.aqkT = *reinterpret_cast<const u32x2*>(rec + BREC_AQKT + lane * 8);
-#pragma unroll
-    for (int kt = 0; kt < 8; ++kt)
-        op.dec[kt] = *reinterpret_cast<const f32x4*>(rec + BREC_DECAY + kt * 64 + q4 * 16);
-    op.dop = u32x2{0u, 0u};
-    if (dvalid) op.dop = *reinterpret_cast<const u32x2*>(drow);
-}
-
-// Fp32 [K, V] tile slice of lane (x, q4), v = 16*vt + x: D[kt][i] = M[16*kt + 4*q4 + i][v]
-// for a state stored [V, K] (v_first) or [K, V].
-__device__ __forceinline__ void load_state_T(const float* src, bool v_first, int v, int q4,
-                                             f32x4 (&D)[8]) {
-#pragma unroll
-    for (int kt = 0; kt < 8; ++kt) {
-        D[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (src) {
-            const int k0 = 16 * kt + 4 * q4;
-            if (v_first) {
-                D[kt] = *reinterpret_cast<const f32x4*>(src + (int64_t)v * DK + k0);
-            } else {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) D[kt][i] = src[(int64_t)(k0 + i) * DK + v];
-            }
-        }
-    }
-}
-
-__device__ __forceinline__ void store_state_T(float* dst, bool v_first, int v, int q4,
-                                              const f32x4 (&D)[8]) {
-    if (!dst) return;
-#pragma unroll
-    for (int kt = 0; kt < 8; ++kt) {
-        const int k0 = 16 * kt + 4 * q4;
-        if (v_first) {
-            *reinterpret_cast<f32x4*>(dst + (int64_t)v * DK + k0) = D[kt];
-        } else {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) dst[(int64_t)(k0 + i) * DK + v] = D[kt][i];
-        }
-    }
-}
-
-__global__ __launch_bounds__(64) void bwd_state_kernel(Params p) {
-    const int lane = threadIdx.x;
-    const int x = lane & 15, q4 = lane >> 4, j4 = lane & 3;
-    const int nbh = (p.cu_seqlens ? p.N : p.B) * p.HV;
-    // XCD-aware as stage 2: the 8 value tiles of a head share one L2.
-    const int wg = blockIdx.x;
-    const int lin = (wg & 7) * nbh + (wg >> 3);
-    const int bh = lin >> 3;
-    const int vt = lin & 7;
-    const int hv = bh - (bh / p.HV) * p.HV;
-    const SeqSpan sp = seq_span(p, bh);
-    const int v = 16 * vt + x;
-    const int64_t sbase = (int64_t)bh * DK * DK;
-    const bool v_first = p.h0_v_first != 0;
-
-    f32x4 D[8];
-    load_state_T(p.dht ? p.dht + sbase : nullptr, v_first, v, q4, D);
-    if (sp.nt > 0) {
-        const int col = 16 * vt + 4 * (x >> 2);
-        const uint8_t* recs = p.ws + sp.rec0 * REC_BYTES;
-        uint16_t* dh_out = p.tr_dh + sp.rec0 * TR_H_ELEMS + vt * TR_H_TILE + 4 * (x >> 2);
-        uint16_t* dvn_out = p.tr_dvn + sp.rec0 * TR_VN_ELEMS + vt * TR_VN_TILE + 4 * (x >> 2);
-        // this lane's dO row piece: token 16*c + 4*q4 + j4, columns col..col+3
-        const int64_t dstride = (int64_t)p.HV * DK;
-        const uint16_t* dbase = p.dout + (sp.tok0 * p.HV + hv) * DK + col;
-        auto drow = [&](int c) { return dbase + (int64_t)(c * BT + 4 * q4 + j4) * dstride; };
-        auto dval = [&](int c) { return c * BT + 4 * q4 + j4 < sp.len; };
-
-        BwdOps cur, nxt;
-        int c = sp.nt - 1;
-        load_bwd_ops(recs + (int64_t)c * REC_BYTES, drow(c), dval(c), lane, q4, cur);
-        for (; c >= 0; --c) {
-            if (c > 0)
-                load_bwd_ops(recs + (int64_t)(c - 1) * REC_BYTES, drow(c - 1), dval(c - 1), lane,
-                             q4, nxt);
-            // dh' = the gradient of the state after chunk c, as bf16 B operands
-            u32x4 hb[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                hb[j] = u32x4{pack2(D[2 * j][0], D[2 * j][1]), pack2(D[2 * j][2], D[2 * j][3]),
-                              pack2(D[2 * j + 1][0], D[2 * j + 1][1]),
-                              pack2(D[2 * j + 1][2], D[2 * j + 1][3])};
-            const u32x2 dt = quad_transpose(cur.dop.x, cur.dop.y, j4);
-            const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-            f32x4 dvn = mfma_bf16_16x16x16(as_i16x4(cur.aqkT), as_i16x4(dt), zero);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) dvn = mfma_bf16_16x16x32(as_bf16x8(cur.kg[j]), as_bf16x8(hb[j]), dvn);
-            // store dh' row pieces (after the products have their operands)
-            uint16_t* dhc = dh_out + (int64_t)c * TR_H_ELEMS;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const u32x2 t0 = quad_transpose(hb[j].x, hb[j].y, j4);
-                const u32x2 t1 = quad_transpose(hb[j].z, hb[j].w, j4);
-                const int k0 = 32 * j + 4 * q4 + j4;
-                *reinterpret_cast<u32x2*>(dhc + k0 * 16) = t0;
-                *reinterpret_cast<u32x2*>(dhc + (k0 + 16) * 16) = t1;
-            }
-            const u32x2 dvb = {pack2(dvn[0], dvn[1]), pack2(dvn[2], dvn[3])};
-            const u32x2 dvt = quad_transpose(dvb.x, dvb.y, j4);
-            *reinterpret_cast<u32x2*>(dvn_out + (int64_t)c * TR_VN_ELEMS + (4 * q4 + j4) * 16) = dvt;
-            // dh = 2^G_last * dh' + [scale qg | -w]^T [dO ; dv_new]
-            const u32x4 bop = {dt.x, dt.y, dvb.x, dvb.y};
-#pragma unroll
-            for (int kt = 0; kt < 8; ++kt) {
-                D[kt] = D[kt] * cur.dec[kt];
-                D[kt] = mfma_bf16_16x16x32(as_bf16x8(cur.upd[kt]), as_bf16x8(bop), D[kt]);
-            }
-            if (c > 0) cur = nxt;
-        }
-    }
-    store_state_T(p.dh0 ? p.dh0 + sbase : nullptr, v_first, v, q4, D);
-}
 
 // ---------------------------------------------------------------------------
 // Per-chunk gradients.
@@ -237,7 +100,15 @@ __device__ __forceinline__ float row_sum16(float s) {
 // One value head's row data of this thread (row i, columns c0 .. c0+7).
 struct HvRow {
     float v[8], g[8], dvn[8], bias[8];
-    float beta;
+    float beta, alog;
+};
+
+// One value head's matrix-op operands for the products over V (wave w:
+// k-tiles 2w, 2w+1), loaded ahead of the intra-chunk work so that their
+// latency overlaps it.
+struct HdhOps {
+    u32x4 bh[4][2], bd[4][2];      // h, dh' rows 16*kt + x, v 32*jv + 8*q4 .. +7
+    u32x4 a_do[4], a_dv[4], a_vn[4];  // dO, dv_new, v_new row x, same v
 };
 
 __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
@@ -315,6 +186,36 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
             r.beta = p.beta_bf16 ? bf2f(static_cast<const uint16_t*>(p.beta)[bi])
                                  : static_cast<const float*>(p.beta)[bi];
         }
+        r.alog = p.use_gate ? p.A_log[hv] : 0.f;
+    };
+    auto load_ops = [&](int hv, HdhOps& o) {
+        const int64_t rec = seq_span(p, seq * HV + hv).rec0 + c;
+        const bool xv = x < nvalid;
+        const uint16_t* hrec = p.tr_h + rec * TR_H_ELEMS;
+        const uint16_t* dhrec = p.tr_dh + rec * TR_H_ELEMS;
+        // blocked layouts: v = 32*jv + 8*q4 + e lies in value tile
+        // 2*jv + q4/2 at column 8*(q4%2) + e
+        const int64_t vnoff = (q4 >> 1) * TR_VN_TILE + x * 16 + 8 * (q4 & 1);
+        const uint16_t* vnrec = p.tr_vn + rec * TR_VN_ELEMS + vnoff;
+        const uint16_t* dvrec = p.tr_dvn + rec * TR_VN_ELEMS + vnoff;
+        const uint16_t* dorow = p.dout + ((sq.tok0 + c * BT + x) * HV + hv) * DK + 8 * q4;
+#pragma unroll
+        for (int jv = 0; jv < 4; ++jv) {
+            o.a_do[jv] = o.a_dv[jv] = o.a_vn[jv] = u32x4{0u, 0u, 0u, 0u};
+            if (xv) {
+                o.a_do[jv] = *reinterpret_cast<const u32x4*>(dorow + 32 * jv);
+                o.a_dv[jv] = *reinterpret_cast<const u32x4*>(dvrec + 2 * jv * TR_VN_TILE);
+                o.a_vn[jv] = *reinterpret_cast<const u32x4*>(vnrec + 2 * jv * TR_VN_TILE);
+            }
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                const int kt = 2 * w + tt;
+                const int64_t off = (2 * jv + (q4 >> 1)) * TR_H_TILE + (16 * kt + x) * 16 +
+                                    8 * (q4 & 1);
+                o.bh[jv][tt] = *reinterpret_cast<const u32x4*>(hrec + off);
+                o.bd[jv][tt] = *reinterpret_cast<const u32x4*>(dhrec + off);
+            }
+        }
     };
 
     // ---- q^, k^ (kernels.py:108-113), once per q/k head ------------------
@@ -322,7 +223,9 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
     load8(p.q + (tok * H + h) * DK + c0, valid, qv);
     load8(p.k + (tok * H + h) * DK + c0, valid, kv);
     HvRow hr;
+    HdhOps ops;
     load_hv(h * rep, hr);
+    load_ops(h * rep, ops);
     float rq = 1.f, rk = 1.f;
     if (p.use_l2norm) {
         float sq2 = 0.f, sk2 = 0.f;
@@ -347,7 +250,10 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
 
     for (int gi = 0; gi < rep; ++gi) {
         const int hv = h * rep + gi;
-        if (gi > 0) load_hv(hv, hr);
+        if (gi > 0) {
+            load_hv(hv, hr);
+            load_ops(hv, ops);
+        }
         const SeqSpan sp = seq_span(p, seq * HV + hv);
         const int64_t rec = sp.rec0 + c;
         const int64_t vrow = (tok * HV + hv) * DK;  // v/g/dO element offset of row i
@@ -355,7 +261,7 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
         // ---- phase 1: gates, cumsum, recentred operands ------------------
         float beta = hr.beta;
         if (p.use_beta_sigmoid) beta = valid ? fast_sigmoid(hr.beta) : 0.f;
-        const float ea = p.use_gate ? expf(p.A_log[hv]) : 0.f;
+        const float ea = p.use_gate ? expf(hr.alog) : 0.f;
         {
             float gv[8];
 #pragma unroll
@@ -408,37 +314,18 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
         // dv_new / v_new and row 16*kt + x of h / dh', v columns
         // 32*jv + 8*q4 .. +7, as 16x16x32 operands.
         {
-            const bool xv = x < nvalid;
-            const uint16_t* hrec = p.tr_h + rec * TR_H_ELEMS;
-            const uint16_t* dhrec = p.tr_dh + rec * TR_H_ELEMS;
-            // blocked layouts: v = 32*jv + 8*q4 + e lies in value tile
-            // 2*jv + q4/2 at column 8*(q4%2) + e
-            const int64_t vnoff = (q4 >> 1) * TR_VN_TILE + x * 16 + 8 * (q4 & 1);
-            const uint16_t* vnrec = p.tr_vn + rec * TR_VN_ELEMS + vnoff;
-            const uint16_t* dvrec = p.tr_dvn + rec * TR_VN_ELEMS + vnoff;
-            const uint16_t* dorow = p.dout + ((sq.tok0 + c * BT + x) * HV + hv) * DK + 8 * q4;
             f32x4 aq[2], aw[2], ak[2], adq = {0.f, 0.f, 0.f, 0.f};
             float pel[2] = {0.f, 0.f};
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) aq[tt] = aw[tt] = ak[tt] = adq;
 #pragma unroll
             for (int jv = 0; jv < 4; ++jv) {
-                u32x4 a_do = {0u, 0u, 0u, 0u}, a_dv = {0u, 0u, 0u, 0u}, a_vn = {0u, 0u, 0u, 0u};
-                if (xv) {
-                    a_do = *reinterpret_cast<const u32x4*>(dorow + 32 * jv);
-                    a_dv = *reinterpret_cast<const u32x4*>(dvrec + 2 * jv * TR_VN_TILE);
-                    a_vn = *reinterpret_cast<const u32x4*>(vnrec + 2 * jv * TR_VN_TILE);
-                }
 #pragma unroll
                 for (int tt = 0; tt < 2; ++tt) {
-                    const int kt = 2 * w + tt;
-                    const int64_t off = (2 * jv + (q4 >> 1)) * TR_H_TILE + (16 * kt + x) * 16 +
-                                        8 * (q4 & 1);
-                    const u32x4 bh = *reinterpret_cast<const u32x4*>(hrec + off);
-                    const u32x4 bd = *reinterpret_cast<const u32x4*>(dhrec + off);
-                    aq[tt] = mfma_bf16_16x16x32(as_bf16x8(a_do), as_bf16x8(bh), aq[tt]);
-                    aw[tt] = mfma_bf16_16x16x32(as_bf16x8(a_dv), as_bf16x8(bh), aw[tt]);
-                    ak[tt] = mfma_bf16_16x16x32(as_bf16x8(a_vn), as_bf16x8(bd), ak[tt]);
+                    const u32x4 bh = ops.bh[jv][tt], bd = ops.bd[jv][tt];
+                    aq[tt] = mfma_bf16_16x16x32(as_bf16x8(ops.a_do[jv]), as_bf16x8(bh), aq[tt]);
+                    aw[tt] = mfma_bf16_16x16x32(as_bf16x8(ops.a_dv[jv]), as_bf16x8(bh), aw[tt]);
+                    ak[tt] = mfma_bf16_16x16x32(as_bf16x8(ops.a_vn[jv]), as_bf16x8(bd), ak[tt]);
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         pel[tt] = fmaf(__builtin_bit_cast(float, bh[e] << 16),
@@ -447,7 +334,8 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
                                        __builtin_bit_cast(float, bd[e] & 0xffff0000u), pel[tt]);
                     }
                 }
-                if (w == 0) adq = mfma_bf16_16x16x32(as_bf16x8(a_do), as_bf16x8(a_vn), adq);
+                if (w == 0)
+                    adq = mfma_bf16_16x16x32(as_bf16x8(ops.a_do[jv]), as_bf16x8(ops.a_vn[jv]), adq);
             }
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
@@ -768,12 +656,6 @@ __global__ __launch_bounds__(RG * DK) void gate_reduce_kernel(Params p) {
 }
 
 }  // namespace
-
-hipError_t launch_bwd_state(const Params& p, hipStream_t stream) {
-    const int64_t grid = (int64_t)(p.cu_seqlens ? p.N : p.B) * p.HV * 8;
-    hipLaunchKernelGGL(bwd_state_kernel, dim3((unsigned)grid), dim3(64), 0, stream, p);
-    return hipGetLastError();
-}
 
 hipError_t launch_bwd_chunk(const Params& p, hipStream_t stream) {
     const int64_t grid = p.cu_seqlens ? (int64_t)p.H * p.NS : (int64_t)p.B * p.H * p.NT;

@@ -281,7 +281,7 @@ int kda_bt16_bwd_hip(const KdaBt16BwdArgs* b, void* stream) {
     if (kda::launch_k1(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
     if (kda::launch_k2_train(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
     if (kda::launch_k1_bwd_records(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
-    if (kda::launch_bwd_state(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
+    if (kda::launch_k2_bwd(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
     if (kda::launch_bwd_chunk(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
     if (p.tr_part && kda::launch_bwd_gate_reduce(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
     return KDA_BT16_OK;

@@ -60,12 +60,18 @@ constexpr int REC_BYTES = 17408;
 //                         the A operand of dh[kt] += [scale*qg | -w]^T @ [dO ; dv_new]
 //   12288   512    AqkT   bf16, [lane][i] = Aqk[4*q4+i][r]: the A operand of Aqk^T @ dO
 //   12800   512    decay  fp32, as REC_DECAY
+//   13312   4096   dO     bf16, [vt][lane][i] = dO[4*q4+i][16*vt+r]: each value
+//                         tile's B operand, where the forward record holds u
+// The shared part and the per-tile slices sit where the forward record's
+// do, so stage 2's record ring streams either kind unchanged.
 constexpr int BREC_KG = 0;
 constexpr int BREC_UPD = 4096;
 constexpr int BREC_AQKT = 12288;
 constexpr int BREC_DECAY = 12800;
-constexpr int BREC_BYTES = 13312;
-static_assert(BREC_BYTES <= REC_BYTES && BREC_DECAY == REC_DECAY, "backward record fits a slot");
+constexpr int BREC_DO = 13312;
+constexpr int BREC_BYTES = 17408;
+static_assert(BREC_BYTES == REC_BYTES && BREC_DECAY == REC_DECAY && BREC_DO == REC_U,
+              "backward record has the forward record's shape");
 
 // Training buffers per record slot, bf16, blocked by 16-column value tile
 // so that each stage-2 work-group (one value tile) writes whole cache lines:
@@ -313,7 +319,7 @@ hipError_t launch_recurrent(const Params& p, hipStream_t stream);
 // Backward (kda_bt16_bwd.hip, and the training variants of the stages).
 hipError_t launch_k1_bwd_records(const Params& p, hipStream_t stream);
 hipError_t launch_k2_train(const Params& p, hipStream_t stream);
-hipError_t launch_bwd_state(const Params& p, hipStream_t stream);
+hipError_t launch_k2_bwd(const Params& p, hipStream_t stream);
 hipError_t launch_bwd_chunk(const Params& p, hipStream_t stream);
 hipError_t launch_bwd_gate_reduce(const Params& p, hipStream_t stream);
 }  // namespace kda

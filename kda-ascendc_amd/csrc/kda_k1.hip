@@ -306,6 +306,22 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k1
                     reinterpret_cast<u32x4*>(rec + BREC_UPD + kt * 1024 + lane * 16));
             }
         }
+        // dO as the B operand of each value tile (T order, the layout of u
+        // in the forward record): [vt][lane][i] = dO[4*q4 + i][16*vt + r].
+        {
+            Row32 dop;
+            load_row(p.dout + vrowoff, valid, colbase, dop);
+            __syncthreads();
+#pragma unroll
+            for (int kt = 0; kt < 8; ++kt) lds_put(s_T, r, colbase, kt, dop.v[kt]);
+            __syncthreads();
+            i16x4 doT[8];
+            load_lds_T(s_T, r, q4, doT);
+#pragma unroll
+            for (int vt = 0; vt < 8; ++vt)
+                __builtin_nontemporal_store(__builtin_bit_cast(u32x2, doT[vt]),
+                                            reinterpret_cast<u32x2*>(rec + BREC_DO + vt * 512 + lane * 8));
+        }
         // kg = bf16(k^ * 2^(G_last - G)) in F order (the A operand of
         // kg @ dh), and the decay 2^G_last.
         u32x2 kgF[8];

@@ -201,6 +201,7 @@ struct Ctx {
     int64_t orow_stride;        // output: elements between consecutive tokens of o
     uint16_t* trh;              // training: h of the first record, this tile, column 4*((lane%16)/4)
     uint16_t* trvn;             // training: v_new of the first record, likewise
+    int rev;                    // backward: step c handles chunk NT - 1 - c
     float scale;
     int NT, T, lane, q4, vt;    // NT chunks over T tokens (this sequence's)
 };
@@ -346,15 +347,18 @@ __device__ __forceinline__ void state_step(const Ctx& cx, f32x4 (&St)[8], StateO
 // v_new into the backward's training buffers (blocked by value tile, so a
 // k-tile of this work-group is 512 contiguous bytes), each 16x16 tile
 // quad-transposed to one 8-byte row piece per lane.
-template <int S, bool TRAIN>
+// Two store waves share that work (PART 0: k-tiles 0-3, PART 1: k-tiles
+// 4-7 and v_new); a single wave would fall behind the state wave.
+template <int S, bool TRAIN, int PART>
 __device__ __forceinline__ void output_step(const Ctx& cx, int c) {
     chunk_barrier();
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (TRAIN) {
         const int j4 = cx.lane & 3;
-        uint16_t* hrec = cx.trh + (int64_t)c * TR_H_ELEMS;
+        const int cs = cx.rev ? cx.NT - 1 - c : c;  // the chunk of step c
+        uint16_t* hrec = cx.trh + (int64_t)cs * TR_H_ELEMS;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 2 * PART; j < 2 * PART + 2; ++j) {
             const u32x4 hc = *reinterpret_cast<const u32x4*>(hc_buf[S % HANDOFF] + j * 1024 + cx.lane * 16);
             const u32x2 t0 = quad_transpose(hc.x, hc.y, j4);
             const u32x2 t1 = quad_transpose(hc.z, hc.w, j4);
@@ -362,10 +366,12 @@ __device__ __forceinline__ void output_step(const Ctx& cx, int c) {
             __builtin_nontemporal_store(t0, reinterpret_cast<u32x2*>(hrec + k0 * 16));
             __builtin_nontemporal_store(t1, reinterpret_cast<u32x2*>(hrec + (k0 + 16) * 16));
         }
-        const u32x2 vn = *reinterpret_cast<const u32x2*>(vn_buf[S % HANDOFF] + cx.lane * 8);
-        const u32x2 vt = quad_transpose(vn.x, vn.y, j4);
-        __builtin_nontemporal_store(
-            vt, reinterpret_cast<u32x2*>(cx.trvn + (int64_t)c * TR_VN_ELEMS + (4 * cx.q4 + j4) * 16));
+        if (PART == 1) {
+            const u32x2 vn = *reinterpret_cast<const u32x2*>(vn_buf[S % HANDOFF] + cx.lane * 8);
+            const u32x2 vt = quad_transpose(vn.x, vn.y, j4);
+            __builtin_nontemporal_store(
+                vt, reinterpret_cast<u32x2*>(cx.trvn + (int64_t)cs * TR_VN_ELEMS + (4 * cx.q4 + j4) * 16));
+        }
         return;
     }
     const uint8_t* slot = ring + S * SLOT;
@@ -397,11 +403,16 @@ __device__ __forceinline__ void output_step(const Ctx& cx, int c) {
         __builtin_nontemporal_store(ot, reinterpret_cast<u32x2*>(cx.obase + (int64_t)t * cx.orow_stride));
 }
 
+// Record offset of step c's chunk (in reverse order for the backward).
+__device__ __forceinline__ uint32_t step_rec(const Ctx& cx, int c) {
+    return (uint32_t)(cx.rev ? cx.NT - 1 - c : c) * REC_BYTES;
+}
+
 // Copy wave, chunk c (slot S).
 template <int S>
 __device__ __forceinline__ void copy_step(const Ctx& cx, int c) {
     if (c + LEAD < cx.NT)
-        issue_chunk(cx.rs, (uint32_t)(c + LEAD) * REC_BYTES,
+        issue_chunk(cx.rs, step_rec(cx, c + LEAD),
                     ring_lds() + ((S + LEAD) % RING) * SLOT, cx.u_off, cx.voff16);
     // chunk c + 2 is read by the state wave after this barrier
     if (c + 2 < cx.NT) wait_chunk(min(LEAD - 2, cx.NT - 3 - c));
@@ -432,11 +443,11 @@ __device__ __forceinline__ void state_round_tail(const Ctx& cx, int c, f32x4 (&S
     if constexpr (N > 1) state_round_tail<(S + 1) % RING, N - 1>(cx, c + 1, St, op, vn);
 }
 
-template <int S, bool TRAIN>
+template <int S, bool TRAIN, int PART>
 __device__ __forceinline__ void output_round(const Ctx& cx, int c) {
-    output_step<S, TRAIN>(cx, c);
+    output_step<S, TRAIN, PART>(cx, c);
     if constexpr (S + 1 < RING) {
-        if (c + 1 < cx.NT) output_round<S + 1, TRAIN>(cx, c + 1);
+        if (c + 1 < cx.NT) output_round<S + 1, TRAIN, PART>(cx, c + 1);
     }
 }
 
@@ -457,8 +468,7 @@ __device__ __forceinline__ void copy_wave(const Params& p, Ctx& cx, const SeqSpa
 #pragma unroll
     for (int d = 0; d < LEAD; ++d)
         if (d < NT)
-            issue_chunk(cx.rs, (uint32_t)d * REC_BYTES, ring_lds() + d * SLOT, cx.u_off,
-                        cx.voff16);
+            issue_chunk(cx.rs, step_rec(cx, d), ring_lds() + d * SLOT, cx.u_off, cx.voff16);
     // chunks 0 and 1 (those that exist) before the first barrier
     wait_chunk(NT >= 2 ? min(LEAD, NT) - 2 : 0);
     copy_barrier();
@@ -466,20 +476,214 @@ __device__ __forceinline__ void copy_wave(const Params& p, Ctx& cx, const SeqSpa
     copy_barrier();  // the output wave's last chunk
 }
 
-template <bool TRAIN>
+template <bool TRAIN, int PART>
 __device__ __forceinline__ void output_wave(const Params& p, Ctx& cx, const SeqSpan& sp, int hv) {
     const int x = cx.lane & 15;
     const int col = 16 * cx.vt + 4 * (x >> 2);
     if constexpr (TRAIN) {
-        cx.trh = p.tr_h + sp.rec0 * TR_H_ELEMS + cx.vt * TR_H_TILE + 4 * (x >> 2);
-        cx.trvn = p.tr_vn + sp.rec0 * TR_VN_ELEMS + cx.vt * TR_VN_TILE + 4 * (x >> 2);
+        // forward recompute: h and v_new; backward: dh' and dv_new
+        uint16_t* bh = cx.rev ? p.tr_dh : p.tr_h;
+        uint16_t* bv = cx.rev ? p.tr_dvn : p.tr_vn;
+        cx.trh = bh + sp.rec0 * TR_H_ELEMS + cx.vt * TR_H_TILE + 4 * (x >> 2);
+        cx.trvn = bv + sp.rec0 * TR_VN_ELEMS + cx.vt * TR_VN_TILE + 4 * (x >> 2);
     } else {
         cx.obase = p.o + (sp.tok0 * p.HV + hv) * DK + col;
         cx.orow_stride = (int64_t)p.HV * DK;
     }
     chunk_barrier();
     chunk_barrier();
-    for (int c = 0; c < cx.NT; c += RING) output_round<0, TRAIN>(cx, c);
+    for (int c = 0; c < cx.NT; c += RING) output_round<0, TRAIN, PART>(cx, c);
+}
+
+// ---------------------------------------------------------------------------
+// Backward: the reverse recurrence of the state gradient dh (K x 16 of this
+// value tile, the layout of S^T above).  Step c handles chunk NT - 1 - c:
+//   dv_new = Aqk^T dO + kg dh'
+//   dh     = 2^G_last * dh' + [scale qg | -w]^T [dO ; dv_new]
+// with dh' the gradient of the state after the chunk.  The record (stage
+// 1's backward record) holds every operand in register order: kg where the
+// forward keeps w, the eight [scale qg | -w]^T tiles over qg and kg, Aqk^T
+// over Aqk, and this tile's dO where the forward keeps u.  dh' and dv_new go
+// to the output wave through the hand-off, as hc and v_new do forward.
+// ---------------------------------------------------------------------------
+
+struct BwdStateOps {
+    u32x4 kg[4];
+    u32x4 upd[8];
+    u32x2 aqkT;
+    u32x2 dop;
+    f32x2 dc;
+};
+
+__device__ __forceinline__ void read_bwd_ops(const uint8_t* slot, int lane, int vt, BwdStateOps& op) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        op.kg[j] = *reinterpret_cast<const u32x4*>(slot + BREC_KG + j * 1024 + lane * 16);
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt)
+        op.upd[kt] = *reinterpret_cast<const u32x4*>(slot + BREC_UPD + kt * 1024 + lane * 16);
+    op.aqkT = *reinterpret_cast<const u32x2*>(slot + BREC_AQKT + lane * 8);
+    op.dop = *reinterpret_cast<const u32x2*>(slot + REC_SHARED + (vt & 1) * 512 + lane * 8);
+    op.dc = *reinterpret_cast<const f32x2*>(slot + decay_offset(lane));
+}
+
+// dh[kt] = 2^G_last * dh[kt] + upd[kt] @ [dO ; dv_new] for one step's ops.
+template <int KT>
+__device__ __forceinline__ void bwd_update(f32x4 (&D)[8], const BwdStateOps& o, const u32x4& bop) {
+    D[KT] = decay_tile<KT>(D[KT], o.dc);
+    D[KT] = mfma_bf16_16x16x32(as_bf16x8(o.upd[KT]), as_bf16x8(bop), D[KT]);
+}
+
+__device__ __forceinline__ u32x4 pack_tiles(const f32x4& a, const f32x4& b) {
+    return u32x4{pack2(a[0], a[1]), pack2(a[2], a[3]), pack2(b[0], b[1]), pack2(b[2], b[3])};
+}
+
+// Step c in slot S, software-pipelined as the forward's state_step: it
+// starts with step c - 1's update, tile by tile, and runs this step's
+// kg @ dh' chain as soon as the tiles it needs are updated.  op[(S+1) & 1]
+// holds step c - 1's operands until its update is done, then receives step
+// c + 1's; bop carries [dO ; dv_new] of step c - 1 in, of step c out.
+template <int S, bool HAS_PREV, bool HAS_NEXT>
+__device__ __forceinline__ void bwd_state_step(const Ctx& cx, f32x4 (&D)[8], BwdStateOps (&op)[2],
+                                               u32x4& bop) {
+    const BwdStateOps& cur = op[S & 1];
+    BwdStateOps& oth = op[(S + 1) & 1];
+    const uint8_t* ns = ring + ((S + 1) % RING) * SLOT;
+    uint8_t* hbuf = hc_buf[S % HANDOFF] + cx.lane * 16;
+#define KDA_FENCE() __builtin_amdgcn_sched_barrier(0)
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    f32x4 dvn = mfma_bf16_16x16x16(as_i16x4(cur.aqkT), as_i16x4(cur.dop), zero);
+    if (HAS_PREV) {
+        bwd_update<0>(D, oth, bop);
+        bwd_update<1>(D, oth, bop);
+    }
+    KDA_FENCE();
+    const u32x4 hb0 = pack_tiles(D[0], D[1]);
+    dvn = mfma_bf16_16x16x32(as_bf16x8(cur.kg[0]), as_bf16x8(hb0), dvn);
+    if (HAS_PREV) {
+        bwd_update<2>(D, oth, bop);
+        bwd_update<3>(D, oth, bop);
+    }
+    *reinterpret_cast<u32x4*>(hbuf + 0 * 1024) = hb0;
+    KDA_FENCE();
+    const u32x4 hb1 = pack_tiles(D[2], D[3]);
+    dvn = mfma_bf16_16x16x32(as_bf16x8(cur.kg[1]), as_bf16x8(hb1), dvn);
+    if (HAS_PREV) {
+        bwd_update<4>(D, oth, bop);
+        bwd_update<5>(D, oth, bop);
+    }
+    *reinterpret_cast<u32x4*>(hbuf + 1 * 1024) = hb1;
+    KDA_FENCE();
+    const u32x4 hb2 = pack_tiles(D[4], D[5]);
+    dvn = mfma_bf16_16x16x32(as_bf16x8(cur.kg[2]), as_bf16x8(hb2), dvn);
+    if (HAS_PREV) {
+        bwd_update<6>(D, oth, bop);
+        bwd_update<7>(D, oth, bop);
+    }
+    *reinterpret_cast<u32x4*>(hbuf + 2 * 1024) = hb2;
+    KDA_FENCE();
+    const u32x4 hb3 = pack_tiles(D[6], D[7]);
+    dvn = mfma_bf16_16x16x32(as_bf16x8(cur.kg[3]), as_bf16x8(hb3), dvn);
+    *reinterpret_cast<u32x4*>(hbuf + 3 * 1024) = hb3;
+    if (HAS_NEXT) read_bwd_ops(ns, cx.lane, cx.vt, oth);
+    KDA_FENCE();
+    const u32x2 dvb = {pack2(dvn[0], dvn[1]), pack2(dvn[2], dvn[3])};
+    *reinterpret_cast<u32x2*>(vn_buf[S % HANDOFF] + cx.lane * 8) = dvb;
+    bop = u32x4{cur.dop.x, cur.dop.y, dvb.x, dvb.y};
+    if (HAS_NEXT) {
+        chunk_barrier_nodrain();
+    } else {
+        chunk_barrier();
+    }
+    KDA_FENCE();
+    if (!HAS_NEXT) {
+        // the last step's update: dh becomes the initial state's gradient
+        bwd_update<0>(D, cur, bop);
+        bwd_update<1>(D, cur, bop);
+        bwd_update<2>(D, cur, bop);
+        bwd_update<3>(D, cur, bop);
+        bwd_update<4>(D, cur, bop);
+        bwd_update<5>(D, cur, bop);
+        bwd_update<6>(D, cur, bop);
+        bwd_update<7>(D, cur, bop);
+    }
+#undef KDA_FENCE
+}
+
+template <int S, int N>
+__device__ __forceinline__ void bwd_round_full(const Ctx& cx, f32x4 (&D)[8], BwdStateOps (&op)[2],
+                                               u32x4& bop) {
+    bwd_state_step<S, true, true>(cx, D, op, bop);
+    if constexpr (N > 1) bwd_round_full<(S + 1) % RING, N - 1>(cx, D, op, bop);
+}
+
+template <int S, int N>
+__device__ __forceinline__ void bwd_round_tail(const Ctx& cx, int c, f32x4 (&D)[8],
+                                               BwdStateOps (&op)[2], u32x4& bop) {
+    if (c >= cx.NT) return;
+    if (c + 1 < cx.NT) {
+        bwd_state_step<S, true, true>(cx, D, op, bop);
+    } else {
+        bwd_state_step<S, true, false>(cx, D, op, bop);
+    }
+    if constexpr (N > 1) bwd_round_tail<(S + 1) % RING, N - 1>(cx, c + 1, D, op, bop);
+}
+
+// Fp32 state slice of this lane from `src` ([V, K] if v_first, else
+// [K, V]; null: zeros): St[kt][i] = S[v][16*kt + 4*q4 + i].
+__device__ __forceinline__ void load_state_from(const float* src, bool v_first, int v, int q4,
+                                                f32x4 (&St)[8]) {
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) {
+        St[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (src) {
+            const int k0 = 16 * kt + 4 * q4;
+            if (v_first) {
+                St[kt] = *reinterpret_cast<const f32x4*>(src + (int64_t)v * DK + k0);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) St[kt][i] = src[(int64_t)(k0 + i) * DK + v];
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ void store_state_to(float* dst, bool v_first, int v, int q4,
+                                               const f32x4 (&St)[8]) {
+    if (!dst) return;
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) {
+        const int k0 = 16 * kt + 4 * q4;
+        if (v_first) {
+            *reinterpret_cast<f32x4*>(dst + (int64_t)v * DK + k0) = St[kt];
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dst[(int64_t)(k0 + i) * DK + v] = St[kt][i];
+        }
+    }
+}
+
+__device__ __forceinline__ void bwd_state_wave(const Params& p, const Ctx& cx, int bh) {
+    const int lane = cx.lane, q4 = cx.q4, vt = cx.vt;
+    const int v = 16 * vt + (lane & 15);
+    const int64_t sbase = (int64_t)bh * DK * DK;
+    f32x4 D[8];
+    load_state_from(p.dht ? p.dht + sbase : nullptr, p.h0_v_first != 0, v, q4, D);
+    chunk_barrier();  // steps 0 and 1 are in the ring
+    BwdStateOps op[2];
+    read_bwd_ops(ring, lane, vt, op[0]);
+    __builtin_amdgcn_s_waitcnt(WAITCNT_LGKM0);
+    u32x4 bop;
+    if (cx.NT > 1) {
+        bwd_state_step<0, false, true>(cx, D, op, bop);
+    } else {
+        bwd_state_step<0, false, false>(cx, D, op, bop);
+    }
+    int c = 1;
+    for (; c + RING < cx.NT; c += RING) bwd_round_full<1, RING>(cx, D, op, bop);
+    bwd_round_tail<1 % RING, RING>(cx, c, D, op, bop);
+    chunk_barrier();  // the output wave's last step
+    store_state_to(p.dh0 ? p.dh0 + sbase : nullptr, p.h0_v_first != 0, v, q4, D);
 }
 
 // S^T tiles of this lane: St[kt][i] = S[v][16*kt + 4*q4 + i], v = 16*vt + lane%16.
@@ -539,7 +743,7 @@ __device__ __forceinline__ void state_wave(const Params& p, const Ctx& cx, int b
     store_state(p, sbase, v, q4, St);
 }
 
-enum Role { STATE = 0, OUTPUT = 1, COPY = 2 };
+enum Role { STATE = 0, OUTPUT = 1, COPY = 2, OUTPUT2 = 3 };
 
 // Every wave executes exactly NT + 2 barriers: one after the prologue, one
 // ending each chunk, and one more for the output wave's last chunk (it runs
@@ -547,10 +751,16 @@ enum Role { STATE = 0, OUTPUT = 1, COPY = 2 };
 // the roles' code paths, the compiler's wait analysis of one role never
 // sees another role's memory operations.
 //
-// TRAIN: the recompute of the backward; the output wave stores the
-// training buffers instead of o (output_step).
-template <bool TRAIN>
-__global__ __launch_bounds__(192) void k2_kernel(Params p) {
+// MODE K2_TRAIN: the recompute of the backward; the output wave stores the
+// training buffers instead of o (output_step).  MODE K2_BWD: the backward's
+// state-gradient chain (bwd_state_wave) over the backward records, in
+// reverse chunk order, its dh' and dv_new stored like the training buffers.
+enum K2Mode { K2_FWD = 0, K2_TRAIN = 1, K2_BWD = 2 };
+
+// The training modes run a fourth wave, OUTPUT2, the second store wave.
+template <int MODE>
+__global__ __launch_bounds__(MODE == K2_FWD ? 192 : 256) void k2_kernel(Params p) {
+    constexpr bool STORE_TR = MODE != K2_FWD;
     const int lane = threadIdx.x & 63;
     const int role = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nbh = (p.cu_seqlens ? p.N : p.B) * p.HV;
@@ -571,6 +781,7 @@ __global__ __launch_bounds__(192) void k2_kernel(Params p) {
     cx.lane = lane;
     cx.q4 = lane >> 4;
     cx.vt = lin & 7;
+    cx.rev = MODE == K2_BWD;
 
     if (sp.nt == 0) {
         // An empty sequence: its final state is its initial state.  Every
@@ -578,18 +789,35 @@ __global__ __launch_bounds__(192) void k2_kernel(Params p) {
         if (role == STATE) {
             f32x4 St[8];
             const int v = 16 * cx.vt + (lane & 15);
-            load_state(p, (int64_t)bh * DK * DK, v, cx.q4, St);
-            store_state(p, (int64_t)bh * DK * DK, v, cx.q4, St);
+            const int64_t sb = (int64_t)bh * DK * DK;
+            if constexpr (MODE == K2_BWD) {
+                // the initial state's gradient is the final state's
+                load_state_from(p.dht ? p.dht + sb : nullptr, p.h0_v_first != 0, v, cx.q4, St);
+                store_state_to(p.dh0 ? p.dh0 + sb : nullptr, p.h0_v_first != 0, v, cx.q4, St);
+            } else {
+                load_state(p, sb, v, cx.q4, St);
+                store_state(p, sb, v, cx.q4, St);
+            }
         }
         __builtin_amdgcn_endpgm();
     }
     if (role == STATE) {
-        state_wave(p, cx, bh);
+        if constexpr (MODE == K2_BWD) {
+            bwd_state_wave(p, cx, bh);
+        } else {
+            state_wave(p, cx, bh);
+        }
         __builtin_amdgcn_endpgm();
     }
     if (role == OUTPUT) {
-        output_wave<TRAIN>(p, cx, sp, hv);
+        output_wave<STORE_TR, 0>(p, cx, sp, hv);
         __builtin_amdgcn_endpgm();
+    }
+    if constexpr (STORE_TR) {
+        if (role == OUTPUT2) {
+            output_wave<STORE_TR, 1>(p, cx, sp, hv);
+            __builtin_amdgcn_endpgm();
+        }
     }
     copy_wave(p, cx, sp);
     __builtin_amdgcn_endpgm();
@@ -599,13 +827,19 @@ __global__ __launch_bounds__(192) void k2_kernel(Params p) {
 
 hipError_t launch_k2(const Params& p, hipStream_t stream) {
     const int64_t grid = (int64_t)(p.cu_seqlens ? p.N : p.B) * p.HV * 8;
-    hipLaunchKernelGGL(k2_kernel<false>, dim3((unsigned)grid), dim3(192), 0, stream, p);
+    hipLaunchKernelGGL(k2_kernel<K2_FWD>, dim3((unsigned)grid), dim3(192), 0, stream, p);
     return hipGetLastError();
 }
 
 hipError_t launch_k2_train(const Params& p, hipStream_t stream) {
     const int64_t grid = (int64_t)(p.cu_seqlens ? p.N : p.B) * p.HV * 8;
-    hipLaunchKernelGGL(k2_kernel<true>, dim3((unsigned)grid), dim3(192), 0, stream, p);
+    hipLaunchKernelGGL(k2_kernel<K2_TRAIN>, dim3((unsigned)grid), dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_k2_bwd(const Params& p, hipStream_t stream) {
+    const int64_t grid = (int64_t)(p.cu_seqlens ? p.N : p.B) * p.HV * 8;
+    hipLaunchKernelGGL(k2_kernel<K2_BWD>, dim3((unsigned)grid), dim3(256), 0, stream, p);
     return hipGetLastError();
 }
 
