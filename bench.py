@@ -11,8 +11,10 @@ restatement of the reference chunked path timed on this host.
 
   python bench.py [--gpus 1] [--steps 200] [--warmup 50] [--no-cpu-baseline]
 
-Two more workloads, each printing its own line in the same format (not the
+More workloads, each printing its own line in the same format (not the
 headline metric):
+  --workload train    one training step of the op (forward, then the
+                      backward through autograd) at the headline shape;
   --workload varlen   the same 8192 tokens and 32 heads as 16 packed
                       sequences of uneven lengths (cu_seqlens), both stages;
   --workload decode   one decode step (T = 1, state updated in place) for
@@ -229,6 +231,85 @@ def run_varlen(args, dev, inputs_cpu) -> dict:
     }
 
 
+def bwd_algorithmic_bytes():
+    """Algorithmic HBM bytes of one backward: it reads q, k, v, g, beta and
+    dO (2 B per element, 2 B of beta) and writes dq, dk, dv, dg (2 B) and
+    dbeta (2 B) per token-head, plus A_log / dt_bias and their gradients:
+    2308 B per token-head."""
+    nth = B * T * H
+    return nth * (5 * D * 2 + 2 + 4 * D * 2 + 2) + 2 * H * (4 + 4 * D)
+
+
+def bwd_matmul_flops():
+    """Matrix-op FLOPs of one backward per chunk-head: the recompute (the
+    forward's 1,900,544), the state-gradient chain (Aqk^T dO, kg dh', and the
+    32-deep update of dh: 1,638,400) and the per-chunk products (dO h^T,
+    dv_new h^T, v_new dh'^T, dO v_new^T, and the fp32 grams and 16-deep
+    products of the intra-chunk gradients: 1,900,544)."""
+    nch = B * H * math.ceil(T / 16)
+    recompute = 4 * (2 * 16 * 16 * D) + 3 * (2 * 16 * D * D) + 2 * 16 * 16 * D
+    chain = 2 * 16 * 16 * D + 2 * 16 * D * D + 2 * D * 32 * D
+    chunk = 3 * (2 * 16 * D * D) + 2 * 16 * 16 * D + 3 * (2 * 16 * 16 * D) + 5 * (2 * 16 * 16 * D)
+    return nch * (recompute + chain + chunk)
+
+
+def run_train(args, dev, inputs_cpu) -> dict:
+    """One training step of the op: kda_bt16_fwd with inputs that require
+    grad, then the backward through autograd (kda_bt16_bwd: the recompute,
+    the state-gradient chain, the per-chunk gradients)."""
+    from kda_bt16 import kda_bt16_bwd
+
+    ins = [x.to(dev) for x in inputs_cpu]
+    leaves = [t.detach().clone().requires_grad_(True) for t in ins]
+    gen = torch.Generator().manual_seed(5)
+    do = torch.randn(B, T, H, D, generator=gen).to(torch.bfloat16).to(dev)
+    flags = dict(scale=SCALE, use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True,
+                 use_beta_sigmoid_in_kernel=True, lower_bound=LOWER_BOUND)
+
+    def step():
+        for t in leaves:
+            t.grad = None
+        o, _ = kda_bt16_fwd(*leaves[:5], A_log=leaves[5], dt_bias=leaves[6], **flags)
+        o.backward(do)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    q, k, v, g, beta, A_log, dt_bias = ins
+    reps = max(args.steps, 10)
+    bwd_ms = time_events(lambda: kda_bt16_bwd(do, q, k, v, g, beta, A_log=A_log,
+                                              dt_bias=dt_bias, **flags), reps)
+    fwd_ms = time_events(lambda: kda_bt16_fwd(q, k, v, g, beta, A_log=A_log, dt_bias=dt_bias,
+                                              **flags), reps)
+    by = bwd_algorithmic_bytes()
+    fl = bwd_matmul_flops()
+    achieved = by / bwd_ms / 1e6
+    return {
+        "metric": "KDA training step (fwd + bwd) tokens/sec at B=1 T=8192 H=32 bf16",
+        "value": round(B * T / (wall_ms / 1e3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"kda_bt16_fwd + autograd backward B={B} T={T} H={H} K=V={D}, "
+                               "zero h0, all in-kernel flags, dO ~N(0,1)",
+                   "global_batch": B, "seq_len": T, "heads": H, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "kernel": "backward (kda_bt16_bwd_hip, 6 launches)",
+                     "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None,
+                     "bwd_ms": round(bwd_ms, 4), "fwd_ms": round(fwd_ms, 4),
+                     "bwd_alg_bytes": by, "bwd_matmul_flops": fl,
+                     "bwd_tflops": round(fl / bwd_ms / 1e9, 2),
+                     "bwd_mfma_frac": round(fl / bwd_ms / 1e9 / BF16_PEAK_TFLOPS, 5)},
+    }
+
+
 DEC_B = 128
 
 
@@ -295,7 +376,8 @@ def main() -> None:
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 256 MiB device copy (3 launches), the reference "
                          "kernel for scaling rocprof FETCH_SIZE / WRITE_SIZE to bytes")
-    ap.add_argument("--workload", choices=("headline", "varlen", "decode"), default="headline")
+    ap.add_argument("--workload", choices=("headline", "varlen", "decode", "train"),
+                    default="headline")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the forward shards over (batch, head) with no "
@@ -321,6 +403,9 @@ def main() -> None:
     inputs_cpu = make_inputs()
     if args.workload == "varlen":
         print(json.dumps(run_varlen(args, dev, inputs_cpu)), flush=True)
+        return
+    if args.workload == "train":
+        print(json.dumps(run_train(args, dev, inputs_cpu)), flush=True)
         return
     q, k, v, g, beta, A_log, dt_bias = (x.to(dev) for x in inputs_cpu)
     kw = dict(scale=SCALE, output_final_state=True, use_qk_l2norm_in_kernel=True,
