@@ -48,11 +48,16 @@ constexpr int LD = DK + 4; // fp32 row stride of the [16][128] LDS matrices
 // operands read from these tiles: lane (n, k') of a wave supplies
 // A[n][4*s + k'] and B[4*s + k'][n] for slab s, and D[m][n] lands in lane
 // n + 16*(m/4) item m%4 (kda_common.h).
+// 74 KiB, so that two work-groups share a CU.  Tiles are reused once dead:
+// dqg first holds the gate cumsum G, dw / dvn later hold dkb / dvb, kp /
+// km / qp / dqg end as dG and the gate's column sums, and the 16x16
+// scratch takes the grams' partial sums.
+constexpr int LDB = DK + 8;  // bf16 row stride of the kb / vb tiles
 struct ChunkSmem {
-    float kp[BT][LD], km[BT][LD], qp[BT][LD], kb[BT][LD], vb[BT][LD];
-    float dw[BT][LD], dvn[BT][LD], dqg[BT][LD], dkg[BT][LD], gsc[BT][LD];
-    float el[DK], del[DK];
-    float partL[4][BT][BT + 1], partA[4][BT][BT + 1];
+    float kp[BT][LD], km[BT][LD], qp[BT][LD];
+    float dw[BT][LD], dvn[BT][LD], dqg[BT][LD], dkg[BT][LD];
+    uint16_t kb[BT][LDB], vb[BT][LDB];  // bf16-valued by construction
+    float el[DK], del[DK], gm[DK], gl[DK];  // 2^G_last, dE_last, G of rows mid / last
     float lraw[BT][BT + 1], ainv[BT][BT + 1], da[BT][BT + 1], m1[BT][BT + 1];
     float dlr[BT][BT + 1], daqm[BT][BT + 1];
     float red[CT / 64];
@@ -78,6 +83,11 @@ __device__ __forceinline__ void lds_put8(float* dst, const float (&x)[8]) {
     *reinterpret_cast<f32x4*>(dst + 4) = f32x4{x[4], x[5], x[6], x[7]};
 }
 
+__device__ __forceinline__ void lds_put8_bf(uint16_t* dst, const float (&x)[8]) {
+    *reinterpret_cast<u32x4*>(dst) =
+        u32x4{pack2(x[0], x[1]), pack2(x[2], x[3]), pack2(x[4], x[5]), pack2(x[6], x[7])};
+}
+
 __device__ __forceinline__ void lds_get8(const float* src, float (&x)[8]) {
     const f32x4 a = *reinterpret_cast<const f32x4*>(src);
     const f32x4 b = *reinterpret_cast<const f32x4*>(src + 4);
@@ -97,11 +107,20 @@ __device__ __forceinline__ float row_sum16(float s) {
     return s;
 }
 
-// One value head's row data of this thread (row i, columns c0 .. c0+7).
+// One value head's row data of this thread (row i, columns c0 .. c0+7):
+// g is the gate's argument g + dt_bias with the in-kernel gate, else g.
 struct HvRow {
-    float v[8], g[8], dvn[8], bias[8];
+    float v[8], g[8], dvn[8];
     float beta, alog;
 };
+
+__device__ __forceinline__ void unpack8(const u32x4& w, float (&out)[8]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        out[2 * j] = __builtin_bit_cast(float, w[j] << 16);
+        out[2 * j + 1] = __builtin_bit_cast(float, w[j] & 0xffff0000u);
+    }
+}
 
 // One value head's matrix-op operands for the products over V (wave w:
 // k-tiles 2w, 2w+1), loaded ahead of the intra-chunk work so that their
@@ -111,7 +130,12 @@ struct HdhOps {
     u32x4 a_do[4], a_dv[4], a_vn[4];  // dO, dv_new, v_new row x, same v
 };
 
-__global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
+// GROUP: grouped value heads (HV > H), the value heads of a q/k head in a
+// loop.  Without it the body runs once, and the compiler keeps nothing live
+// across iterations (hoisted addresses and row values would otherwise hold
+// registers through the whole body).
+template <bool GROUP>
+__global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(GROUP ? 1 : 2))) void bwd_chunk_kernel(Params p) {
     __shared__ ChunkSmem sm;
     const int t = threadIdx.x;
     const int lane = t & 63, w = t >> 6;
@@ -170,15 +194,14 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
                 r.g[4 + j] = b[j];
             }
         }
-        f32x4 ba = {0.f, 0.f, 0.f, 0.f}, bb = ba;
         if (p.use_gate && p.dt_bias) {
-            ba = *reinterpret_cast<const f32x4*>(p.dt_bias + hv * DK + c0);
-            bb = *reinterpret_cast<const f32x4*>(p.dt_bias + hv * DK + c0 + 4);
-        }
+            const f32x4 ba = *reinterpret_cast<const f32x4*>(p.dt_bias + hv * DK + c0);
+            const f32x4 bb = *reinterpret_cast<const f32x4*>(p.dt_bias + hv * DK + c0 + 4);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            r.bias[j] = ba[j];
-            r.bias[4 + j] = bb[j];
+            for (int j = 0; j < 4; ++j) {
+                r.g[j] += ba[j];
+                r.g[4 + j] += bb[j];
+            }
         }
         r.beta = 0.f;
         if (valid) {
@@ -218,16 +241,20 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
         }
     };
 
-    // ---- q^, k^ (kernels.py:108-113), once per q/k head ------------------
-    float qv[8], kv[8], qn[8], kn[8];
-    load8(p.q + (tok * H + h) * DK + c0, valid, qv);
-    load8(p.k + (tok * H + h) * DK + c0, valid, kv);
+    // ---- q^, k^ (kernels.py:108-113), once per q/k head; the raw rows stay
+    // packed and q^ / k^ are re-formed where needed --------------------------
+    u32x4 qraw = {0u, 0u, 0u, 0u}, kraw = qraw;
+    if (valid) {
+        qraw = *reinterpret_cast<const u32x4*>(p.q + (tok * H + h) * DK + c0);
+        kraw = *reinterpret_cast<const u32x4*>(p.k + (tok * H + h) * DK + c0);
+    }
     HvRow hr;
-    HdhOps ops;
     load_hv(h * rep, hr);
-    load_ops(h * rep, ops);
     float rq = 1.f, rk = 1.f;
     if (p.use_l2norm) {
+        float qv[8], kv[8];
+        unpack8(qraw, qv);
+        unpack8(kraw, kv);
         float sq2 = 0.f, sk2 = 0.f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -239,21 +266,26 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
         rq = 1.f / sqrtf(sq2 + L2_EPS);
         rk = 1.f / sqrtf(sk2 + L2_EPS);
     }
+    // q^ and k^ as the forward rounds them (bf16 after the l2norm)
+    auto qk_hat = [&](float (&qn)[8], float (&kn)[8]) {
+        unpack8(qraw, qn);
+        unpack8(kraw, kn);
+        if (p.use_l2norm) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        qn[j] = p.use_l2norm ? round_bf(qv[j] * rq) : qv[j];
-        kn[j] = p.use_l2norm ? round_bf(kv[j] * rk) : kv[j];
-    }
+            for (int j = 0; j < 8; ++j) {
+                qn[j] = round_bf(qn[j] * rq);
+                kn[j] = round_bf(kn[j] * rk);
+            }
+        }
+    };
     float dQN[8], dKN[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) dQN[j] = dKN[j] = 0.f;
 
-    for (int gi = 0; gi < rep; ++gi) {
+    const int nrep = GROUP ? rep : 1;
+    for (int gi = 0; gi < nrep; ++gi) {
         const int hv = h * rep + gi;
-        if (gi > 0) {
-            load_hv(hv, hr);
-            load_ops(hv, ops);
-        }
+        if (gi > 0) load_hv(hv, hr);
         const SeqSpan sp = seq_span(p, seq * HV + hv);
         const int64_t rec = sp.rec0 + c;
         const int64_t vrow = (tok * HV + hv) * DK;  // v/g/dO element offset of row i
@@ -266,11 +298,10 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
             float gv[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float gg = p.use_gate ? p.lower_bound * fast_sigmoid(ea * (hr.g[j] + hr.bias[j]))
-                                            : hr.g[j];
+                const float gg = p.use_gate ? p.lower_bound * fast_sigmoid(ea * hr.g[j]) : hr.g[j];
                 gv[j] = valid ? gg : 0.f;
             }
-            lds_put8(&sm.gsc[i][c0], gv);
+            lds_put8(&sm.dqg[i][c0], gv);  // the gate, then its cumsum G
             lds_put8(&sm.dvn[i][c0], hr.dvn);
         }
         __syncthreads();
@@ -278,24 +309,39 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
             float run = 0.f;
 #pragma unroll
             for (int r = 0; r < BT; ++r) {
-                run += sm.gsc[r][t];
-                sm.gsc[r][t] = run * RCP_LN2;
+                run += sm.dqg[r][t];
+                sm.dqg[r][t] = run * RCP_LN2;
             }
         }
         __syncthreads();
-        if (t < DK) sm.el[t] = fast_exp2(sm.gsc[last][t]);
-        float E[8], eq[8], ek[8], kgl[8];
-        {
-            float G[8], Gm[8], Gl[8], o1[8], o2[8], o3[8], o4[8], o5[8];
-            lds_get8(&sm.gsc[i][c0], G);
-            lds_get8(&sm.gsc[mid][c0], Gm);
-            lds_get8(&sm.gsc[last][c0], Gl);
+        if (t < DK) {
+            sm.el[t] = fast_exp2(sm.dqg[last][t]);
+            sm.gm[t] = sm.dqg[mid][t];
+            sm.gl[t] = sm.dqg[last][t];
+        }
+        // E = 2^G, the recentred 2^(G - G_mid), 2^(G_mid - G), and
+        // 2^(G_last - G), from this row's G and the rows mid and last
+        float G[8];
+        lds_get8(&sm.dqg[i][c0], G);
+        auto gates = [&](float (&E)[8], float (&eq)[8], float (&ek)[8], float (&kgl)[8]) {
+            float Gm[8], Gl[8];
+            lds_get8(&sm.gm[c0], Gm);
+            lds_get8(&sm.gl[c0], Gl);
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 E[j] = valid ? fast_exp2(G[j]) : 0.f;
                 eq[j] = valid ? fast_exp2(G[j] - Gm[j]) : 0.f;
                 ek[j] = valid ? fast_exp2(Gm[j] - G[j]) : 0.f;
                 kgl[j] = valid ? fast_exp2(Gl[j] - G[j]) : 0.f;
+            }
+        };
+        __syncthreads();  // gm, gl
+        {
+            float E[8], eq[8], ek[8], kgl[8], qn[8], kn[8], o1[8], o2[8], o3[8], o4[8], o5[8];
+            gates(E, eq, ek, kgl);
+            qk_hat(qn, kn);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
                 o1[j] = qn[j] * eq[j];
                 o2[j] = kn[j] * eq[j];
                 o3[j] = kn[j] * ek[j];
@@ -305,15 +351,18 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
             lds_put8(&sm.qp[i][c0], o1);
             lds_put8(&sm.kp[i][c0], o2);
             lds_put8(&sm.km[i][c0], o3);
-            lds_put8(&sm.kb[i][c0], o4);
-            lds_put8(&sm.vb[i][c0], o5);
+            lds_put8_bf(&sm.kb[i][c0], o4);
+            lds_put8_bf(&sm.vb[i][c0], o5);
         }
+        __syncthreads();  // G is read; phase 2 overwrites dqg
 
         // ---- phase 2: products over V on the matrix cores ----------------
         // Wave w owns k-tiles 2w, 2w+1.  Lane (x, q4) feeds row x of dO /
         // dv_new / v_new and row 16*kt + x of h / dh', v columns
         // 32*jv + 8*q4 .. +7, as 16x16x32 operands.
         {
+            HdhOps ops;
+            load_ops(hv, ops);
             f32x4 aq[2], aw[2], ak[2], adq = {0.f, 0.f, 0.f, 0.f};
             float pel[2] = {0.f, 0.f};
 #pragma unroll
@@ -362,31 +411,41 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
         }
         __syncthreads();
 
-        // ---- phase 3: the grams Lraw = kp km^T and dA = dw kb^T + du vb^T,
-        // each wave over 32 of the 128 columns ------------------------------
+        // ---- phase 3: the grams Lraw = kp km^T (waves 0, 1: 64 columns
+        // each) and dA = dw kb^T + du vb^T (waves 2, 3), partial sums in the
+        // 16x16 scratch (m1, dlr, ainv, da) --------------------------------
         {
-            f32x4 lr = {0.f, 0.f, 0.f, 0.f}, da = lr;
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            if (w < 2) {
 #pragma unroll
-            for (int sl = 0; sl < 8; ++sl) {
-                const int col = 32 * w + 4 * sl + q4;
-                lr = mfma_f32_16x16x4(sm.kp[x][col], sm.km[x][col], lr);
-                da = mfma_f32_16x16x4(sm.dw[x][col], sm.kb[x][col], da);
-                da = mfma_f32_16x16x4(sm.dvn[x][col], sm.vb[x][col], da);
-            }
+                for (int sl = 0; sl < 16; ++sl) {
+                    const int col = 64 * w + 4 * sl + q4;
+                    acc = mfma_f32_16x16x4(sm.kp[x][col], sm.km[x][col], acc);
+                }
+            } else if (w == 2) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                sm.partL[w][4 * q4 + e][x] = lr[e];
-                sm.partA[w][4 * q4 + e][x] = da[e];
+                for (int sl = 0; sl < 32; ++sl) {
+                    const int col = 4 * sl + q4;
+                    acc = mfma_f32_16x16x4(sm.dw[x][col], bf2f(sm.kb[x][col]), acc);
+                }
+            } else {
+#pragma unroll
+                for (int sl = 0; sl < 32; ++sl) {
+                    const int col = 4 * sl + q4;
+                    acc = mfma_f32_16x16x4(sm.dvn[x][col], bf2f(sm.vb[x][col]), acc);
+                }
             }
+            float (*part)[BT + 1] = w == 0 ? sm.m1 : w == 1 ? sm.dlr : w == 2 ? sm.ainv : sm.da;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) part[4 * q4 + e][x] = acc[e];
         }
         __syncthreads();
         {
-            const float lraw = sm.partL[0][i][cb] + sm.partL[1][i][cb] + sm.partL[2][i][cb] +
-                               sm.partL[3][i][cb];
+            const float lraw = sm.m1[i][cb] + sm.dlr[i][cb];
+            const float da = sm.ainv[i][cb] + sm.da[i][cb];
             sm.lraw[i][cb] = lraw;
             sm.m1[i][cb] = (i > cb) ? beta * lraw : 0.f;  // L, read by the solve
-            sm.da[i][cb] = sm.partA[0][i][cb] + sm.partA[1][i][cb] + sm.partA[2][i][cb] +
-                           sm.partA[3][i][cb];
+            sm.da[i][cb] = da;
         }
         __syncthreads();
         if (t < BT) {
@@ -429,7 +488,7 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
         __syncthreads();
 
         // ---- phase 5: dL = -A^T dA A^T (strictly lower), dLr = beta dL; the
-        // dkb / dvb tiles replace kb / vb (read for the last time above) ----
+        // dkb / dvb tiles replace dw / du (read for the last time above) ----
         float dbl;
         {
             float s2 = 0.f;
@@ -443,8 +502,8 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
                 const int col = 16 * (2 * w + tt) + x;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    sm.kb[4 * q4 + e][col] = dkbt[tt][e];
-                    sm.vb[4 * q4 + e][col] = dvbt[tt][e];
+                    sm.dw[4 * q4 + e][col] = dkbt[tt][e];
+                    sm.dvn[4 * q4 + e][col] = dvbt[tt][e];
                 }
             }
         }
@@ -479,11 +538,14 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
         float dG[8];
         {
             float dkp[8], dqp[8], dkm[8], dkb[8], dvb[8], dqg[8], dkg[8], dv[8];
+            float E[8], eq[8], ek[8], kgl[8], qn[8], kn[8];
+            gates(E, eq, ek, kgl);
+            qk_hat(qn, kn);
             lds_get8(&sm.kp[i][c0], dkp);
             lds_get8(&sm.qp[i][c0], dqp);
             lds_get8(&sm.km[i][c0], dkm);
-            lds_get8(&sm.kb[i][c0], dkb);
-            lds_get8(&sm.vb[i][c0], dvb);
+            lds_get8(&sm.dw[i][c0], dkb);
+            lds_get8(&sm.dvn[i][c0], dvb);
             lds_get8(&sm.dqg[i][c0], dqg);
             lds_get8(&sm.dkg[i][c0], dkg);
             float dbeta = 0.f, kgkg[8];
@@ -512,9 +574,9 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
                     else static_cast<float*>(p.dbeta)[bi] = db;
                 }
             }
-            // gsc and dkg are read only by their owning thread since phase 1
-            lds_put8(&sm.gsc[i][c0], dG);
-            lds_put8(&sm.dkg[i][c0], kgkg);
+            // kp and km (dkp, dkm) are read only by their owning thread here
+            lds_put8(&sm.kp[i][c0], dG);
+            lds_put8(&sm.km[i][c0], kgkg);
         }
         __syncthreads();
 
@@ -524,20 +586,20 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
         if (t < DK) {
             float s2 = 0.f;
 #pragma unroll
-            for (int r = 0; r < BT; ++r) s2 += sm.dkg[r][t];
-            sm.gsc[last][t] += LN2 * (s2 + sm.el[t] * sm.del[t]);
+            for (int r = 0; r < BT; ++r) s2 += sm.km[r][t];
+            sm.kp[last][t] += LN2 * (s2 + sm.el[t] * sm.del[t]);
         }
         __syncthreads();
         {
             float dg[8], suf[8], own[8];
-            lds_get8(&sm.gsc[i][c0], own);  // dG with the last row's terms
+            lds_get8(&sm.kp[i][c0], own);  // dG with the last row's terms
 #pragma unroll
             for (int j = 0; j < 8; ++j) suf[j] = 0.f;
 #pragma unroll
             for (int r = 0; r < BT; ++r) {
                 if (r >= i && r < nvalid) {
                     float row[8];
-                    lds_get8(&sm.gsc[r][c0], row);
+                    lds_get8(&sm.kp[r][c0], row);
 #pragma unroll
                     for (int j = 0; j < 8; ++j) suf[j] += row[j];
                 }
@@ -547,7 +609,7 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
             for (int j = 0; j < 8; ++j) {
                 float d;
                 if (p.use_gate) {
-                    const float sarg = hr.g[j] + hr.bias[j];
+                    const float sarg = hr.g[j];
                     const float sg = fast_sigmoid(ea * sarg);
                     d = RCP_LN2 * suf[j] * p.lower_bound * sg * (1.f - sg) * ea;
                     pdt[j] = valid ? d : 0.f;
@@ -570,9 +632,9 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
             }
             if (gate_grads) {
                 // column sums for ddt_bias, dA_log's terms, through the dead
-                // dqg / dw tiles
-                lds_put8(&sm.dqg[i][c0], pdt);
-                lds_put8(&sm.dw[i][c0], pal);
+                // qp / dqg tiles
+                lds_put8(&sm.qp[i][c0], pdt);
+                lds_put8(&sm.dqg[i][c0], pal);
             }
         }
         if (gate_grads) {
@@ -581,8 +643,8 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
                 float sdt = 0.f, sal = 0.f;
 #pragma unroll
                 for (int r = 0; r < BT; ++r) {
-                    sdt += sm.dqg[r][t];
-                    sal += sm.dw[r][t];
+                    sdt += sm.qp[r][t];
+                    sal += sm.dqg[r][t];
                 }
                 p.tr_part[rec * PART_STRIDE + t] = sdt;
 #pragma unroll
@@ -597,6 +659,9 @@ __global__ __launch_bounds__(CT) void bwd_chunk_kernel(Params p) {
 
     // ---- l2norm backward, dq / dk summed over the group -------------------
     if (p.use_l2norm) {
+        float qv[8], kv[8];
+        unpack8(qraw, qv);
+        unpack8(kraw, kv);
         float dq_dot = 0.f, dk_dot = 0.f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -659,7 +724,11 @@ __global__ __launch_bounds__(RG * DK) void gate_reduce_kernel(Params p) {
 
 hipError_t launch_bwd_chunk(const Params& p, hipStream_t stream) {
     const int64_t grid = p.cu_seqlens ? (int64_t)p.H * p.NS : (int64_t)p.B * p.H * p.NT;
-    hipLaunchKernelGGL(bwd_chunk_kernel, dim3((unsigned)grid), dim3(CT), 0, stream, p);
+    if (p.HV > p.H) {
+        hipLaunchKernelGGL(bwd_chunk_kernel<true>, dim3((unsigned)grid), dim3(CT), 0, stream, p);
+    } else {
+        hipLaunchKernelGGL(bwd_chunk_kernel<false>, dim3((unsigned)grid), dim3(CT), 0, stream, p);
+    }
     return hipGetLastError();
 }
 
