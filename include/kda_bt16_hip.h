@@ -184,10 +184,10 @@ typedef struct KdaBt16BwdArgs {
     size_t workspace_bytes;
 } KdaBt16BwdArgs;
 
-/* Workspace of kda_bt16_bwd_hip: per 16-token record slot, the 17 KiB
- * record, bf16 h and dh (32 KiB each), v_new and dv_new (4 KiB each) and the
- * gate partial sums (528 B): ~89.5 KiB (1.43 GiB at B=1 T=8192 H=32).
- * Returns 0 for an unsupported geometry. */
+/* Workspace of kda_bt16_bwd_hip: per 16-token record slot, the forward and
+ * the backward records (17 KiB each), bf16 h and dh (32 KiB each), v_new and
+ * dv_new (4 KiB each) and the gate partial sums (528 B): ~106.5 KiB
+ * (1.70 GiB at B=1 T=8192 H=32).  Returns 0 for an unsupported geometry. */
 size_t kda_bt16_bwd_workspace_bytes(const KdaBt16Args* fwd);
 
 int kda_bt16_bwd_hip(const KdaBt16BwdArgs* args, void* stream);

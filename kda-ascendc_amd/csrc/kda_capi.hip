@@ -151,13 +151,15 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // Backward workspace regions, in order.
 struct BwdLayout {
-    size_t rec, h, vn, dh, dvn, part, total;
+    size_t rec, brec, h, vn, dh, dvn, part, total;
 };
 
 BwdLayout bwd_layout(int64_t R) {
     BwdLayout L;
     size_t off = 0;
     L.rec = off;
+    off = align256(off + (size_t)R * kda::REC_BYTES);
+    L.brec = off;
     off = align256(off + (size_t)R * kda::REC_BYTES);
     L.h = off;
     off = align256(off + (size_t)R * kda::TR_H_ELEMS * 2);
@@ -260,6 +262,7 @@ int kda_bt16_bwd_hip(const KdaBt16BwdArgs* b, void* stream) {
     if ((reinterpret_cast<uintptr_t>(b->workspace) & 255u) != 0) return KDA_BT16_EWORKSPACE;
     uint8_t* ws = static_cast<uint8_t*>(b->workspace);
     p.ws = ws + L.rec;
+    p.ws_bwd = ws + L.brec;
     p.tr_h = reinterpret_cast<uint16_t*>(ws + L.h);
     p.tr_vn = reinterpret_cast<uint16_t*>(ws + L.vn);
     p.tr_dh = reinterpret_cast<uint16_t*>(ws + L.dh);
@@ -278,9 +281,8 @@ int kda_bt16_bwd_hip(const KdaBt16BwdArgs* b, void* stream) {
     p.ddt_bias = b->ddt_bias;
     p.dh0 = b->dh0;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (kda::launch_k1(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
+    if (kda::launch_k1_both_records(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
     if (kda::launch_k2_train(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
-    if (kda::launch_k1_bwd_records(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
     if (kda::launch_k2_bwd(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
     if (kda::launch_bwd_chunk(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
     if (p.tr_part && kda::launch_bwd_gate_reduce(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;

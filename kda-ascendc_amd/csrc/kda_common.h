@@ -50,8 +50,8 @@ constexpr int REC_SHARED = 13312;  // bytes every value tile reads
 constexpr int REC_BYTES = 17408;
 
 // Backward record (kda_bt16_bwd_hip): what the reverse state chain feeds
-// its matrix cores, written by stage 1 in place of the forward record once
-// the recompute has consumed that.  Same slot indexing.
+// its matrix cores, written by the backward's stage-1 pass next to the
+// forward record (a second region, same slot indexing).
 //   offset  bytes  content
 //   0       4096   kg     bf16, F order, [j][lane][8] (k-tiles 2j, 2j+1):
 //                         the A operand of dv_new += kg @ dh
@@ -135,6 +135,7 @@ struct Params {
     // the shapes of q, k, v; dg and dbeta in the element types of g and beta;
     // dA_log [HV], ddt_bias [HV*128] and dh0 (state layout of h0), each
     // optional as its input is.
+    uint8_t* ws_bwd;  // backward records (same slot indexing as ws)
     uint16_t* tr_h;
     uint16_t* tr_vn;
     uint16_t* tr_dh;
@@ -317,7 +318,7 @@ hipError_t launch_k1(const Params& p, hipStream_t stream);
 hipError_t launch_k2(const Params& p, hipStream_t stream);
 hipError_t launch_recurrent(const Params& p, hipStream_t stream);
 // Backward (kda_bt16_bwd.hip, and the training variants of the stages).
-hipError_t launch_k1_bwd_records(const Params& p, hipStream_t stream);
+hipError_t launch_k1_both_records(const Params& p, hipStream_t stream);
 hipError_t launch_k2_train(const Params& p, hipStream_t stream);
 hipError_t launch_k2_bwd(const Params& p, hipStream_t stream);
 hipError_t launch_bwd_chunk(const Params& p, hipStream_t stream);

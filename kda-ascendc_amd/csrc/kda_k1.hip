@@ -72,10 +72,12 @@ __device__ __forceinline__ u32x2 pack4(f32x4 v) { return pack4(v.x, v.y, v.z, v.
 // values): each wave spends most of its life waiting on its loads, and a
 // third wave per SIMD hides more of that than the two that 172 VGPRs allow.
 //
-// BWD = true writes the backward record (kda_common.h) instead: the same
-// chunk quantities in the operand orders of the reverse state chain.
-template <bool BWD>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k1_kernel(Params p) {
+// BOTH = true (the backward's recompute, two waves per SIMD: it holds more)
+// also writes the backward record
+// (kda_common.h) to p.ws_bwd: the same chunk quantities in the operand
+// orders of the reverse state chain, from one read of the inputs.
+template <bool BOTH>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(BOTH ? 2 : 3))) void k1_kernel(Params p) {
     __shared__ __attribute__((aligned(16))) uint16_t s_T[BT * LROW];  // transpose tile
     __shared__ __attribute__((aligned(16))) float s_L[BT * BT];
     __shared__ float s_X[BT * (BT + 1)];
@@ -216,8 +218,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k1
         L[i] = (r > s) ? acc_kk[i] * beta : 0.f;
     }
     const u32x2 aqk_bf = pack4(aqk);
-    if constexpr (!BWD)
-        __builtin_nontemporal_store(aqk_bf, reinterpret_cast<u32x2*>(rec + REC_AQK + lane * 8));
+    __builtin_nontemporal_store(aqk_bf, reinterpret_cast<u32x2*>(rec + REC_AQK + lane * 8));
 
     // ---- (I + L)^-1 by forward substitution (kernels.py:157-167) ---------
     // Lane r solves column s = r: a[t] = A_inv[t][s], with a[s] = 1,
@@ -252,8 +253,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k1
     const i16x4 A_op = as_i16x4(ainv_bf);
     const i16x4 A_neg = as_i16x4(ainv_bf ^ 0x80008000u);
 
-    if constexpr (BWD) {
+    if constexpr (BOTH) {
         // ---- backward record ---------------------------------------------
+        uint8_t* brec = p.ws_bwd + (sp.rec0 + c) * REC_BYTES;
         // Aqk^T as an A operand: lane (r, q4) takes Aqk[4*q4 + i][r], the
         // transpose of what it holds, through s_L (free after the solve).
         *reinterpret_cast<f32x4*>(s_L + r * BT + 4 * q4) = aqk;
@@ -263,7 +265,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k1
 #pragma unroll
             for (int i = 0; i < 4; ++i) at[i] = s_L[(4 * q4 + i) * BT + r];
             __builtin_nontemporal_store(pack4(at),
-                                        reinterpret_cast<u32x2*>(rec + BREC_AQKT + lane * 8));
+                                        reinterpret_cast<u32x2*>(brec + BREC_AQKT + lane * 8));
         }
         // -w in T order straight from the matrix cores: (-A) @ kb tile kt
         // lands as -w[4*q4 + i][16*kt + r].  bf16(scale * q^ * 2^G) goes
@@ -303,7 +305,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k1
                 const u32x2 qv = __builtin_bit_cast(u32x2, qsT[kt]);
                 __builtin_nontemporal_store(
                     u32x4{qv.x, qv.y, wT[kt].x, wT[kt].y},
-                    reinterpret_cast<u32x4*>(rec + BREC_UPD + kt * 1024 + lane * 16));
+                    reinterpret_cast<u32x4*>(brec + BREC_UPD + kt * 1024 + lane * 16));
             }
         }
         // dO as the B operand of each value tile (T order, the layout of u
@@ -320,7 +322,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k1
 #pragma unroll
             for (int vt = 0; vt < 8; ++vt)
                 __builtin_nontemporal_store(__builtin_bit_cast(u32x2, doT[vt]),
-                                            reinterpret_cast<u32x2*>(rec + BREC_DO + vt * 512 + lane * 8));
+                                            reinterpret_cast<u32x2*>(brec + BREC_DO + vt * 512 + lane * 8));
         }
         // kg = bf16(k^ * 2^(G_last - G)) in F order (the A operand of
         // kg @ dh), and the decay 2^G_last.
@@ -337,14 +339,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k1
             if (r == 0)
                 __builtin_nontemporal_store(
                     f32x4{fast_exp2(gl[0]), fast_exp2(gl[1]), fast_exp2(gl[2]), fast_exp2(gl[3])},
-                    reinterpret_cast<f32x4*>(rec + BREC_DECAY + kt * 64 + q4 * 16));
+                    reinterpret_cast<f32x4*>(brec + BREC_DECAY + kt * 64 + q4 * 16));
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             __builtin_nontemporal_store(
                 u32x4{kgF[2 * j].x, kgF[2 * j].y, kgF[2 * j + 1].x, kgF[2 * j + 1].y},
-                reinterpret_cast<u32x4*>(rec + BREC_KG + j * 1024 + lane * 16));
-        return;
+                reinterpret_cast<u32x4*>(brec + BREC_KG + j * 1024 + lane * 16));
+        __syncthreads();
     }
 
     // ---- u = A @ bf16(v * beta) (kernels.py:173-174) ----------------------
@@ -476,7 +478,7 @@ hipError_t launch_k1(const Params& p, hipStream_t stream) {
     return hipGetLastError();
 }
 
-hipError_t launch_k1_bwd_records(const Params& p, hipStream_t stream) {
+hipError_t launch_k1_both_records(const Params& p, hipStream_t stream) {
     const int64_t grid = p.cu_seqlens ? (int64_t)p.HV * p.NS : (int64_t)p.B * p.HV * p.NT;
     hipLaunchKernelGGL(k1_kernel<true>, dim3((unsigned)grid), dim3(64), 0, stream, p);
     return hipGetLastError();

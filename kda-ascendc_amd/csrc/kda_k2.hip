@@ -461,8 +461,8 @@ __device__ __forceinline__ void copy_round(const Ctx& cx, int c) {
 
 __device__ __forceinline__ void copy_wave(const Params& p, Ctx& cx, const SeqSpan& sp) {
     const int NT = cx.NT;
-    cx.rs = __builtin_amdgcn_make_buffer_rsrc(p.ws + sp.rec0 * REC_BYTES, (short)0,
-                                              NT * REC_BYTES, BUF_DWORD3);
+    uint8_t* recs = (cx.rev ? p.ws_bwd : p.ws) + sp.rec0 * REC_BYTES;
+    cx.rs = __builtin_amdgcn_make_buffer_rsrc(recs, (short)0, NT * REC_BYTES, BUF_DWORD3);
     cx.voff16 = cx.lane * 16;
     cx.u_off = REC_U + 1024 * (cx.vt >> 1);
 #pragma unroll

@@ -156,10 +156,11 @@ def test_bwd_struct_layout_matches_header_field_order():
 
 
 def test_bwd_workspace_bytes():
-    # per record slot: record, bf16 h and dh, v_new and dv_new, gate partials;
+    # per record slot: forward and backward records, bf16 h and dh, v_new and
+    # dv_new, gate partials;
     # each region 256-byte aligned
     R = 32 * 512
-    per = [17408, 32768, 4096, 32768, 4096, 132 * 4]
+    per = [17408, 17408, 32768, 4096, 32768, 4096, 132 * 4]
     assert _hip.bwd_workspace_bytes(_args(B=1, T=8192, H=32, HV=32)) == sum(
         (R * x + 255) // 256 * 256 for x in per)
     assert _hip.bwd_workspace_bytes(_args(K=64)) == 0
