@@ -257,6 +257,15 @@ __device__ __forceinline__ float row_scan16(float x) {
     return x;
 }
 
+// Lane LANE of each 16-lane row to the whole row (DPP row_newbcast).
+template <int LANE>
+__device__ __forceinline__ float row_bcast(float v) {
+    constexpr int ROW_NEWBCAST = 0x150;
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                                 ROW_NEWBCAST + LANE, 0xf, 0xf,
+                                                                 false));
+}
+
 __device__ __forceinline__ float shfl(float x, int src_lane) {
     return __builtin_bit_cast(
         float, __builtin_amdgcn_ds_bpermute(src_lane << 2, __builtin_bit_cast(int, x)));

@@ -191,19 +191,33 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(BOTH ? 2 : 3
     const int mid = min(BT / 2, nvalid - 1);
     const int last = nvalid - 1;
     const int row0 = lane & 48;
+    // Row mid's and row last's values reach the rows of their 16-lane
+    // group by DPP broadcast in a full chunk (mid = 8, last = 15), by a
+    // cross-lane permute in a sequence's partial last chunk.
+    const bool full = nvalid == BT;
+    auto bcast_mid = [&](auto use) {
+        if (full) use([](float x) { return row_bcast<BT / 2>(x); });
+        else use([&](float x) { return shfl(x, row0 | mid); });
+    };
+    auto bcast_last = [&](auto use) {
+        if (full) use([](float x) { return row_bcast<BT - 1>(x); });
+        else use([&](float x) { return shfl(x, row0 | last); });
+    };
     f32x4 acc_qk = {0.f, 0.f, 0.f, 0.f};
     f32x4 acc_kk = {0.f, 0.f, 0.f, 0.f};
+    bcast_mid([&](auto from_mid) {
 #pragma unroll
-    for (int j = 0; j < 32; ++j) {
-        const float gm = G[j] - shfl(G[j], row0 | mid);
-        const float gq = valid ? fast_exp2(gm) : 0.f;
-        const float gk = valid ? fast_exp2(-gm) : 0.f;
-        const float qv = elem(qp, j), kv = elem(kp, j);
-        // A = Ks (rows s), B = Qs / Kq (columns t): lane (t, q4) receives
-        // Aqk[t][4*q4 + i] and Akk[t][4*q4 + i].
-        acc_qk = mfma_f32_16x16x4(kv * gk, qv * gq, acc_qk);
-        acc_kk = mfma_f32_16x16x4(kv * gk, kv * gq, acc_kk);
-    }
+        for (int j = 0; j < 32; ++j) {
+            const float gm = G[j] - from_mid(G[j]);
+            const float gq = valid ? fast_exp2(gm) : 0.f;
+            const float gk = valid ? fast_exp2(-gm) : 0.f;
+            const float qv = elem(qp, j), kv = elem(kp, j);
+            // A = Ks (rows s), B = Qs / Kq (columns t): lane (t, q4) receives
+            // Aqk[t][4*q4 + i] and Akk[t][4*q4 + i].
+            acc_qk = mfma_f32_16x16x4(kv * gk, qv * gq, acc_qk);
+            acc_kk = mfma_f32_16x16x4(kv * gk, kv * gq, acc_kk);
+        }
+    });
 
     // This chunk's record.  Its stores are non-temporal: the records are
     // written once here and read once by stage 2, and left dirty in L2 they
@@ -327,20 +341,22 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(BOTH ? 2 : 3
         // kg = bf16(k^ * 2^(G_last - G)) in F order (the A operand of
         // kg @ dh), and the decay 2^G_last.
         u32x2 kgF[8];
+        bcast_last([&](auto from_last) {
 #pragma unroll
-        for (int kt = 0; kt < 8; ++kt) {
-            float kg[4], gl[4];
+            for (int kt = 0; kt < 8; ++kt) {
+                float kg[4], gl[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                gl[i] = shfl(G[4 * kt + i], row0 | last);
-                kg[i] = elem(kp, 4 * kt + i) * fast_exp2(gl[i] - G[4 * kt + i]);
+                for (int i = 0; i < 4; ++i) {
+                    gl[i] = from_last(G[4 * kt + i]);
+                    kg[i] = elem(kp, 4 * kt + i) * fast_exp2(gl[i] - G[4 * kt + i]);
+                }
+                kgF[kt] = pack4(kg[0], kg[1], kg[2], kg[3]);
+                if (r == 0)
+                    __builtin_nontemporal_store(
+                        f32x4{fast_exp2(gl[0]), fast_exp2(gl[1]), fast_exp2(gl[2]), fast_exp2(gl[3])},
+                        reinterpret_cast<f32x4*>(brec + BREC_DECAY + kt * 64 + q4 * 16));
             }
-            kgF[kt] = pack4(kg[0], kg[1], kg[2], kg[3]);
-            if (r == 0)
-                __builtin_nontemporal_store(
-                    f32x4{fast_exp2(gl[0]), fast_exp2(gl[1]), fast_exp2(gl[2]), fast_exp2(gl[3])},
-                    reinterpret_cast<f32x4*>(brec + BREC_DECAY + kt * 64 + q4 * 16));
-        }
+        });
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             __builtin_nontemporal_store(
@@ -428,20 +444,22 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(BOTH ? 2 : 3
 
     // ---- kg = bf16(k^ * 2^(G_last - G)) and the decay 2^G_last of the state
     // (kernels.py:282-290), kg stored in T order (stage 2's A operand).
+    bcast_last([&](auto from_last) {
 #pragma unroll
-    for (int kt = 0; kt < 8; ++kt) {
-        float kg[4], gl[4];
+        for (int kt = 0; kt < 8; ++kt) {
+            float kg[4], gl[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            gl[i] = shfl(G[4 * kt + i], row0 | last);
-            kg[i] = elem(kp, 4 * kt + i) * fast_exp2(gl[i] - G[4 * kt + i]);
+            for (int i = 0; i < 4; ++i) {
+                gl[i] = from_last(G[4 * kt + i]);
+                kg[i] = elem(kp, 4 * kt + i) * fast_exp2(gl[i] - G[4 * kt + i]);
+            }
+            lds_put(s_T, r, colbase, kt, pack4(kg[0], kg[1], kg[2], kg[3]));
+            if (r == 0)
+                __builtin_nontemporal_store(
+                    f32x4{fast_exp2(gl[0]), fast_exp2(gl[1]), fast_exp2(gl[2]), fast_exp2(gl[3])},
+                    reinterpret_cast<f32x4*>(rec + REC_DECAY + kt * 64 + q4 * 16));
         }
-        lds_put(s_T, r, colbase, kt, pack4(kg[0], kg[1], kg[2], kg[3]));
-        if (r == 0)
-            __builtin_nontemporal_store(
-                f32x4{fast_exp2(gl[0]), fast_exp2(gl[1]), fast_exp2(gl[2]), fast_exp2(gl[3])},
-                reinterpret_cast<f32x4*>(rec + REC_DECAY + kt * 64 + q4 * 16));
-    }
+    });
     __syncthreads();
     {
         i16x4 kgT[8];

@@ -137,15 +137,7 @@ __device__ __forceinline__ void read_state_ops_b(const uint8_t* slot, int lane, 
 
 // Scales the state tile kt by its decay: element i of lane (x, q4) takes
 // 2^G_last[16*kt + 4*q4 + i] from lane 2*kt + i/2 of its row (DPP
-// row_newbcast), component i % 2.
-template <int LANE>
-__device__ __forceinline__ float row_bcast(float v) {
-    constexpr int ROW_NEWBCAST = 0x150;  // DPP: lane LANE of each row to the whole row
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
-                                                                 ROW_NEWBCAST + LANE, 0xf, 0xf,
-                                                                 false));
-}
-
+// row_newbcast, row_bcast in kda_common.h), component i % 2.
 template <int KT>
 __device__ __forceinline__ f32x4 decay_tile(f32x4 st, f32x2 dc) {
     return f32x4{st[0] * row_bcast<2 * KT>(dc.x), st[1] * row_bcast<2 * KT>(dc.y),
