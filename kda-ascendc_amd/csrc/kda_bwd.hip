@@ -290,7 +290,10 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(GROUP ? 1 : 
         const int64_t rec = sp.rec0 + c;
         const int64_t vrow = (tok * HV + hv) * DK;  // v/g/dO element offset of row i
 
-        // ---- phase 1: gates, cumsum, recentred operands ------------------
+        // ---- phase 1: gates, cumsum, recentred operands; the matrix-op
+        // operands of phase 2 are loaded meanwhile ---------------------------
+        HdhOps ops;
+        load_ops(hv, ops);
         float beta = hr.beta;
         if (p.use_beta_sigmoid) beta = valid ? fast_sigmoid(hr.beta) : 0.f;
         const float ea = p.use_gate ? expf(hr.alog) : 0.f;
@@ -306,10 +309,14 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(GROUP ? 1 : 
         }
         __syncthreads();
         if ((p.use_gate || p.g_log) && t < DK) {
+            // all 16 rows of column t read first, so their reads overlap
+            float col[BT];
+#pragma unroll
+            for (int r = 0; r < BT; ++r) col[r] = sm.dqg[r][t];
             float run = 0.f;
 #pragma unroll
             for (int r = 0; r < BT; ++r) {
-                run += sm.dqg[r][t];
+                run += col[r];
                 sm.dqg[r][t] = run * RCP_LN2;
             }
         }
@@ -361,8 +368,6 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(GROUP ? 1 : 
         // dv_new / v_new and row 16*kt + x of h / dh', v columns
         // 32*jv + 8*q4 .. +7, as 16x16x32 operands.
         {
-            HdhOps ops;
-            load_ops(hv, ops);
             f32x4 aq[2], aw[2], ak[2], adq = {0.f, 0.f, 0.f, 0.f};
             float pel[2] = {0.f, 0.f};
 #pragma unroll
