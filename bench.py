@@ -300,7 +300,7 @@ def run_train(args, dev, inputs_cpu) -> dict:
         "config": {"workload": f"kda_bt16_fwd + autograd backward B={B} T={T} H={H} K=V={D}, "
                                "zero h0, all in-kernel flags, dO ~N(0,1)",
                    "global_batch": B, "seq_len": T, "heads": H, "parallelism": "none (1 GPU)"},
-        "roofline": {"bound": "hbm", "kernel": "backward (kda_bt16_bwd_hip, 6 launches)",
+        "roofline": {"bound": "hbm", "kernel": "backward (kda_bt16_bwd_hip, 5 launches)",
                      "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None,
                      "bwd_ms": round(bwd_ms, 4), "fwd_ms": round(fwd_ms, 4),

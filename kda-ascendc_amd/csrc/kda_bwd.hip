@@ -5,11 +5,11 @@
 // FLA's chunk_kda_bwd) is: recompute w/u and the chunk states, then the
 // reverse recurrence of the state gradient, then the per-chunk WY, gram,
 // gate and l2norm gradients and the reverse cumsum of dg.  Here, after the
-// recompute (stage 1, then stage 2 storing bf16 h and v_new per chunk, then
-// stage 1 again writing the backward records):
+// recompute (one stage-1 pass writing the forward and the backward records,
+// then stage 2 storing bf16 h and v_new per chunk):
 //
 //   k2_kernel<K2_BWD> (kda_k2.hip) the reverse recurrence of the state
-//                     gradient dh, stage 2's three-wave layout run over
+//                     gradient dh, stage 2's four-wave layout run over
 //                     the backward records in reverse chunk order:
 //                       dv_new = Aqk^T dO + kg dh'
 //                       dh     = 2^G_last * dh' + (scale qg)^T dO - w^T dv_new
