@@ -130,9 +130,9 @@ int to_params_recurrent(const KdaBt16Args* a, Params& p) {
     if (!a->q || !a->k || !a->v || !a->g || !a->beta || !a->o) return KDA_BT16_EINVAL;
     if (p.use_gate && !a->A_log) return KDA_BT16_EINVAL;
     if (a->dbg_Aqk || a->dbg_A_inv || a->dbg_w || a->dbg_u || a->dbg_g) return KDA_BT16_EINVAL;
-    // 16-byte state rows; 2-byte q/k/v elements read in pairs.
-    if (misaligned(a->q, 4) || misaligned(a->k, 4) || misaligned(a->v, 2) ||
-        misaligned(a->g, a->g_dtype == KDA_BT16_DTYPE_BF16 ? 2 : 4) ||
+    // 16-byte state pieces; q, k, v and g rows read in 4-column pieces.
+    if (misaligned(a->q, 16) || misaligned(a->k, 16) || misaligned(a->v, 16) ||
+        misaligned(a->g, 16) ||
         misaligned(a->beta, a->beta_dtype == KDA_BT16_DTYPE_BF16 ? 2 : 4) ||
         misaligned(a->dt_bias, 4) || misaligned(a->h0, 16) || misaligned(a->ht, 16) ||
         misaligned(a->o, (a->flags & KDA_BT16_O_FP32) ? 4 : 2))

@@ -16,21 +16,21 @@
 // decode step (README.md:503-505).  No rounding happens between tokens, so
 // with o in fp32 the kernel is also an on-GPU gold for the chunked path.
 //
-// One work-group of two waves per (batch, value head).  Lane v of the
-// work-group owns row v of S in 128 VGPRs, so the per-token products
-// S k^ and S q^ are per-lane dot products with no cross-lane reduction.
-// Each token's decay, k^ and q^ (128 values each) are formed by every wave
-// for itself (lane l: elements 2l, 2l+1; the l2 norms by a wave-wide
-// butterfly sum) into its own LDS area and read back as broadcasts.
-// A V-first state ([V, K], row v contiguous) is moved between HBM and the
-// lanes' rows through LDS: the work-group reads and writes it with
-// coalesced 16-byte accesses (each wave instruction covers 1 KiB of
-// consecutive memory), and each lane reads or writes its row in LDS, rows
-// padded to 132 floats so that the 16-byte row accesses of 16 consecutive
-// lanes fall in distinct banks.  Read directly, lane v's 16-byte pieces of
-// row v sit 512 bytes apart across the wave and every load instruction
-// touches 64 cache lines.  A K-first state ([K, V]) is already coalesced
-// for this lane-per-row layout (lane v reads S[k][v] for each k).
+// One work-group of 256 threads per (sequence or batch row, value head).
+// Thread t = 32 * hw + j holds the 64 state elements at memory offsets
+// 1024 * i + 4 * t + c (i = 0..15, c = 0..3) of the head's 128 x 128 state,
+// so every state load and store is a 16-byte access and each wave
+// instruction covers 1 KiB of consecutive memory, in either layout.  What
+// those elements are depends on the layout:
+//   V-first ([V, K], row v contiguous): S[v = 8i + hw][k = 4j + c].  The
+//     products S k^ and S q^ reduce over k across the 32 lanes of a
+//     half-wave (hw), which all hold one set of rows.
+//   K-first ([K, V]): S[v = 4j + c][k = 8i + hw].  The products reduce
+//     over i in registers, then over the eight half-waves: lane pairs of a
+//     wave by a shuffle, the four waves through LDS.
+// The state lives in registers for the whole sequence (64 floats per
+// thread), so four work-groups share a CU and the decode step streams the
+// states at the memory system's rate.
 // Grouped value heads (GVA): value head hv reads q/k head hv / (HV / H)
 // (kernels.py:88).  Varlen: one work-group per (sequence, value head), over
 // the sequence's tokens, with states [N, HV, ...].
@@ -40,152 +40,286 @@ namespace kda {
 
 namespace {
 
+constexpr int RT = 256;  // threads per work-group
+
 __device__ __forceinline__ float load_scalar(const void* base, int is_bf16, int64_t i) {
     return is_bf16 ? bf2f(static_cast<const uint16_t*>(base)[i])
                    : static_cast<const float*>(base)[i];
 }
 
-__device__ __forceinline__ float wave_sum(float x) {
+// Sum over the 32 lanes of a half-wave; every lane receives it.
+__device__ __forceinline__ float half_sum(float x) {
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
+    for (int m = 16; m >= 1; m >>= 1) x += __shfl_xor(x, m, 32);
     return x;
 }
 
 __device__ __forceinline__ float sigmoid_precise(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-constexpr int SROW = DK + 4;  // padded LDS row of the state, in floats
-constexpr int NTHREADS = 128;
+// The decay alpha of one element of a token, in the three gate modes; gp is
+// the element's G_{t-1} of the cumsum form (reset every 16 tokens).
+__device__ __forceinline__ float decay_of(const Params& p, float g, float ea, float dtb, float& gp,
+                                          bool chunk_start) {
+    if (p.use_gate) return expf(p.lower_bound * sigmoid_precise(ea * (g + dtb)));
+    if (p.g_log) return expf(g);
+    if (chunk_start) gp = 0.0f;
+    const float a = exp2f(g - gp);
+    gp = g;
+    return a;
+}
 
-__global__ __launch_bounds__(NTHREADS) void recurrent_kernel(Params p) {
+// One token's raw inputs for this thread.  V-first: q, k and g at the
+// thread's columns 4j .. 4j+3 and, for threads 0..31, v[4t .. 4t+3] (staged
+// for the work-group).  K-first: q, k and g at columns 2l, 2l+1 for the
+// lanes l of wave 0 (which form the token's vectors), and v[4j .. 4j+3]
+// for every thread.  beta for all.
+struct TokRaw {
+    u32x2 q, k;
+    float g[4];
+    float beta;
+    u32x2 v;
+};
+
+template <bool VFIRST>
+__device__ __forceinline__ void load_tok(const Params& p, const SeqSpan& sp, int tt, int h, int hv,
+                                         int t, TokRaw& r) {
+    const int64_t rq = (sp.tok0 + tt) * p.H + h;
+    const int64_t rv = (sp.tok0 + tt) * p.HV + hv;
+    const int j = t & 31;
+    r.q = r.k = r.v = u32x2{0u, 0u};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) r.g[c] = 0.f;
+    if (VFIRST) {
+        const int col = 4 * j;
+        r.q = *reinterpret_cast<const u32x2*>(p.q + rq * DK + col);
+        r.k = *reinterpret_cast<const u32x2*>(p.k + rq * DK + col);
+        if (p.g_bf16) {
+            const u32x2 gw =
+                *reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(p.g) + rv * DK + col);
+            r.g[0] = __builtin_bit_cast(float, gw.x << 16);
+            r.g[1] = __builtin_bit_cast(float, gw.x & 0xffff0000u);
+            r.g[2] = __builtin_bit_cast(float, gw.y << 16);
+            r.g[3] = __builtin_bit_cast(float, gw.y & 0xffff0000u);
+        } else {
+            const f32x4 gv =
+                *reinterpret_cast<const f32x4*>(static_cast<const float*>(p.g) + rv * DK + col);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) r.g[c] = gv[c];
+        }
+        if (t < 32) r.v = *reinterpret_cast<const u32x2*>(p.v + rv * DK + 4 * t);
+    } else {
+        if (t < 64) {
+            const int col = 2 * t;
+            r.q.x = *reinterpret_cast<const uint32_t*>(p.q + rq * DK + col);
+            r.k.x = *reinterpret_cast<const uint32_t*>(p.k + rq * DK + col);
+            if (p.g_bf16) {
+                const uint32_t gw =
+                    *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(p.g) + rv * DK + col);
+                r.g[0] = __builtin_bit_cast(float, gw << 16);
+                r.g[1] = __builtin_bit_cast(float, gw & 0xffff0000u);
+            } else {
+                const f32x2 gv =
+                    *reinterpret_cast<const f32x2*>(static_cast<const float*>(p.g) + rv * DK + col);
+                r.g[0] = gv.x;
+                r.g[1] = gv.y;
+            }
+        }
+        r.v = *reinterpret_cast<const u32x2*>(p.v + rv * DK + 4 * j);
+    }
+    r.beta = load_scalar(p.beta, p.beta_bf16, rv);
+}
+
+__device__ __forceinline__ float lo16(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+__device__ __forceinline__ float hi16(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
+
+__device__ __forceinline__ void store_o(const Params& p, int64_t idx, float x) {
+    if (p.o_fp32) {
+        reinterpret_cast<float*>(p.o)[idx] = x;
+    } else {
+        p.o[idx] = f2bf(x);
+    }
+}
+
+template <bool VFIRST>
+__global__ __launch_bounds__(RT) void recurrent_kernel(Params p) {
     const int HV = p.HV, H = p.H;
     const int bhv = blockIdx.x;  // (batch row or sequence) * HV + hv
     const int hv = bhv - (bhv / HV) * HV;
     const int h = hv / (HV / H);
     const SeqSpan sp = seq_span(p, bhv);
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int vrow = 64 * w + lane;  // this lane's row of S
-    const int k0 = 2 * lane;         // this lane's two elements of the token vectors
-
-    // Per wave: [0] decay, [1] k^, [2] q^ of the current token.
-    __shared__ __attribute__((aligned(16))) float vec[2][3][DK];
-    // A V-first state on its way in or out.
-    __shared__ __attribute__((aligned(16))) float stage[DK * SROW];
-
-    float S[DK];
+    const int t = threadIdx.x;
+    const int w = t >> 6, hw = t >> 5, j = t & 31;
     const int64_t sbase = (int64_t)bhv * DK * DK;
+
+    // V-first: the token's v, double-buffered by token parity.
+    __shared__ __attribute__((aligned(16))) float s_v[2][DK];
+    // K-first: the token's decay, k^ and q^ (formed by wave 0), and the
+    // per-wave partial sums of S k^ and S q^.
+    __shared__ __attribute__((aligned(16))) float s_vec[3][DK];
+    __shared__ __attribute__((aligned(16))) float s_red[2][4][DK];
+
+    f32x4 S[16];
+    const float* h0 = p.h0 ? p.h0 + sbase : nullptr;
 #pragma unroll
-    for (int k = 0; k < DK; ++k) S[k] = 0.0f;
-    if (p.h0) {
-        if (p.h0_v_first) {
-            // pass i: thread x moves floats 4 * (128 i + x) .. + 3
-#pragma unroll 8
-            for (int i = 0; i < DK * DK / (4 * NTHREADS); ++i) {
-                const int e = 4 * (i * NTHREADS + (int)threadIdx.x);
-                const f32x4 r = *reinterpret_cast<const f32x4*>(p.h0 + sbase + e);
-                *reinterpret_cast<f32x4*>(stage + (e >> 7) * SROW + (e & (DK - 1))) = r;
-            }
-            __syncthreads();
-#pragma unroll
-            for (int k = 0; k < DK; k += 4) {
-                const f32x4 r = *reinterpret_cast<const f32x4*>(stage + vrow * SROW + k);
-                S[k] = r[0]; S[k + 1] = r[1]; S[k + 2] = r[2]; S[k + 3] = r[3];
-            }
-        } else {
-#pragma unroll
-            for (int k = 0; k < DK; ++k) S[k] = p.h0[sbase + (int64_t)k * DK + vrow];
-        }
+    for (int i = 0; i < 16; ++i) {
+        S[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (h0) S[i] = *reinterpret_cast<const f32x4*>(h0 + 1024 * i + 4 * t);
     }
 
     const float ea = p.use_gate ? expf(p.A_log[hv]) : 0.0f;
-    float dtb0 = 0.0f, dtb1 = 0.0f;
-    if (p.use_gate && p.dt_bias) {
-        dtb0 = p.dt_bias[hv * DK + k0];
-        dtb1 = p.dt_bias[hv * DK + k0 + 1];
+    // V-first: every thread forms its columns 4j .. 4j+3; K-first: wave 0
+    // forms columns 2*lane, 2*lane+1 for the work-group.
+    const int col = VFIRST ? 4 * j : 2 * (t & 63);
+    const bool former = VFIRST || w == 0;
+    float dtb[4] = {0.f, 0.f, 0.f, 0.f};
+    if (p.use_gate && p.dt_bias && former) {
+#pragma unroll
+        for (int c = 0; c < (VFIRST ? 4 : 2); ++c) dtb[c] = p.dt_bias[hv * DK + col + c];
     }
+    float gp[4] = {0.f, 0.f, 0.f, 0.f};  // G_{t-1} of the cumsum form
+    const bool vlane = VFIRST ? t < 32 : true;  // V-first: threads that stage v
 
-    float gp0 = 0.0f, gp1 = 0.0f;  // G_{t-1} of the cumsum form
-    for (int t = 0; t < sp.len; ++t) {
-        const int64_t rq = (sp.tok0 + t) * H + h;   // q/k row
-        const int64_t rv = (sp.tok0 + t) * HV + hv; // v/g/beta/o row
+    TokRaw cur, nxt;
+    if (sp.len > 0) load_tok<VFIRST>(p, sp, 0, h, hv, t, cur);
+    for (int tt = 0; tt < sp.len; ++tt) {
+        if (tt + 1 < sp.len) load_tok<VFIRST>(p, sp, tt + 1, h, hv, t, nxt);
+        const int64_t rv = (sp.tok0 + tt) * HV + hv;
+        const bool chunk_start = (tt % BT) == 0;
+        float beta = cur.beta;
+        if (p.use_beta_sigmoid) beta = sigmoid_precise(beta);
 
-        float q0 = bf2f(p.q[rq * DK + k0]), q1 = bf2f(p.q[rq * DK + k0 + 1]);
-        float c0 = bf2f(p.k[rq * DK + k0]), c1 = bf2f(p.k[rq * DK + k0 + 1]);
-        if (p.use_l2norm) {
-            const float nq = sqrtf(wave_sum(q0 * q0 + q1 * q1) + L2_EPS);
-            const float nk = sqrtf(wave_sum(c0 * c0 + c1 * c1) + L2_EPS);
-            q0 /= nq; q1 /= nq;
-            c0 /= nk; c1 /= nk;
-        }
-        const float g0 = load_scalar(p.g, p.g_bf16, rv * DK + k0);
-        const float g1 = load_scalar(p.g, p.g_bf16, rv * DK + k0 + 1);
-        float a0, a1;
-        if (p.use_gate) {
-            a0 = expf(p.lower_bound * sigmoid_precise(ea * (g0 + dtb0)));
-            a1 = expf(p.lower_bound * sigmoid_precise(ea * (g1 + dtb1)));
-        } else if (p.g_log) {
-            a0 = expf(g0);
-            a1 = expf(g1);
-        } else {
-            if (t % BT == 0) gp0 = gp1 = 0.0f;
-            a0 = exp2f(g0 - gp0);
-            a1 = exp2f(g1 - gp1);
-            gp0 = g0;
-            gp1 = g1;
-        }
-        vec[w][0][k0] = a0; vec[w][0][k0 + 1] = a1;
-        vec[w][1][k0] = c0; vec[w][1][k0 + 1] = c1;
-        vec[w][2][k0] = q0; vec[w][2][k0 + 1] = q1;
-
-        float bt = load_scalar(p.beta, p.beta_bf16, rv);
-        if (p.use_beta_sigmoid) bt = sigmoid_precise(bt);
-        const float vt = bf2f(p.v[rv * DK + vrow]);
-
-        // Lanes read what other lanes of the wave wrote: the wave barrier
-        // keeps the compiler from moving reads above the writes, and one
-        // wave's LDS operations execute in order.
-        __builtin_amdgcn_wave_barrier();
-        float pred = 0.0f;
+        if constexpr (VFIRST) {
+            // this thread's columns of q^, k^ and the decay
+            float qv[4] = {lo16(cur.q.x), hi16(cur.q.x), lo16(cur.q.y), hi16(cur.q.y)};
+            float kv[4] = {lo16(cur.k.x), hi16(cur.k.x), lo16(cur.k.y), hi16(cur.k.y)};
+            if (p.use_l2norm) {
+                float sq = 0.f, sk = 0.f;
 #pragma unroll
-        for (int k = 0; k < DK; ++k) {
-            S[k] *= vec[w][0][k];
-            pred = fmaf(S[k], vec[w][1][k], pred);
-        }
-        const float vnew = bt * (vt - pred);
-        float acc = 0.0f;
+                for (int c = 0; c < 4; ++c) {
+                    sq = fmaf(qv[c], qv[c], sq);
+                    sk = fmaf(kv[c], kv[c], sk);
+                }
+                const float nq = sqrtf(half_sum(sq) + L2_EPS);
+                const float nk = sqrtf(half_sum(sk) + L2_EPS);
 #pragma unroll
-        for (int k = 0; k < DK; ++k) {
-            S[k] = fmaf(vnew, vec[w][1][k], S[k]);
-            acc = fmaf(S[k], vec[w][2][k], acc);
-        }
-        const float ot = p.scale * acc;
-        if (p.o_fp32) {
-            reinterpret_cast<float*>(p.o)[rv * DK + vrow] = ot;
+                for (int c = 0; c < 4; ++c) {
+                    qv[c] /= nq;
+                    kv[c] /= nk;
+                }
+            }
+            float a[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) a[c] = decay_of(p, cur.g[c], ea, dtb[c], gp[c], chunk_start);
+            float* sv = s_v[tt & 1];
+            if (vlane)
+                *reinterpret_cast<f32x4*>(sv + 4 * t) =
+                    f32x4{lo16(cur.v.x), hi16(cur.v.x), lo16(cur.v.y), hi16(cur.v.y)};
+            __syncthreads();
+            float ov = 0.f;  // o of row 8 * j + hw, kept by lane j < 16
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                float part = 0.f;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    S[i][c] *= a[c];
+                    part = fmaf(S[i][c], kv[c], part);
+                }
+                const float pred = half_sum(part);
+                const float vnew = beta * (sv[8 * i + hw] - pred);
+                float po = 0.f;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    S[i][c] = fmaf(vnew, kv[c], S[i][c]);
+                    po = fmaf(S[i][c], qv[c], po);
+                }
+                const float o = half_sum(po);
+                if (j == i) ov = o;
+            }
+            if (j < 16) store_o(p, rv * DK + 8 * j + hw, p.scale * ov);
         } else {
-            p.o[rv * DK + vrow] = f2bf(ot);
+            // wave 0 forms the token's decay, k^ and q^ for the work-group
+            if (w == 0) {
+                float q0 = lo16(cur.q.x), q1 = hi16(cur.q.x);
+                float k0 = lo16(cur.k.x), k1 = hi16(cur.k.x);
+                if (p.use_l2norm) {
+                    float sq = fmaf(q0, q0, q1 * q1), sk = fmaf(k0, k0, k1 * k1);
+#pragma unroll
+                    for (int m = 32; m >= 1; m >>= 1) {
+                        sq += __shfl_xor(sq, m, 64);
+                        sk += __shfl_xor(sk, m, 64);
+                    }
+                    const float nq = sqrtf(sq + L2_EPS), nk = sqrtf(sk + L2_EPS);
+                    q0 /= nq; q1 /= nq;
+                    k0 /= nk; k1 /= nk;
+                }
+                const int e = 2 * t;
+                s_vec[0][e] = decay_of(p, cur.g[0], ea, dtb[0], gp[0], chunk_start);
+                s_vec[0][e + 1] = decay_of(p, cur.g[1], ea, dtb[1], gp[1], chunk_start);
+                s_vec[1][e] = k0;
+                s_vec[1][e + 1] = k1;
+                s_vec[2][e] = q0;
+                s_vec[2][e + 1] = q1;
+            }
+            __syncthreads();
+            float kv[16], qv[16];
+            float part[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int k = 8 * i + hw;
+                const float a = s_vec[0][k];
+                kv[i] = s_vec[1][k];
+                qv[i] = s_vec[2][k];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    S[i][c] *= a;
+                    part[c] = fmaf(S[i][c], kv[i], part[c]);
+                }
+            }
+            // S k^ over this thread's 16 k, then the two half-waves of the
+            // wave, then the four waves
+#pragma unroll
+            for (int c = 0; c < 4; ++c) part[c] += __shfl_xor(part[c], 32, 64);
+            if ((t & 32) == 0)
+                *reinterpret_cast<f32x4*>(&s_red[0][w][4 * j]) = f32x4{part[0], part[1], part[2], part[3]};
+            __syncthreads();
+            const float vv[4] = {lo16(cur.v.x), hi16(cur.v.x), lo16(cur.v.y), hi16(cur.v.y)};
+            float vnew[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int v = 4 * j + c;
+                const float pred = s_red[0][0][v] + s_red[0][1][v] + s_red[0][2][v] + s_red[0][3][v];
+                vnew[c] = beta * (vv[c] - pred);
+            }
+            float po[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    S[i][c] = fmaf(vnew[c], kv[i], S[i][c]);
+                    po[c] = fmaf(S[i][c], qv[i], po[c]);
+                }
+            }
+#pragma unroll
+            for (int c = 0; c < 4; ++c) po[c] += __shfl_xor(po[c], 32, 64);
+            if ((t & 32) == 0)
+                *reinterpret_cast<f32x4*>(&s_red[1][w][4 * j]) = f32x4{po[0], po[1], po[2], po[3]};
+            __syncthreads();
+            if (t < 32) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int v = 4 * j + c;
+                    const float o = s_red[1][0][v] + s_red[1][1][v] + s_red[1][2][v] + s_red[1][3][v];
+                    store_o(p, rv * DK + v, p.scale * o);
+                }
+            }
         }
-        // The next token's writes stay below this token's reads.
-        __builtin_amdgcn_wave_barrier();
+        if (tt + 1 < sp.len) cur = nxt;
     }
 
     if (p.ht) {
-        if (p.ht_v_first) {
-            // Other lanes may still be reading their rows of a staged h0.
-            __syncthreads();
+        float* ht = p.ht + sbase;
 #pragma unroll
-            for (int k = 0; k < DK; k += 4)
-                *reinterpret_cast<f32x4*>(stage + vrow * SROW + k) =
-                    f32x4{S[k], S[k + 1], S[k + 2], S[k + 3]};
-            __syncthreads();
-#pragma unroll 8
-            for (int i = 0; i < DK * DK / (4 * NTHREADS); ++i) {
-                const int e = 4 * (i * NTHREADS + (int)threadIdx.x);
-                *reinterpret_cast<f32x4*>(p.ht + sbase + e) =
-                    *reinterpret_cast<const f32x4*>(stage + (e >> 7) * SROW + (e & (DK - 1)));
-            }
-        } else {
-#pragma unroll
-            for (int k = 0; k < DK; ++k) p.ht[sbase + (int64_t)k * DK + vrow] = S[k];
-        }
+        for (int i = 0; i < 16; ++i) *reinterpret_cast<f32x4*>(ht + 1024 * i + 4 * t) = S[i];
     }
 }
 
@@ -193,7 +327,11 @@ __global__ __launch_bounds__(NTHREADS) void recurrent_kernel(Params p) {
 
 hipError_t launch_recurrent(const Params& p, hipStream_t stream) {
     const int64_t grid = (int64_t)(p.cu_seqlens ? p.N : p.B) * p.HV;
-    hipLaunchKernelGGL(recurrent_kernel, dim3((unsigned)grid), dim3(NTHREADS), 0, stream, p);
+    if (p.h0_v_first) {
+        hipLaunchKernelGGL(recurrent_kernel<true>, dim3((unsigned)grid), dim3(RT), 0, stream, p);
+    } else {
+        hipLaunchKernelGGL(recurrent_kernel<false>, dim3((unsigned)grid), dim3(RT), 0, stream, p);
+    }
     return hipGetLastError();
 }
 

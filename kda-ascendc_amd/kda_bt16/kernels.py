@@ -714,6 +714,7 @@ def kda_recurrent_fwd(
     if scale is None:
         scale = K ** -0.5
     dev = q.device
+    q, k, v, g = (_aligned(x) for x in (q, k, v, g))
     h0 = initial_state
     if h0 is not None and h0.data_ptr() % 16 != 0:
         if inplace_final_state:

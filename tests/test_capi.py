@@ -139,6 +139,9 @@ def test_recurrent_entry_argument_checks():
     full = dict(q=fake, k=fake, v=fake, g=fake, beta=fake, o=fake)
     assert f(ctypes.byref(_args(H=2, HV=4, **full, dbg_Aqk=fake)), None) == -1  # debug outputs
     assert f(ctypes.byref(_args(**full, ht=fake + 8)), None) == -1  # 16-byte state alignment
+    # q, k, v and g are read in 4-column pieces: 16-byte aligned rows
+    for name in ("q", "k", "v", "g"):
+        assert f(ctypes.byref(_args(**{**full, name: fake + 8})), None) == -1, name
     assert f(ctypes.byref(_args(**{**full, "o": fake + 2}, flags=_hip.O_FP32)), None) == -1
 
 
