@@ -29,8 +29,8 @@
 //     over i in registers, then over the eight half-waves: lane pairs of a
 //     wave by a shuffle, the four waves through LDS.
 // The state lives in registers for the whole sequence (64 floats per
-// thread), so four work-groups share a CU and the decode step streams the
-// states at the memory system's rate.
+// thread, 165 VGPRs in all), so three work-groups share a CU and the decode
+// step streams the states at close to the memory system's rate.
 // Grouped value heads (GVA): value head hv reads q/k head hv / (HV / H)
 // (kernels.py:88).  Varlen: one work-group per (sequence, value head), over
 // the sequence's tokens, with states [N, HV, ...].
