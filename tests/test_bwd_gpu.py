@@ -249,3 +249,39 @@ def test_bwd_headline_shape(gpu_device):
         assert _rel(sl(out[n]), gold[n]) < 1e-2, n
     assert _rel(out["dA_log"][hs], gold["dA_log"]) < 1e-2
     assert _rel(out["ddt_bias"].view(H, 128)[hs].reshape(-1), gold["ddt_bias"]) < 1e-2
+
+
+BWD_CONFIGS = {
+    # BASELINE configs[1] and configs[4] (configs[2] is test_bwd_headline_shape)
+    "c1_B2_T4096_H8": dict(B=2, T=4096, H=8, h0_std=0.05),
+    "c4_B16_T2048_H32": dict(B=16, T=2048, H=32, h0_std=0.05, g_std=2.0),
+}
+
+
+@pytest.mark.parametrize("name", list(BWD_CONFIGS))
+def test_bwd_baseline_configs(name, gpu_device):
+    """The backward at BASELINE sizes, with an initial state and dht: every
+    gradient finite, and two (batch, head) pairs (the op is independent per
+    pair) against the fp64 chunked restatement, gate parameters included
+    through their per-head slices.  configs[4] has strong decay (g ~N(0, 2))."""
+    cfg = dict(BWD_CONFIGS[name])
+    B, T, H = cfg.pop("B"), cfg.pop("T"), cfg.pop("H")
+    c = make_inputs(B, T, H, seed=42, **cfg)
+    gen = torch.Generator().manual_seed(17)
+    do = torch.randn(B, T, H, 128, generator=gen).to(torch.bfloat16)
+    dht = torch.randn(B, H, 128, 128, generator=gen) * 0.05
+    x = dict(q=c["q"], k=c["k"], v=c["v"], g=c["g"], beta=c["beta"], do=do, h0=c["h0"], dht=dht,
+             A_log=c["A_log"], dt_bias=c["dt_bias"])
+    print(f"[bwd] {name}", flush=True)
+    out = _hip_bwd(x, gpu_device, scale=None)
+    for n in GRADS:
+        assert torch.isfinite(out[n]).all(), n
+    for b, h in ((0, 0), (B - 1, H - 1)):
+        sl = lambda t: t[b:b + 1, :, h:h + 1].contiguous()
+        gold = chunked_backward(
+            sl(c["q"]), sl(c["k"]), sl(c["v"]), sl(c["g"]).float(), sl(c["beta"]).float(),
+            sl(do).float(), None, dht=dht[b:b + 1, h:h + 1], A_log=c["A_log"][h:h + 1],
+            dt_bias=c["dt_bias"][h * 128:(h + 1) * 128], initial_state=c["h0"][b:b + 1, h:h + 1])
+        for n in ("dq", "dk", "dv", "dg", "dbeta"):
+            assert _rel(sl(out[n]), gold[n]) < 1e-2, (b, h, n)
+        assert _rel(out["dh0"][b:b + 1, h:h + 1], gold["dh0"]) < 1e-2, (b, h)
