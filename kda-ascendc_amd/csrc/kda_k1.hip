@@ -76,38 +76,26 @@ __device__ __forceinline__ u32x2 pack4(f32x4 v) { return pack4(v.x, v.y, v.z, v.
 // also writes the backward record
 // (kda_common.h) to p.ws_bwd: the same chunk quantities in the operand
 // orders of the reverse state chain, from one read of the inputs.
-template <bool BOTH>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(BOTH ? 2 : 3))) void k1_kernel(Params p) {
-    __shared__ __attribute__((aligned(16))) uint16_t s_T[BT * LROW];  // transpose tile
-    __shared__ __attribute__((aligned(16))) float s_L[BT * BT];
-    __shared__ float s_X[BT * (BT + 1)];
+// LDS of a work-group (one wave): the transpose tile, L and the solve's
+// columns.
+__shared__ __attribute__((aligned(16))) uint16_t s_T[BT * LROW];
+__shared__ __attribute__((aligned(16))) float s_L[BT * BT];
+__shared__ float s_X[BT * (BT + 1)];
 
+// One chunk (value head hv, chunk c of sequence sp).  FULL: all 16 rows
+// are tokens (every chunk but a sequence's partial last one), so the
+// row-validity selects and the rows mid = 8, last = 15 are compile-time.
+template <bool BOTH, bool FULL>
+__device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const SeqSpan& sp) {
     const int lane = threadIdx.x;
     const int r = lane & 15;
     const int q4 = lane >> 4;
     const int colbase = 4 * q4;
     const int H = p.H, HV = p.HV;
-    int hv, c;
-    SeqSpan sp;
-    if (p.cu_seqlens) {
-        // Slot x of value head hv belongs to the sequence n with the largest
-        // floor(bos_n / 16) + n <= x; slots past its last chunk are gaps.
-        hv = blockIdx.x / p.NS;
-        const int x = blockIdx.x - hv * p.NS;
-        const int n = find_sequence(p, x, lane);
-        sp = seq_span(p, n * HV + hv);
-        c = (int)((int64_t)x - (sp.rec0 - (int64_t)hv * p.NS));
-        if (c < 0 || c >= sp.nt) return;  // wave-uniform: no barrier passed yet
-    } else {
-        c = blockIdx.x % p.NT;
-        const int bh = blockIdx.x / p.NT;
-        hv = bh - (bh / HV) * HV;
-        sp = seq_span(p, bh);
-    }
     const int h = hv / (HV / H);  // the q/k head of this value head
     const int t0 = c * BT;
-    const int nvalid = min(BT, sp.len - t0);
-    const bool valid = r < nvalid;
+    const int nvalid = FULL ? BT : min(BT, sp.len - t0);
+    const bool valid = FULL || r < nvalid;
     const int64_t tok = sp.tok0 + t0 + r;        // token of this lane's row
     const int64_t rowoff = (tok * H + h) * DK;    // q/k element offset of that row
     const int64_t vrowoff = (tok * HV + hv) * DK; // v/g element offset of that row
@@ -194,13 +182,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(BOTH ? 2 : 3
     // Row mid's and row last's values reach the rows of their 16-lane
     // group by DPP broadcast in a full chunk (mid = 8, last = 15), by a
     // cross-lane permute in a sequence's partial last chunk.
-    const bool full = nvalid == BT;
     auto bcast_mid = [&](auto use) {
-        if (full) use([](float x) { return row_bcast<BT / 2>(x); });
+        if constexpr (FULL) use([](float x) { return row_bcast<BT / 2>(x); });
         else use([&](float x) { return shfl(x, row0 | mid); });
     };
     auto bcast_last = [&](auto use) {
-        if (full) use([](float x) { return row_bcast<BT - 1>(x); });
+        if constexpr (FULL) use([](float x) { return row_bcast<BT - 1>(x); });
         else use([&](float x) { return shfl(x, row0 | last); });
     };
     f32x4 acc_qk = {0.f, 0.f, 0.f, 0.f};
@@ -488,18 +475,50 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(BOTH ? 2 : 3
     }
 }
 
+// ALL_FULL: fixed-length batch with T a multiple of 16, so every chunk is
+// full.  Otherwise every chunk takes the general path: both variants in one
+// kernel would not fit the register budget of three waves per SIMD.
+template <bool BOTH, bool ALL_FULL>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(BOTH ? 2 : 3))) void k1_kernel(Params p) {
+    const int lane = threadIdx.x;
+    const int HV = p.HV;
+    int hv, c;
+    SeqSpan sp;
+    if (p.cu_seqlens) {
+        // Slot x of value head hv belongs to the sequence n with the largest
+        // floor(bos_n / 16) + n <= x; slots past its last chunk are gaps.
+        hv = blockIdx.x / p.NS;
+        const int x = blockIdx.x - hv * p.NS;
+        const int n = find_sequence(p, x, lane);
+        sp = seq_span(p, n * HV + hv);
+        c = (int)((int64_t)x - (sp.rec0 - (int64_t)hv * p.NS));
+        if (c < 0 || c >= sp.nt) return;  // wave-uniform: no barrier passed yet
+    } else {
+        c = blockIdx.x % p.NT;
+        const int bh = blockIdx.x / p.NT;
+        hv = bh - (bh / HV) * HV;
+        sp = seq_span(p, bh);
+    }
+    k1_chunk<BOTH, ALL_FULL>(p, hv, c, sp);
+}
+
 }  // namespace
 
-hipError_t launch_k1(const Params& p, hipStream_t stream) {
+namespace {
+template <bool BOTH>
+hipError_t launch(const Params& p, hipStream_t stream) {
     const int64_t grid = p.cu_seqlens ? (int64_t)p.HV * p.NS : (int64_t)p.B * p.HV * p.NT;
-    hipLaunchKernelGGL(k1_kernel<false>, dim3((unsigned)grid), dim3(64), 0, stream, p);
+    if (!p.cu_seqlens && p.T % BT == 0) {
+        hipLaunchKernelGGL((k1_kernel<BOTH, true>), dim3((unsigned)grid), dim3(64), 0, stream, p);
+    } else {
+        hipLaunchKernelGGL((k1_kernel<BOTH, false>), dim3((unsigned)grid), dim3(64), 0, stream, p);
+    }
     return hipGetLastError();
 }
+}  // namespace
 
-hipError_t launch_k1_both_records(const Params& p, hipStream_t stream) {
-    const int64_t grid = p.cu_seqlens ? (int64_t)p.HV * p.NS : (int64_t)p.B * p.HV * p.NT;
-    hipLaunchKernelGGL(k1_kernel<true>, dim3((unsigned)grid), dim3(64), 0, stream, p);
-    return hipGetLastError();
-}
+hipError_t launch_k1(const Params& p, hipStream_t stream) { return launch<false>(p, stream); }
+
+hipError_t launch_k1_both_records(const Params& p, hipStream_t stream) { return launch<true>(p, stream); }
 
 }  // namespace kda
