@@ -82,10 +82,17 @@ __shared__ __attribute__((aligned(16))) uint16_t s_T[BT * LROW];
 __shared__ __attribute__((aligned(16))) float s_L[BT * BT];
 __shared__ float s_X[BT * (BT + 1)];
 
+// Stands in for the optional per-column operands (dt_bias, A_log) when
+// they are absent: the loads stay unconditional.  Never written; global
+// memory (not constant) so that the selected pointer stays a global one and
+// its loads are ordered with the others for the wait counters.
+__device__ float kZeroCols[DK];
+
 // One chunk (value head hv, chunk c of sequence sp).  FULL: all 16 rows
 // are tokens (every chunk but a sequence's partial last one), so the
 // row-validity selects and the rows mid = 8, last = 15 are compile-time.
-template <bool BOTH, bool FULL>
+// GB16: g is bf16 (else fp32).
+template <bool BOTH, bool FULL, bool GB16>
 __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const SeqSpan& sp) {
     const int lane = threadIdx.x;
     const int r = lane & 15;
@@ -101,32 +108,48 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
     const int64_t vrowoff = (tok * HV + hv) * DK; // v/g element offset of that row
 
     // ---- loads (kernels.py:97-106); padded rows read as zero -------------
+    // Every load of the chunk is issued before the first wait: values are
+    // converted only where they are used, and optional operands are read
+    // through a pointer select (kZeroCols when absent) rather than behind a
+    // branch, so that no load waits for another's round trip.
     Row32 qp, kp, vp;
     load_row(p.q + rowoff, valid, colbase, qp);
     load_row(p.k + rowoff, valid, colbase, kp);
     load_row(p.v + vrowoff, valid, colbase, vp);
-    float G[32];
-    if (p.g_bf16) {
-        Row32 gp;
+    Row32 dop;     // the backward's dO rows (BOTH)
+    if constexpr (BOTH) load_row(p.dout + vrowoff, valid, colbase, dop);
+    Row32 gp;      // g as bf16 (GB16)
+    f32x4 gf[8];   // g as fp32
+    if constexpr (GB16) {
         load_row(static_cast<const uint16_t*>(p.g) + vrowoff, valid, colbase, gp);
-#pragma unroll
-        for (int j = 0; j < 32; ++j) G[j] = elem(gp, j);
     } else {
         const float* gsrc = static_cast<const float*>(p.g) + vrowoff;
 #pragma unroll
         for (int kt = 0; kt < 8; ++kt) {
-            f32x4 a = {0.f, 0.f, 0.f, 0.f};
-            if (valid) a = *reinterpret_cast<const f32x4*>(gsrc + 16 * kt + colbase);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) G[4 * kt + i] = a[i];
+            gf[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (valid) gf[kt] = *reinterpret_cast<const f32x4*>(gsrc + 16 * kt + colbase);
         }
     }
-    float beta = 0.f;
+    const bool has_bias = p.use_gate && p.dt_bias;
+    const float* biasp = has_bias ? p.dt_bias + hv * DK : kZeroCols;
+    f32x4 bias[8];
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) bias[kt] = *reinterpret_cast<const f32x4*>(biasp + 16 * kt + colbase);
+    uint32_t beta_bits = 0u;  // raw: bf16 in the low half, or fp32
     if (valid) {
         const int64_t bi = tok * HV + hv;
-        beta = p.beta_bf16 ? bf2f(static_cast<const uint16_t*>(p.beta)[bi])
-                           : static_cast<const float*>(p.beta)[bi];
+        if (p.beta_bf16) beta_bits = static_cast<const uint16_t*>(p.beta)[bi];
+        else beta_bits = static_cast<const uint32_t*>(p.beta)[bi];
     }
+    float ea = expf(*(p.use_gate ? p.A_log + hv : kZeroCols));
+    asm volatile("" : "+v"(ea));  // formed here, not sunk to its use
+    float G[32];
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) G[4 * kt + i] = GB16 ? elem(gp, 4 * kt + i) : gf[kt][i];
+    }
+    float beta = __builtin_bit_cast(float, p.beta_bf16 ? beta_bits << 16 : beta_bits);
     if (p.use_beta_sigmoid) beta = fast_sigmoid(beta);
 
     // ---- q/k l2norm, rounded back to bf16 (kernels.py:108-113) -----------
@@ -154,15 +177,11 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
 
     // ---- gate and chunk-local log2 cumsum (kernels.py:115-124) -----------
     if (p.use_gate) {
-        const float ea = expf(p.A_log[hv]);
-        const float* bias = p.dt_bias ? p.dt_bias + hv * DK : nullptr;
 #pragma unroll
         for (int kt = 0; kt < 8; ++kt) {
-            f32x4 bb = {0.f, 0.f, 0.f, 0.f};
-            if (bias) bb = *reinterpret_cast<const f32x4*>(bias + 16 * kt + colbase);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float s = bias ? G[4 * kt + i] + bb[i] : G[4 * kt + i];
+                const float s = has_bias ? G[4 * kt + i] + bias[kt][i] : G[4 * kt + i];
                 float gate = p.lower_bound * fast_sigmoid(ea * s);
                 gate = valid ? gate : 0.f;
                 G[4 * kt + i] = row_scan16(gate) * RCP_LN2;
@@ -312,8 +331,6 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
         // dO as the B operand of each value tile (T order, the layout of u
         // in the forward record): [vt][lane][i] = dO[4*q4 + i][16*vt + r].
         {
-            Row32 dop;
-            load_row(p.dout + vrowoff, valid, colbase, dop);
             __syncthreads();
 #pragma unroll
             for (int kt = 0; kt < 8; ++kt) lds_put(s_T, r, colbase, kt, dop.v[kt]);
@@ -478,7 +495,7 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
 // ALL_FULL: fixed-length batch with T a multiple of 16, so every chunk is
 // full.  Otherwise every chunk takes the general path: both variants in one
 // kernel would not fit the register budget of three waves per SIMD.
-template <bool BOTH, bool ALL_FULL>
+template <bool BOTH, bool ALL_FULL, bool GB16>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(BOTH ? 2 : 3))) void k1_kernel(Params p) {
     const int lane = threadIdx.x;
     const int HV = p.HV;
@@ -499,7 +516,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(BOTH ? 2 : 3
         hv = bh - (bh / HV) * HV;
         sp = seq_span(p, bh);
     }
-    k1_chunk<BOTH, ALL_FULL>(p, hv, c, sp);
+    k1_chunk<BOTH, ALL_FULL, GB16>(p, hv, c, sp);
 }
 
 }  // namespace
@@ -508,11 +525,10 @@ namespace {
 template <bool BOTH>
 hipError_t launch(const Params& p, hipStream_t stream) {
     const int64_t grid = p.cu_seqlens ? (int64_t)p.HV * p.NS : (int64_t)p.B * p.HV * p.NT;
-    if (!p.cu_seqlens && p.T % BT == 0) {
-        hipLaunchKernelGGL((k1_kernel<BOTH, true>), dim3((unsigned)grid), dim3(64), 0, stream, p);
-    } else {
-        hipLaunchKernelGGL((k1_kernel<BOTH, false>), dim3((unsigned)grid), dim3(64), 0, stream, p);
-    }
+    const bool all_full = !p.cu_seqlens && p.T % BT == 0;
+    auto kern = all_full ? (p.g_bf16 ? k1_kernel<BOTH, true, true> : k1_kernel<BOTH, true, false>)
+                         : (p.g_bf16 ? k1_kernel<BOTH, false, true> : k1_kernel<BOTH, false, false>);
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64), 0, stream, p);
     return hipGetLastError();
 }
 }  // namespace
