@@ -114,6 +114,15 @@ struct HvRow {
     float beta, alog;
 };
 
+// The same, as loaded: packed rows and raw bits, converted only where they
+// are first used, so that no load waits for another's round trip.
+struct HvRaw {
+    u32x4 v, dvn, g[2];  // g: bf16 in g[0], or fp32 bits in g[0..1]
+    f32x4 bias[2];
+    uint32_t beta;       // bf16 in the low half, or fp32 bits
+    float alog;
+};
+
 __device__ __forceinline__ void unpack8(const u32x4& w, float (&out)[8]) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -173,47 +182,65 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(GROUP ? 1 : 
     const bool valid = i < nvalid;
     const int64_t tok = sq.tok0 + c * BT + i;
 
-    auto load_hv = [&](int hv, HvRow& r) {
+    // Every load of a value head is issued before the first wait.  Rows
+    // past the chunk's last token read that token's row (in bounds) and are
+    // zeroed where they are used; absent operands read kZeroCols.
+    const int64_t tokc = sq.tok0 + c * BT + (valid ? i : nvalid - 1);
+    const bool has_bias = p.use_gate && p.dt_bias;
+    auto load_hv = [&](int hv, HvRaw& r) {
         const SeqSpan sp = seq_span(p, seq * HV + hv);
         const int64_t rec = sp.rec0 + c;
-        const int64_t vrow = (tok * HV + hv) * DK;
-        load8(p.v + vrow + c0, valid, r.v);
-        load8(p.tr_dvn + rec * TR_VN_ELEMS + (cb >> 1) * TR_VN_TILE + i * 16 + 8 * (cb & 1), valid,
-              r.dvn);
+        const int64_t vrow = (tokc * HV + hv) * DK;
+        // (the row loads last: an address formed after a load may take that
+        // load's destination registers and wait for it)
+        const int64_t bi = tokc * HV + hv;
+        if (p.beta_bf16) r.beta = static_cast<const uint16_t*>(p.beta)[bi];
+        else r.beta = static_cast<const uint32_t*>(p.beta)[bi];
+        r.alog = *(p.use_gate ? p.A_log + hv : kZeroCols);
+        const float* biasp = has_bias ? p.dt_bias + hv * DK : kZeroCols;
+        r.bias[0] = *reinterpret_cast<const f32x4*>(biasp + c0);
+        r.bias[1] = *reinterpret_cast<const f32x4*>(biasp + c0 + 4);
+        r.dvn = *reinterpret_cast<const u32x4*>(p.tr_dvn + rec * TR_VN_ELEMS + (cb >> 1) * TR_VN_TILE +
+                                                i * 16 + 8 * (cb & 1));
+        r.v = *reinterpret_cast<const u32x4*>(p.v + vrow + c0);
+        // bf16: 16 bytes (read twice); fp32: 32 bytes
+        const uint32_t* gsrc = p.g_bf16
+            ? reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(p.g) + vrow + c0)
+            : reinterpret_cast<const uint32_t*>(static_cast<const float*>(p.g) + vrow + c0);
+        r.g[0] = *reinterpret_cast<const u32x4*>(gsrc);
+        r.g[1] = *reinterpret_cast<const u32x4*>(gsrc + (p.g_bf16 ? 0 : 4));
+    };
+    // g is the gate's argument g + dt_bias with the in-kernel gate; rows
+    // past the last token hold v = dv_new = beta = 0 and g = dt_bias.
+    auto decode_hv = [&](const HvRaw& r, HvRow& o) {
+        float v[8], dv[8], g[8];
+        unpack8(r.v, v);
+        unpack8(r.dvn, dv);
         if (p.g_bf16) {
-            load8(static_cast<const uint16_t*>(p.g) + vrow + c0, valid, r.g);
+            unpack8(r.g[0], g);
         } else {
-            f32x4 a = {0.f, 0.f, 0.f, 0.f}, b = a;
-            if (valid) {
-                a = *reinterpret_cast<const f32x4*>(static_cast<const float*>(p.g) + vrow + c0);
-                b = *reinterpret_cast<const f32x4*>(static_cast<const float*>(p.g) + vrow + c0 + 4);
-            }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                r.g[j] = a[j];
-                r.g[4 + j] = b[j];
+                // (vector elements copied out first: a bit cast of the
+                // element itself read element 0 whatever j was)
+                const uint32_t lo = r.g[0][j], hi = r.g[1][j];
+                g[j] = __builtin_bit_cast(float, lo);
+                g[4 + j] = __builtin_bit_cast(float, hi);
             }
         }
-        if (p.use_gate && p.dt_bias) {
-            const f32x4 ba = *reinterpret_cast<const f32x4*>(p.dt_bias + hv * DK + c0);
-            const f32x4 bb = *reinterpret_cast<const f32x4*>(p.dt_bias + hv * DK + c0 + 4);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                r.g[j] += ba[j];
-                r.g[4 + j] += bb[j];
-            }
+        for (int j = 0; j < 8; ++j) {
+            o.v[j] = valid ? v[j] : 0.f;
+            o.dvn[j] = valid ? dv[j] : 0.f;
+            const float gv = valid ? g[j] : 0.f;
+            o.g[j] = has_bias ? gv + r.bias[j >> 2][j & 3] : gv;
         }
-        r.beta = 0.f;
-        if (valid) {
-            const int64_t bi = tok * HV + hv;
-            r.beta = p.beta_bf16 ? bf2f(static_cast<const uint16_t*>(p.beta)[bi])
-                                 : static_cast<const float*>(p.beta)[bi];
-        }
-        r.alog = p.use_gate ? p.A_log[hv] : 0.f;
+        const float b = __builtin_bit_cast(float, p.beta_bf16 ? r.beta << 16 : r.beta);
+        o.beta = valid ? b : 0.f;
+        o.alog = r.alog;
     };
     auto load_ops = [&](int hv, HdhOps& o) {
         const int64_t rec = seq_span(p, seq * HV + hv).rec0 + c;
-        const bool xv = x < nvalid;
         const uint16_t* hrec = p.tr_h + rec * TR_H_ELEMS;
         const uint16_t* dhrec = p.tr_dh + rec * TR_H_ELEMS;
         // blocked layouts: v = 32*jv + 8*q4 + e lies in value tile
@@ -221,15 +248,13 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(GROUP ? 1 : 
         const int64_t vnoff = (q4 >> 1) * TR_VN_TILE + x * 16 + 8 * (q4 & 1);
         const uint16_t* vnrec = p.tr_vn + rec * TR_VN_ELEMS + vnoff;
         const uint16_t* dvrec = p.tr_dvn + rec * TR_VN_ELEMS + vnoff;
-        const uint16_t* dorow = p.dout + ((sq.tok0 + c * BT + x) * HV + hv) * DK + 8 * q4;
+        const int xr = x < nvalid ? x : nvalid - 1;
+        const uint16_t* dorow = p.dout + ((sq.tok0 + c * BT + xr) * HV + hv) * DK + 8 * q4;
 #pragma unroll
         for (int jv = 0; jv < 4; ++jv) {
-            o.a_do[jv] = o.a_dv[jv] = o.a_vn[jv] = u32x4{0u, 0u, 0u, 0u};
-            if (xv) {
-                o.a_do[jv] = *reinterpret_cast<const u32x4*>(dorow + 32 * jv);
-                o.a_dv[jv] = *reinterpret_cast<const u32x4*>(dvrec + 2 * jv * TR_VN_TILE);
-                o.a_vn[jv] = *reinterpret_cast<const u32x4*>(vnrec + 2 * jv * TR_VN_TILE);
-            }
+            o.a_do[jv] = *reinterpret_cast<const u32x4*>(dorow + 32 * jv);
+            o.a_dv[jv] = *reinterpret_cast<const u32x4*>(dvrec + 2 * jv * TR_VN_TILE);
+            o.a_vn[jv] = *reinterpret_cast<const u32x4*>(vnrec + 2 * jv * TR_VN_TILE);
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
                 const int kt = 2 * w + tt;
@@ -240,16 +265,23 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(GROUP ? 1 : 
             }
         }
     };
+    // Rows x past the last token of a partial chunk as zero (dO, dv_new,
+    // v_new); a full chunk skips this without waiting on the loads.
+    auto mask_ops = [&](HdhOps& o) {
+        if (nvalid < BT && x >= nvalid) {
+#pragma unroll
+            for (int jv = 0; jv < 4; ++jv) o.a_do[jv] = o.a_dv[jv] = o.a_vn[jv] = u32x4{0u, 0u, 0u, 0u};
+        }
+    };
 
     // ---- q^, k^ (kernels.py:108-113), once per q/k head; the raw rows stay
     // packed and q^ / k^ are re-formed where needed --------------------------
-    u32x4 qraw = {0u, 0u, 0u, 0u}, kraw = qraw;
-    if (valid) {
-        qraw = *reinterpret_cast<const u32x4*>(p.q + (tok * H + h) * DK + c0);
-        kraw = *reinterpret_cast<const u32x4*>(p.k + (tok * H + h) * DK + c0);
-    }
-    HvRow hr;
-    load_hv(h * rep, hr);
+    const u32x4 qraw = *reinterpret_cast<const u32x4*>(p.q + (tokc * H + h) * DK + c0);
+    const u32x4 kraw = *reinterpret_cast<const u32x4*>(p.k + (tokc * H + h) * DK + c0);
+    HvRaw hraw;
+    HdhOps ops;
+    load_ops(h * rep, ops);
+    load_hv(h * rep, hraw);
     float rq = 1.f, rk = 1.f;
     if (p.use_l2norm) {
         float qv[8], kv[8];
@@ -267,15 +299,18 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(GROUP ? 1 : 
         rk = 1.f / sqrtf(sk2 + L2_EPS);
     }
     // q^ and k^ as the forward rounds them (bf16 after the l2norm)
+    // (zero in rows past the last token)
     auto qk_hat = [&](float (&qn)[8], float (&kn)[8]) {
         unpack8(qraw, qn);
         unpack8(kraw, kn);
-        if (p.use_l2norm) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < 8; ++j) {
+            if (p.use_l2norm) {
                 qn[j] = round_bf(qn[j] * rq);
                 kn[j] = round_bf(kn[j] * rk);
             }
+            qn[j] = valid ? qn[j] : 0.f;
+            kn[j] = valid ? kn[j] : 0.f;
         }
     };
     float dQN[8], dKN[8];
@@ -285,15 +320,18 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(GROUP ? 1 : 
     const int nrep = GROUP ? rep : 1;
     for (int gi = 0; gi < nrep; ++gi) {
         const int hv = h * rep + gi;
-        if (gi > 0) load_hv(hv, hr);
+        if (gi > 0) {
+            load_ops(hv, ops);
+            load_hv(hv, hraw);
+        }
+        HvRow hr;
+        decode_hv(hraw, hr);
         const SeqSpan sp = seq_span(p, seq * HV + hv);
         const int64_t rec = sp.rec0 + c;
         const int64_t vrow = (tok * HV + hv) * DK;  // v/g/dO element offset of row i
 
         // ---- phase 1: gates, cumsum, recentred operands; the matrix-op
         // operands of phase 2 are loaded meanwhile ---------------------------
-        HdhOps ops;
-        load_ops(hv, ops);
         float beta = hr.beta;
         if (p.use_beta_sigmoid) beta = valid ? fast_sigmoid(hr.beta) : 0.f;
         const float ea = p.use_gate ? expf(hr.alog) : 0.f;
@@ -364,6 +402,7 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(GROUP ? 1 : 
         __syncthreads();  // G is read; phase 2 overwrites dqg
 
         // ---- phase 2: products over V on the matrix cores ----------------
+        mask_ops(ops);
         // Wave w owns k-tiles 2w, 2w+1.  Lane (x, q4) feeds row x of dO /
         // dv_new / v_new and row 16*kt + x of h / dh', v columns
         // 32*jv + 8*q4 .. +7, as 16x16x32 operands.

@@ -190,6 +190,15 @@ __device__ __forceinline__ SeqSpan seq_span(const Params& p, int bh) {
     return s;
 }
 
+// Stands in for an optional per-column operand (dt_bias, A_log) that is
+// absent, so that its loads stay unconditional (a pointer select, not a
+// branch).  Never written.  Global memory, not constant, so that the
+// selected pointer stays a global one and its loads are counted in order
+// with the others by the wait counters.  One copy per source file.
+namespace {
+__device__ __attribute__((visibility("hidden"))) float kZeroCols[DK];
+}
+
 // Varlen: the sequence n whose record slots hold slot x, i.e. the largest n
 // with floor(cu_seqlens[n] / 16) + n <= x (strictly increasing in n for a
 // non-decreasing cu_seqlens).  A 64-way search: each round every lane tests

@@ -82,12 +82,6 @@ __shared__ __attribute__((aligned(16))) uint16_t s_T[BT * LROW];
 __shared__ __attribute__((aligned(16))) float s_L[BT * BT];
 __shared__ float s_X[BT * (BT + 1)];
 
-// Stands in for the optional per-column operands (dt_bias, A_log) when
-// they are absent: the loads stay unconditional.  Never written; global
-// memory (not constant) so that the selected pointer stays a global one and
-// its loads are ordered with the others for the wait counters.
-__device__ float kZeroCols[DK];
-
 // One chunk (value head hv, chunk c of sequence sp).  FULL: all 16 rows
 // are tokens (every chunk but a sequence's partial last one), so the
 // row-validity selects and the rows mid = 8, last = 15 are compile-time.
