@@ -219,9 +219,10 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
         }
     });
 
-    // This chunk's record.  Its stores are non-temporal: the records are
-    // written once here and read once by stage 2, and left dirty in L2 they
-    // slow stage 2's own stores by the write-backs they force.
+    // This chunk's record, written with ordinary stores: the grid runs the
+    // chunks last to first (k1_kernel), so the records stage 2 reads first
+    // are the ones written last, still in L2 and the infinity cache.  (The
+    // backward record below is streamed out with non-temporal stores.)
     uint8_t* rec = p.ws + (sp.rec0 + c) * REC_BYTES;
 
     f32x4 aqk, L;
@@ -232,7 +233,7 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
         L[i] = (r > s) ? acc_kk[i] * beta : 0.f;
     }
     const u32x2 aqk_bf = pack4(aqk);
-    __builtin_nontemporal_store(aqk_bf, reinterpret_cast<u32x2*>(rec + REC_AQK + lane * 8));
+    *reinterpret_cast<u32x2*>(rec + REC_AQK + lane * 8) = aqk_bf;
 
     // ---- (I + L)^-1 by forward substitution (kernels.py:157-167) ---------
     // Lane r solves column s = r: a[t] = A_inv[t][s], with a[s] = 1,
@@ -379,8 +380,7 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
         for (int vt = 0; vt < 8; ++vt) {
             const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
             const u32x2 ub = pack4(mfma_bf16_16x16x16(A_op, vbT[vt], zero));
-            __builtin_nontemporal_store(
-                ub, reinterpret_cast<u32x2*>(rec + REC_U + vt * 512 + lane * 8));
+            *reinterpret_cast<u32x2*>(rec + REC_U + vt * 512 + lane * 8) = ub;
             if (p.dbg_u) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -416,8 +416,7 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const u32x4 qgj = {qgp[2 * j].x, qgp[2 * j].y, qgp[2 * j + 1].x, qgp[2 * j + 1].y};
-        __builtin_nontemporal_store(qgj,
-                                    reinterpret_cast<u32x4*>(rec + REC_QG + j * 1024 + lane * 16));
+        *reinterpret_cast<u32x4*>(rec + REC_QG + j * 1024 + lane * 16) = qgj;
     }
     __syncthreads();
     // The record holds -w (stage 2 forms u - w @ hc^T as one accumulation
@@ -436,7 +435,7 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const u32x4 wj = {wpk[2 * j].x, wpk[2 * j].y, wpk[2 * j + 1].x, wpk[2 * j + 1].y};
-        __builtin_nontemporal_store(wj, reinterpret_cast<u32x4*>(rec + REC_W + j * 1024 + lane * 16));
+        *reinterpret_cast<u32x4*>(rec + REC_W + j * 1024 + lane * 16) = wj;
     }
     __syncthreads();
 
@@ -453,9 +452,8 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
             }
             lds_put(s_T, r, colbase, kt, pack4(kg[0], kg[1], kg[2], kg[3]));
             if (r == 0)
-                __builtin_nontemporal_store(
-                    f32x4{fast_exp2(gl[0]), fast_exp2(gl[1]), fast_exp2(gl[2]), fast_exp2(gl[3])},
-                    reinterpret_cast<f32x4*>(rec + REC_DECAY + kt * 64 + q4 * 16));
+                *reinterpret_cast<f32x4*>(rec + REC_DECAY + kt * 64 + q4 * 16) =
+                    f32x4{fast_exp2(gl[0]), fast_exp2(gl[1]), fast_exp2(gl[2]), fast_exp2(gl[3])};
         }
     });
     __syncthreads();
@@ -466,9 +464,7 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
         for (int j = 0; j < 4; ++j) {
             const u32x2 a = __builtin_bit_cast(u32x2, kgT[2 * j]);
             const u32x2 bq = __builtin_bit_cast(u32x2, kgT[2 * j + 1]);
-            __builtin_nontemporal_store(
-                u32x4{a.x, a.y, bq.x, bq.y},
-                reinterpret_cast<u32x4*>(rec + REC_KG + j * 1024 + lane * 16));
+            *reinterpret_cast<u32x4*>(rec + REC_KG + j * 1024 + lane * 16) = u32x4{a.x, a.y, bq.x, bq.y};
         }
     }
 
@@ -505,8 +501,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(BOTH ? 2 : 3
         c = (int)((int64_t)x - (sp.rec0 - (int64_t)hv * p.NS));
         if (c < 0 || c >= sp.nt) return;  // wave-uniform: no barrier passed yet
     } else {
-        c = blockIdx.x % p.NT;
-        const int bh = blockIdx.x / p.NT;
+        // chunk-major, last chunk first: the work-groups in flight together
+        // read whole token rows of q/k/v/g, and the records of the first
+        // chunks, which stage 2 starts with, are written last
+        const int nbh = p.B * HV;
+        const int bh = blockIdx.x % nbh;
+        c = p.NT - 1 - (int)(blockIdx.x / nbh);
         hv = bh - (bh / HV) * HV;
         sp = seq_span(p, bh);
     }
