@@ -129,6 +129,10 @@ struct Params {
     const void* cu_seqlens;
     int cu_i64;
     int N, NS;
+    // Stage 2 with several sequences (or batch rows) per work-group: the
+    // sequences are split into seq_groups contiguous groups (set by
+    // launch_k2, 0 for one work-group per sequence).
+    int seq_groups;
     // Backward only (kda_bt16_bwd_hip).  Training buffers indexed by record
     // slot (layouts above), the incoming gradients dO [B,T,HV,V] bf16 and
     // dht (state layout of ht, optional), and the outputs: dq, dk, dv bf16 in
@@ -155,9 +159,13 @@ struct Params {
 
 // Bounds of sequence n of a varlen batch, clamped into [0, T] so that a
 // malformed cu_seqlens never leads outside the tensors.
+// cu_seqlens is read through the constant address space (it is not
+// written while a kernel runs): a uniform index then becomes a scalar load,
+// which no vector-memory wait has to cover.
 __device__ __forceinline__ int cu_at(const Params& p, int i) {
-    const int64_t x = p.cu_i64 ? static_cast<const int64_t*>(p.cu_seqlens)[i]
-                               : (int64_t) static_cast<const int32_t*>(p.cu_seqlens)[i];
+    typedef __attribute__((address_space(4))) const int64_t c_i64;
+    typedef __attribute__((address_space(4))) const int32_t c_i32;
+    const int64_t x = p.cu_i64 ? ((c_i64*)p.cu_seqlens)[i] : (int64_t)((c_i32*)p.cu_seqlens)[i];
     return (int)(x < 0 ? 0 : (x > p.T ? p.T : x));
 }
 

@@ -25,6 +25,7 @@
 // The three meet at one barrier per chunk.  Only the copy wave waits on
 // loads and only the output wave stores, so neither memory latency sits on
 // the state wave's chain.
+#include <algorithm>
 #include <type_traits>
 
 #include "kda_common.h"
@@ -735,6 +736,223 @@ __device__ __forceinline__ void state_wave(const Params& p, const Ctx& cx, int b
     store_state(p, sbase, v, q4, St);
 }
 
+// ---------------------------------------------------------------------------
+// Several sequences per work-group (forward).  With more (sequence, head,
+// value tile) triples than CUs, one work-group per triple would run in
+// rounds, each paying its own ring fill and drain.  Instead a work-group
+// takes a (group of sequences, value head, value tile) and runs the chunks
+// of its sequences as one stream of steps through the same ring: step j is
+// chunk c of sequence n in walk order.  At the first chunk of a sequence
+// the state wave finishes the previous sequence (its last update, its
+// final state stored), takes the new initial state, prefetched one
+// sequence ahead, and runs the step without the previous update.  The copy
+// and output waves only follow the walk to address records and o rows.
+// ---------------------------------------------------------------------------
+
+// Position in the walk over the non-empty sequences [.., n_end) of a group.
+struct SeqWalk {
+    int n, n_end;  // current sequence (n_end once past the last)
+    int c;         // chunk within it
+    SeqSpan sp;    // its span (value head hv)
+};
+
+// Moves to the first non-empty sequence at or after n.
+__device__ __forceinline__ void walk_seek(const Params& p, int hv, SeqWalk& w, int n) {
+    for (; n < w.n_end; ++n) {
+        w.sp = seq_span(p, n * p.HV + hv);
+        if (w.sp.nt > 0) break;
+    }
+    w.n = n;
+    w.c = 0;
+}
+
+__device__ __forceinline__ void walk_init(const Params& p, int hv, int n0, int n1, SeqWalk& w) {
+    w.n_end = n1;
+    walk_seek(p, hv, w, n0);
+}
+
+__device__ __forceinline__ void walk_advance(const Params& p, int hv, SeqWalk& w) {
+    if (++w.c == w.sp.nt) walk_seek(p, hv, w, w.n + 1);
+}
+
+// Issues the loads of sequence n's initial state (zeros without h0).  A
+// uniform branch with no use of the loaded registers, so no wait here: the
+// wait falls where the state is first used.
+__device__ __forceinline__ void issue_state_load(const Params& p, int n, int hv, int v, int q4,
+                                                 f32x4 (&St)[8]) {
+    const int64_t sbase = ((int64_t)n * p.HV + hv) * DK * DK;
+    if (p.h0 && p.h0_v_first) {
+#pragma unroll
+        for (int kt = 0; kt < 8; ++kt)
+            St[kt] = *reinterpret_cast<const f32x4*>(p.h0 + sbase + (int64_t)v * DK + 16 * kt + 4 * q4);
+    } else {
+        load_state(p, sbase, v, q4, St);
+    }
+}
+
+struct MsCtx {
+    int hv, n0, n1, J;  // value head, sequences [n0, n1), steps
+};
+
+// The state wave's step j in slot S: the pipelined step, or at a
+// sequence's first chunk, the boundary (rare, kept out of the hot path).
+template <int S, bool HAS_NEXT>
+__device__ __forceinline__ void state_step_ms(const Params& p, const Ctx& cx, const MsCtx& m,
+                                              f32x4 (&St)[8], StateOps (&op)[2], i16x4& vn,
+                                              SeqWalk& w, int& last_n, f32x4 (&Hn)[8], SeqWalk& nx) {
+    const int v = 16 * cx.vt + (cx.lane & 15);
+    if (__builtin_expect(w.c == 0, 0)) {
+        // the previous sequence's last update (chunk j - 1), then its state
+        const StateOps& prev = op[(S + 1) & 1];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const u32x2 k0 = {prev.kg[j].x, prev.kg[j].y};
+            const u32x2 k1 = {prev.kg[j].z, prev.kg[j].w};
+            St[2 * j] = mfma_bf16_16x16x16(as_i16x4(k0), vn, St[2 * j]);
+            St[2 * j + 1] = mfma_bf16_16x16x16(as_i16x4(k1), vn, St[2 * j + 1]);
+        }
+        store_state(p, ((int64_t)last_n * p.HV + m.hv) * DK * DK, v, cx.q4, St);
+#pragma unroll
+        for (int kt = 0; kt < 8; ++kt) St[kt] = Hn[kt];
+        walk_seek(p, m.hv, nx, nx.n + 1);
+        if (nx.n < m.n1) issue_state_load(p, nx.n, m.hv, v, cx.q4, Hn);
+        state_step<S, false, HAS_NEXT>(cx, St, op, vn);
+    } else {
+        state_step<S, true, HAS_NEXT>(cx, St, op, vn);
+    }
+    last_n = w.n;
+    walk_advance(p, m.hv, w);
+}
+
+template <int S, int N>
+__device__ __forceinline__ void state_round_full_ms(const Params& p, const Ctx& cx, const MsCtx& m,
+                                                    f32x4 (&St)[8], StateOps (&op)[2], i16x4& vn,
+                                                    SeqWalk& w, int& last_n, f32x4 (&Hn)[8],
+                                                    SeqWalk& nx) {
+    state_step_ms<S, true>(p, cx, m, St, op, vn, w, last_n, Hn, nx);
+    if constexpr (N > 1)
+        state_round_full_ms<(S + 1) % RING, N - 1>(p, cx, m, St, op, vn, w, last_n, Hn, nx);
+}
+
+template <int S, int N>
+__device__ __forceinline__ void state_round_tail_ms(const Params& p, const Ctx& cx, const MsCtx& m,
+                                                    int j, f32x4 (&St)[8], StateOps (&op)[2],
+                                                    i16x4& vn, SeqWalk& w, int& last_n,
+                                                    f32x4 (&Hn)[8], SeqWalk& nx) {
+    if (j >= m.J) return;
+    if (j + 1 < m.J) {
+        state_step_ms<S, true>(p, cx, m, St, op, vn, w, last_n, Hn, nx);
+    } else {
+        state_step_ms<S, false>(p, cx, m, St, op, vn, w, last_n, Hn, nx);
+    }
+    if constexpr (N > 1)
+        state_round_tail_ms<(S + 1) % RING, N - 1>(p, cx, m, j + 1, St, op, vn, w, last_n, Hn, nx);
+}
+
+__device__ __forceinline__ void state_wave_ms(const Params& p, const Ctx& cx, const MsCtx& m) {
+    const int lane = cx.lane, q4 = cx.q4;
+    const int v = 16 * cx.vt + (lane & 15);
+    // an empty sequence's final state is its initial state
+    for (int n = m.n0; n < m.n1; ++n) {
+        if (seq_span(p, n * p.HV + m.hv).nt == 0) {
+            f32x4 E[8];
+            const int64_t sb = ((int64_t)n * p.HV + m.hv) * DK * DK;
+            load_state(p, sb, v, q4, E);
+            store_state(p, sb, v, q4, E);
+        }
+    }
+    if (m.J == 0) return;
+    SeqWalk w, nx;
+    walk_init(p, m.hv, m.n0, m.n1, w);
+    f32x4 St[8], Hn[8];
+    load_state(p, ((int64_t)w.n * p.HV + m.hv) * DK * DK, v, q4, St);
+    nx = w;
+    walk_seek(p, m.hv, nx, w.n + 1);
+    if (nx.n < m.n1) issue_state_load(p, nx.n, m.hv, v, q4, Hn);
+    chunk_barrier();  // chunks 0 and 1 are in the ring
+    StateOps op[2];
+    read_state_ops_a(ring, lane, cx.vt, op[0]);
+    read_state_ops_b(ring, lane, op[0]);
+    __builtin_amdgcn_s_waitcnt(WAITCNT_LGKM0);
+    i16x4 vn;
+    if (m.J > 1) {
+        state_step<0, false, true>(cx, St, op, vn);
+    } else {
+        state_step<0, false, false>(cx, St, op, vn);
+    }
+    int last_n = w.n;
+    walk_advance(p, m.hv, w);
+    int j = 1;
+    for (; j + RING < m.J; j += RING)
+        state_round_full_ms<1, RING>(p, cx, m, St, op, vn, w, last_n, Hn, nx);
+    state_round_tail_ms<1 % RING, RING>(p, cx, m, j, St, op, vn, w, last_n, Hn, nx);
+    chunk_barrier();  // the output wave's last chunk
+    store_state(p, ((int64_t)last_n * p.HV + m.hv) * DK * DK, v, q4, St);
+}
+
+template <int S>
+__device__ __forceinline__ void output_round_ms(const Params& p, Ctx& cx, const MsCtx& m, int j,
+                                                SeqWalk& w) {
+    cx.obase = p.o + (w.sp.tok0 * p.HV + m.hv) * DK + 16 * cx.vt + 4 * ((cx.lane & 15) >> 2);
+    cx.T = w.sp.len;
+    output_step<S, false, 0>(cx, w.c);
+    walk_advance(p, m.hv, w);
+    if constexpr (S + 1 < RING) {
+        if (j + 1 < m.J) output_round_ms<S + 1>(p, cx, m, j + 1, w);
+    }
+}
+
+__device__ __forceinline__ void output_wave_ms(const Params& p, Ctx& cx, const MsCtx& m) {
+    if (m.J == 0) return;
+    SeqWalk w;
+    walk_init(p, m.hv, m.n0, m.n1, w);
+    cx.orow_stride = (int64_t)p.HV * DK;
+    chunk_barrier();
+    chunk_barrier();
+    for (int j = 0; j < m.J; j += RING) output_round_ms<0>(p, cx, m, j, w);
+}
+
+// Issues the record of the walk's current step into `slot`.
+__device__ __forceinline__ void issue_ms(const Params& p, const Ctx& cx, const SeqWalk& w,
+                                         lds_u8* slot) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        p.ws + w.sp.rec0 * REC_BYTES, (short)0, w.sp.nt * REC_BYTES, BUF_DWORD3);
+    issue_chunk(rs, (uint32_t)w.c * REC_BYTES, slot, cx.u_off, cx.voff16);
+}
+
+template <int S>
+__device__ __forceinline__ void copy_round_ms(const Params& p, const Ctx& cx, const MsCtx& m,
+                                              int j, SeqWalk& w) {
+    if (j + LEAD < m.J) {
+        issue_ms(p, cx, w, ring_lds() + ((S + LEAD) % RING) * SLOT);
+        walk_advance(p, m.hv, w);
+    }
+    if (j + 2 < m.J) wait_chunk(min(LEAD - 2, m.J - 3 - j));
+    copy_barrier();
+    if constexpr (S + 1 < RING) {
+        if (j + 1 < m.J) copy_round_ms<S + 1>(p, cx, m, j + 1, w);
+    }
+}
+
+__device__ __forceinline__ void copy_wave_ms(const Params& p, Ctx& cx, const MsCtx& m) {
+    if (m.J == 0) return;
+    SeqWalk w;
+    walk_init(p, m.hv, m.n0, m.n1, w);
+    cx.voff16 = cx.lane * 16;
+    cx.u_off = REC_U + 1024 * (cx.vt >> 1);
+#pragma unroll
+    for (int d = 0; d < LEAD; ++d) {
+        if (d < m.J) {
+            issue_ms(p, cx, w, ring_lds() + d * SLOT);
+            walk_advance(p, m.hv, w);
+        }
+    }
+    wait_chunk(m.J >= 2 ? min(LEAD, m.J) - 2 : 0);
+    copy_barrier();
+    for (int j = 0; j < m.J; j += RING) copy_round_ms<0>(p, cx, m, j, w);
+    copy_barrier();  // the output wave's last chunk
+}
+
 enum Role { STATE = 0, OUTPUT = 1, COPY = 2, OUTPUT2 = 3 };
 
 // Every wave executes exactly NT + 2 barriers: one after the prologue, one
@@ -747,14 +965,47 @@ enum Role { STATE = 0, OUTPUT = 1, COPY = 2, OUTPUT2 = 3 };
 // training buffers instead of o (output_step).  MODE K2_BWD: the backward's
 // state-gradient chain (bwd_state_wave) over the backward records, in
 // reverse chunk order, its dh' and dv_new stored like the training buffers.
-enum K2Mode { K2_FWD = 0, K2_TRAIN = 1, K2_BWD = 2 };
+// MODE K2_FWD_MS: the forward with several sequences per work-group
+// (above); grid seq_groups * HV * 8.
+enum K2Mode { K2_FWD = 0, K2_TRAIN = 1, K2_BWD = 2, K2_FWD_MS = 3 };
 
 // The training modes run a fourth wave, OUTPUT2, the second store wave.
 template <int MODE>
-__global__ __launch_bounds__(MODE == K2_FWD ? 192 : 256) void k2_kernel(Params p) {
-    constexpr bool STORE_TR = MODE != K2_FWD;
+__global__ __launch_bounds__(MODE == K2_FWD || MODE == K2_FWD_MS ? 192 : 256) void k2_kernel(Params p) {
+    constexpr bool STORE_TR = MODE == K2_TRAIN || MODE == K2_BWD;
     const int lane = threadIdx.x & 63;
     const int role = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if constexpr (MODE == K2_FWD_MS) {
+        // (group, value head, value tile), XCD aware as below
+        const int G = p.seq_groups;
+        const int ngh = G * p.HV;
+        const int wg = blockIdx.x;
+        const int lin = (wg & 7) * ngh + (wg >> 3);
+        const int gh = lin >> 3;
+        const int g = gh / p.HV;
+        const int nseq = p.cu_seqlens ? p.N : p.B;
+        MsCtx m;
+        m.hv = gh - g * p.HV;
+        m.n0 = (int)((int64_t)g * nseq / G);
+        m.n1 = (int)((int64_t)(g + 1) * nseq / G);
+        m.J = 0;
+        for (int n = m.n0; n < m.n1; ++n) m.J += seq_span(p, n * p.HV + m.hv).nt;
+        Ctx cx;
+        cx.scale = p.scale;
+        cx.lane = lane;
+        cx.q4 = lane >> 4;
+        cx.vt = lin & 7;
+        cx.rev = 0;
+        cx.NT = m.J;
+        if (role == STATE) {
+            state_wave_ms(p, cx, m);
+        } else if (role == OUTPUT) {
+            output_wave_ms(p, cx, m);
+        } else {
+            copy_wave_ms(p, cx, m);
+        }
+        __builtin_amdgcn_endpgm();
+    }
     const int nbh = (p.cu_seqlens ? p.N : p.B) * p.HV;
 
     // Work-group -> (head, value tile), XCD aware: consecutive work-group ids
@@ -817,8 +1068,34 @@ __global__ __launch_bounds__(MODE == K2_FWD ? 192 : 256) void k2_kernel(Params p
 
 }  // namespace
 
+// CUs of the current device (cached per device).
+static int cu_count() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
 hipError_t launch_k2(const Params& p, hipStream_t stream) {
-    const int64_t grid = (int64_t)(p.cu_seqlens ? p.N : p.B) * p.HV * 8;
+    const int nseq = p.cu_seqlens ? p.N : p.B;
+    const int64_t tiles = (int64_t)p.HV * 8;
+    const int ncu = cu_count();
+    if (nseq > 1 && nseq * tiles > ncu) {
+        // several sequences per work-group, in as many groups as fill the
+        // CUs once (at least one)
+        Params q = p;
+        q.seq_groups = (int)std::max<int64_t>(1, std::min<int64_t>(nseq, ncu / tiles));
+        hipLaunchKernelGGL(k2_kernel<K2_FWD_MS>, dim3((unsigned)(q.seq_groups * tiles)), dim3(192), 0,
+                           stream, q);
+        return hipGetLastError();
+    }
+    const int64_t grid = nseq * tiles;
     hipLaunchKernelGGL(k2_kernel<K2_FWD>, dim3((unsigned)grid), dim3(192), 0, stream, p);
     return hipGetLastError();
 }

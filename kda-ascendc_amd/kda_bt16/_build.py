@@ -34,6 +34,11 @@ HIPCC_FLAGS = [
     # with VALU ops every chunk, and AGPR-resident accumulators would need a
     # copy out and back each time.
     "-mllvm", "-amdgpu-mfma-vgpr-form",
+    # No implicit multiply-add fusion: each product and sum rounds where the
+    # source writes it (explicit fmaf() stays fused), so that variants of a
+    # kernel (full-chunk or not, one sequence per work-group or several)
+    # give identical bits, and the rounding follows the oracle's order.
+    "-ffp-contract=off",
 ]
 
 

@@ -203,6 +203,66 @@ def test_chunked_varlen_many_sequences(gpu_device):
         assert torch.equal(o[:, a:b], on) and torch.equal(ht[n:n + 1], htn), n
 
 
+# More (sequence, value head, value tile) triples than the GPU has CUs:
+# stage 2 then runs several sequences per work-group, in groups, through one
+# record ring (k2_kernel's multi-sequence mode).  Its results must equal one
+# call per sequence bit for bit, with empty sequences first, inside and last
+# in a group, and with or without initial and final states.
+MS_LENS = [0, 33, 16, 0, 0, 129, 1, 47, 0, 200, 15, 17, 0, 64, 3, 90, 31, 0, 48, 2,
+           77, 0, 16, 5, 250, 0, 12, 33, 8, 0, 0, 61, 19, 140, 4, 0, 28, 56, 9, 0]
+
+
+@pytest.mark.parametrize("with_h0,with_ht,vfirst",
+                         [(True, True, True), (False, True, True), (True, False, True),
+                          (True, True, False)])
+def test_varlen_multi_sequence_work_groups(with_h0, with_ht, vfirst, gpu_device):
+    cu_list = [0]
+    for n in MS_LENS:
+        cu_list.append(cu_list[-1] + n)
+    N, T, HV = len(MS_LENS), cu_list[-1], 8
+    props = torch.cuda.get_device_properties(gpu_device)
+    assert N * HV * 8 > props.multi_processor_count, "the case must exceed one work-group per CU"
+    print(f"[ms] N={N} T={T} HV={HV} h0={with_h0} ht={with_ht} vfirst={vfirst}", flush=True)
+    c = _inputs(T, 4, HV, seed=71, S=N)
+    d = _dev(c, gpu_device)
+    h0 = None
+    if with_h0:
+        h0 = d["h0"] if vfirst else d["h0"].transpose(-1, -2).contiguous()
+    cu = torch.tensor(cu_list, dtype=torch.int64, device=gpu_device)
+    kw = dict(scale=0.1, output_final_state=with_ht, state_v_first=vfirst,
+              **_gated_kw(c, gpu_device))
+    o, ht = kda_bt16_fwd(d["q"], d["k"], d["v"], d["g"], d["beta"], initial_state=h0,
+                         cu_seqlens=cu, **kw)
+    assert (ht is None) == (not with_ht)
+    for n in range(N):
+        a, b = cu_list[n], cu_list[n + 1]
+        if a == b:
+            if with_ht:
+                want = h0[n] if with_h0 else torch.zeros_like(ht[n])
+                assert torch.equal(ht[n], want), f"empty sequence {n}"
+            continue
+        on, htn = kda_bt16_fwd(*(d[x][:, a:b].contiguous() for x in ("q", "k", "v", "g", "beta")),
+                               initial_state=None if h0 is None else h0[n:n + 1].contiguous(), **kw)
+        assert torch.equal(o[:, a:b], on), f"sequence {n}: o differs"
+        if with_ht:
+            assert torch.equal(ht[n:n + 1], htn), f"sequence {n}: ht differs"
+
+
+def test_fixed_length_batch_multi_sequence_work_groups(gpu_device):
+    """B = 8 rows of 300 tokens, HV = 8: 512 triples, so stage 2 takes two
+    or more rows per work-group; each row equals its own call."""
+    B, T, HV = 8, 300, 8
+    c = _inputs(T, 2, HV, seed=73, B=B)
+    d = _dev(c, gpu_device)
+    kw = dict(scale=0.1, output_final_state=True, **_gated_kw(c, gpu_device))
+    o, ht = kda_bt16_fwd(d["q"], d["k"], d["v"], d["g"], d["beta"], initial_state=d["h0"], **kw)
+    for b in range(B):
+        ob, htb = kda_bt16_fwd(*(d[x][b:b + 1] for x in ("q", "k", "v", "g", "beta")),
+                               initial_state=d["h0"][b:b + 1], **kw)
+        assert torch.equal(o[b:b + 1], ob), f"row {b}: o differs"
+        assert torch.equal(ht[b:b + 1], htb), f"row {b}: ht differs"
+
+
 def test_varlen_single_sequence_equals_fixed_length(gpu_device):
     c = _dev(_inputs(300, 2, 2, seed=67), gpu_device)
     kw = dict(scale=0.1, initial_state=c["h0"], output_final_state=True, **_gated_kw(c))
