@@ -680,19 +680,23 @@ __device__ __forceinline__ void bwd_state_wave(const Params& p, const Ctx& cx, i
 }
 
 // S^T tiles of this lane: St[kt][i] = S[v][16*kt + 4*q4 + i], v = 16*vt + lane%16.
+// (The layout and presence tests are outside the loads, so that all of them
+// are in flight before the first wait.)
 __device__ __forceinline__ void load_state(const Params& p, int64_t sbase, int v, int q4,
                                            f32x4 (&St)[8]) {
+    if (!p.h0) {
 #pragma unroll
-    for (int kt = 0; kt < 8; ++kt) {
-        St[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (p.h0) {
-            const int k0 = 16 * kt + 4 * q4;
-            if (p.h0_v_first) {
-                St[kt] = *reinterpret_cast<const f32x4*>(p.h0 + sbase + (int64_t)v * DK + k0);
-            } else {
+        for (int kt = 0; kt < 8; ++kt) St[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    } else if (p.h0_v_first) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) St[kt][i] = p.h0[sbase + (int64_t)(k0 + i) * DK + v];
-            }
+        for (int kt = 0; kt < 8; ++kt)
+            St[kt] = *reinterpret_cast<const f32x4*>(p.h0 + sbase + (int64_t)v * DK + 16 * kt + 4 * q4);
+    } else {
+#pragma unroll
+        for (int kt = 0; kt < 8; ++kt) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                St[kt][i] = p.h0[sbase + (int64_t)(16 * kt + 4 * q4 + i) * DK + v];
         }
     }
 }
@@ -700,14 +704,16 @@ __device__ __forceinline__ void load_state(const Params& p, int64_t sbase, int v
 __device__ __forceinline__ void store_state(const Params& p, int64_t sbase, int v, int q4,
                                             const f32x4 (&St)[8]) {
     if (!p.ht) return;
+    if (p.ht_v_first) {
 #pragma unroll
-    for (int kt = 0; kt < 8; ++kt) {
-        const int k0 = 16 * kt + 4 * q4;
-        if (p.ht_v_first) {
-            *reinterpret_cast<f32x4*>(p.ht + sbase + (int64_t)v * DK + k0) = St[kt];
-        } else {
+        for (int kt = 0; kt < 8; ++kt)
+            *reinterpret_cast<f32x4*>(p.ht + sbase + (int64_t)v * DK + 16 * kt + 4 * q4) = St[kt];
+    } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) p.ht[sbase + (int64_t)(k0 + i) * DK + v] = St[kt][i];
+        for (int kt = 0; kt < 8; ++kt) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                p.ht[sbase + (int64_t)(16 * kt + 4 * q4 + i) * DK + v] = St[kt][i];
         }
     }
 }
@@ -744,9 +750,12 @@ __device__ __forceinline__ void state_wave(const Params& p, const Ctx& cx, int b
 // of its sequences as one stream of steps through the same ring: step j is
 // chunk c of sequence n in walk order.  At the first chunk of a sequence
 // the state wave finishes the previous sequence (its last update, its
-// final state stored), takes the new initial state, prefetched one
-// sequence ahead, and runs the step without the previous update.  The copy
-// and output waves only follow the walk to address records and o rows.
+// final state stored), takes the new initial state (its loads issued
+// before that update, so their latency overlaps it) and runs the step
+// without the previous update.  The copy and output waves only follow the
+// walk to address records and o rows.  The state wave keeps no load in
+// flight across steps: a pending load would make the compiler's waits in
+// later steps cover the final-state stores too.
 // ---------------------------------------------------------------------------
 
 // Position in the walk over the non-empty sequences [.., n_end) of a group.
@@ -775,34 +784,23 @@ __device__ __forceinline__ void walk_advance(const Params& p, int hv, SeqWalk& w
     if (++w.c == w.sp.nt) walk_seek(p, hv, w, w.n + 1);
 }
 
-// Issues the loads of sequence n's initial state (zeros without h0).  A
-// uniform branch with no use of the loaded registers, so no wait here: the
-// wait falls where the state is first used.
-__device__ __forceinline__ void issue_state_load(const Params& p, int n, int hv, int v, int q4,
-                                                 f32x4 (&St)[8]) {
-    const int64_t sbase = ((int64_t)n * p.HV + hv) * DK * DK;
-    if (p.h0 && p.h0_v_first) {
-#pragma unroll
-        for (int kt = 0; kt < 8; ++kt)
-            St[kt] = *reinterpret_cast<const f32x4*>(p.h0 + sbase + (int64_t)v * DK + 16 * kt + 4 * q4);
-    } else {
-        load_state(p, sbase, v, q4, St);
-    }
-}
 
 struct MsCtx {
     int hv, n0, n1, J;  // value head, sequences [n0, n1), steps
 };
 
-// The state wave's step j in slot S: the pipelined step, or at a
-// sequence's first chunk, the boundary (rare, kept out of the hot path).
+// The state wave's step j in slot S.  At a sequence's first chunk a short
+// boundary block comes first (rare, kept off the hot path): the previous
+// sequence's last update (chunk j - 1) and its final state, then the new
+// initial state, whose loads are issued before that update so their
+// latency overlaps it.  v_new is then zeroed, so the step's own update of
+// chunk j - 1 adds exact zeros, and every step runs the one pipelined body.
 template <int S, bool HAS_NEXT>
 __device__ __forceinline__ void state_step_ms(const Params& p, const Ctx& cx, const MsCtx& m,
                                               f32x4 (&St)[8], StateOps (&op)[2], i16x4& vn,
-                                              SeqWalk& w, int& last_n, f32x4 (&Hn)[8], SeqWalk& nx) {
-    const int v = 16 * cx.vt + (cx.lane & 15);
+                                              SeqWalk& w, int& last_n) {
     if (__builtin_expect(w.c == 0, 0)) {
-        // the previous sequence's last update (chunk j - 1), then its state
+        const int v = 16 * cx.vt + (cx.lane & 15);
         const StateOps& prev = op[(S + 1) & 1];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -812,41 +810,44 @@ __device__ __forceinline__ void state_step_ms(const Params& p, const Ctx& cx, co
             St[2 * j + 1] = mfma_bf16_16x16x16(as_i16x4(k1), vn, St[2 * j + 1]);
         }
         store_state(p, ((int64_t)last_n * p.HV + m.hv) * DK * DK, v, cx.q4, St);
-#pragma unroll
-        for (int kt = 0; kt < 8; ++kt) St[kt] = Hn[kt];
-        walk_seek(p, m.hv, nx, nx.n + 1);
-        if (nx.n < m.n1) issue_state_load(p, nx.n, m.hv, v, cx.q4, Hn);
-        state_step<S, false, HAS_NEXT>(cx, St, op, vn);
-    } else {
-        state_step<S, true, HAS_NEXT>(cx, St, op, vn);
+        load_state(p, ((int64_t)w.n * p.HV + m.hv) * DK * DK, v, cx.q4, St);
+        vn = i16x4{0, 0, 0, 0};
     }
+    state_step<S, true, HAS_NEXT>(cx, St, op, vn);
     last_n = w.n;
     walk_advance(p, m.hv, w);
+}
+
+// A round with no sequence boundary: the plain pipelined steps (the same
+// code as one sequence per work-group, so the hot loop stays compact).
+template <int S, int N>
+__device__ __forceinline__ void state_round_plain(const Ctx& cx, f32x4 (&St)[8], StateOps (&op)[2],
+                                                  i16x4& vn) {
+    state_step<S, true, true>(cx, St, op, vn);
+    if constexpr (N > 1) state_round_plain<(S + 1) % RING, N - 1>(cx, St, op, vn);
 }
 
 template <int S, int N>
 __device__ __forceinline__ void state_round_full_ms(const Params& p, const Ctx& cx, const MsCtx& m,
                                                     f32x4 (&St)[8], StateOps (&op)[2], i16x4& vn,
-                                                    SeqWalk& w, int& last_n, f32x4 (&Hn)[8],
-                                                    SeqWalk& nx) {
-    state_step_ms<S, true>(p, cx, m, St, op, vn, w, last_n, Hn, nx);
+                                                    SeqWalk& w, int& last_n) {
+    state_step_ms<S, true>(p, cx, m, St, op, vn, w, last_n);
     if constexpr (N > 1)
-        state_round_full_ms<(S + 1) % RING, N - 1>(p, cx, m, St, op, vn, w, last_n, Hn, nx);
+        state_round_full_ms<(S + 1) % RING, N - 1>(p, cx, m, St, op, vn, w, last_n);
 }
 
 template <int S, int N>
 __device__ __forceinline__ void state_round_tail_ms(const Params& p, const Ctx& cx, const MsCtx& m,
                                                     int j, f32x4 (&St)[8], StateOps (&op)[2],
-                                                    i16x4& vn, SeqWalk& w, int& last_n,
-                                                    f32x4 (&Hn)[8], SeqWalk& nx) {
+                                                    i16x4& vn, SeqWalk& w, int& last_n) {
     if (j >= m.J) return;
     if (j + 1 < m.J) {
-        state_step_ms<S, true>(p, cx, m, St, op, vn, w, last_n, Hn, nx);
+        state_step_ms<S, true>(p, cx, m, St, op, vn, w, last_n);
     } else {
-        state_step_ms<S, false>(p, cx, m, St, op, vn, w, last_n, Hn, nx);
+        state_step_ms<S, false>(p, cx, m, St, op, vn, w, last_n);
     }
     if constexpr (N > 1)
-        state_round_tail_ms<(S + 1) % RING, N - 1>(p, cx, m, j + 1, St, op, vn, w, last_n, Hn, nx);
+        state_round_tail_ms<(S + 1) % RING, N - 1>(p, cx, m, j + 1, St, op, vn, w, last_n);
 }
 
 __device__ __forceinline__ void state_wave_ms(const Params& p, const Ctx& cx, const MsCtx& m) {
@@ -862,13 +863,10 @@ __device__ __forceinline__ void state_wave_ms(const Params& p, const Ctx& cx, co
         }
     }
     if (m.J == 0) return;
-    SeqWalk w, nx;
+    SeqWalk w;
     walk_init(p, m.hv, m.n0, m.n1, w);
-    f32x4 St[8], Hn[8];
+    f32x4 St[8];
     load_state(p, ((int64_t)w.n * p.HV + m.hv) * DK * DK, v, q4, St);
-    nx = w;
-    walk_seek(p, m.hv, nx, w.n + 1);
-    if (nx.n < m.n1) issue_state_load(p, nx.n, m.hv, v, q4, Hn);
     chunk_barrier();  // chunks 0 and 1 are in the ring
     StateOps op[2];
     read_state_ops_a(ring, lane, cx.vt, op[0]);
@@ -882,10 +880,24 @@ __device__ __forceinline__ void state_wave_ms(const Params& p, const Ctx& cx, co
     }
     int last_n = w.n;
     walk_advance(p, m.hv, w);
+    // Rounds of RING steps from step 1 on.  Rounds without a boundary run
+    // in an inner loop of their own, so that what the boundary rounds keep
+    // live is not live there.
     int j = 1;
-    for (; j + RING < m.J; j += RING)
-        state_round_full_ms<1, RING>(p, cx, m, St, op, vn, w, last_n, Hn, nx);
-    state_round_tail_ms<1 % RING, RING>(p, cx, m, j, St, op, vn, w, last_n, Hn, nx);
+    while (j + RING < m.J) {
+        while (j + RING < m.J && w.c != 0 && w.sp.nt - w.c >= RING) {
+            state_round_plain<1, RING>(cx, St, op, vn);
+            last_n = w.n;
+            w.c += RING;
+            if (w.c == w.sp.nt) walk_seek(p, m.hv, w, w.n + 1);
+            j += RING;
+        }
+        if (j + RING < m.J) {
+            state_round_full_ms<1, RING>(p, cx, m, St, op, vn, w, last_n);
+            j += RING;
+        }
+    }
+    state_round_tail_ms<1 % RING, RING>(p, cx, m, j, St, op, vn, w, last_n);
     chunk_barrier();  // the output wave's last chunk
     store_state(p, ((int64_t)last_n * p.HV + m.hv) * DK * DK, v, q4, St);
 }
