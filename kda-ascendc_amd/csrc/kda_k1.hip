@@ -413,10 +413,13 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
         lds_put(s_T, r, colbase, kt, pack4(kb[0], kb[1], kb[2], kb[3]));
         qgp[kt] = pack4(qg[0], qg[1], qg[2], qg[3]);
     }
+    // (the backward's recompute produces no o and never reads qg)
+    if constexpr (!BOTH) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const u32x4 qgj = {qgp[2 * j].x, qgp[2 * j].y, qgp[2 * j + 1].x, qgp[2 * j + 1].y};
-        *reinterpret_cast<u32x4*>(rec + REC_QG + j * 1024 + lane * 16) = qgj;
+        for (int j = 0; j < 4; ++j) {
+            const u32x4 qgj = {qgp[2 * j].x, qgp[2 * j].y, qgp[2 * j + 1].x, qgp[2 * j + 1].y};
+            *reinterpret_cast<u32x4*>(rec + REC_QG + j * 1024 + lane * 16) = qgj;
+        }
     }
     __syncthreads();
     // The record holds -w (stage 2 forms u - w @ hc^T as one accumulation

@@ -56,6 +56,9 @@ static_assert(SHARED_LOADS * 1024 == REC_SHARED, "shared part must be whole KiB"
 static_assert(RING % HANDOFF == 0 && RING % 2 == 0, "slot indices follow the chunk index");
 static_assert(LEAD >= 2 && LEAD <= RING - 3, "ring reuse order");
 static_assert((LEAD - 1) * LOADS_PER_CHUNK <= 63, "vmcnt is a 6-bit count");
+// The training recompute (no o) skips the record's qg: 10 loads a chunk.
+constexpr int LOADS_NO_QG = LOADS_PER_CHUNK - (REC_KG - REC_QG) / 1024;
+static_assert(REC_QG % 1024 == 0 && REC_KG - REC_QG == 4096, "qg is four whole loads");
 
 // Hand-off from the state wave to the output wave, in slot c % HANDOFF:
 // hc as the four 16x16x32 B operands (lane l's 16 bytes of operand j at
@@ -72,20 +75,22 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 // Copy wave: wait until the chunk followed by `n_after` issued chunks has
 // landed (0 <= n_after <= LEAD - 2).
-template <int N>
+// NL: loads issued per chunk.
+template <int N, int NL>
 __device__ __forceinline__ void wait_chunk_ladder(int n_after) {
     if constexpr (N == 0) {
         wait_vmcnt<0>();
     } else {
         if (n_after >= N) {
-            wait_vmcnt<N * LOADS_PER_CHUNK>();
+            wait_vmcnt<N * NL>();
         } else {
-            wait_chunk_ladder<N - 1>(n_after);
+            wait_chunk_ladder<N - 1, NL>(n_after);
         }
     }
 }
 
-__device__ __forceinline__ void wait_chunk(int n_after) { wait_chunk_ladder<LEAD - 2>(n_after); }
+template <int NL = LOADS_PER_CHUNK>
+__device__ __forceinline__ void wait_chunk(int n_after) { wait_chunk_ladder<LEAD - 2, NL>(n_after); }
 
 // Buffer descriptor word 3 for raw byte-addressed buffers on gfx9-family
 // parts (gfx950 included).
@@ -93,10 +98,13 @@ constexpr int BUF_DWORD3 = 0x00020000;
 
 // One chunk's copy: 13 shared KiB, then the u pair.  Buffer loads with the
 // chunk offset in an SGPR and a fixed per-lane VGPR offset.
+// NL == LOADS_NO_QG: without qg (its slot bytes are left as they were).
+template <int NL = LOADS_PER_CHUNK>
 __device__ __forceinline__ void issue_chunk(__amdgpu_buffer_rsrc_t rs, uint32_t chunk_off,
                                             lds_u8* slot, uint32_t u_off, uint32_t voff16) {
 #pragma unroll
     for (int i = 0; i < LOADS_PER_CHUNK; ++i) {
+        if (NL == LOADS_NO_QG && i >= REC_QG / 1024 && i < REC_KG / 1024) continue;
         const uint32_t src = i < SHARED_LOADS ? chunk_off + i * 1024 : chunk_off + u_off;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_u8*)(slot + i * 1024), 16, voff16, src,
                                                  0, 0);
@@ -401,14 +409,14 @@ __device__ __forceinline__ uint32_t step_rec(const Ctx& cx, int c) {
     return (uint32_t)(cx.rev ? cx.NT - 1 - c : c) * REC_BYTES;
 }
 
-// Copy wave, chunk c (slot S).
-template <int S>
+// Copy wave, chunk c (slot S); NL loads a chunk.
+template <int S, int NL>
 __device__ __forceinline__ void copy_step(const Ctx& cx, int c) {
     if (c + LEAD < cx.NT)
-        issue_chunk(cx.rs, step_rec(cx, c + LEAD),
-                    ring_lds() + ((S + LEAD) % RING) * SLOT, cx.u_off, cx.voff16);
+        issue_chunk<NL>(cx.rs, step_rec(cx, c + LEAD),
+                        ring_lds() + ((S + LEAD) % RING) * SLOT, cx.u_off, cx.voff16);
     // chunk c + 2 is read by the state wave after this barrier
-    if (c + 2 < cx.NT) wait_chunk(min(LEAD - 2, cx.NT - 3 - c));
+    if (c + 2 < cx.NT) wait_chunk<NL>(min(LEAD - 2, cx.NT - 3 - c));
     copy_barrier();
 }
 
@@ -444,14 +452,15 @@ __device__ __forceinline__ void output_round(const Ctx& cx, int c) {
     }
 }
 
-template <int S>
+template <int S, int NL>
 __device__ __forceinline__ void copy_round(const Ctx& cx, int c) {
-    copy_step<S>(cx, c);
+    copy_step<S, NL>(cx, c);
     if constexpr (S + 1 < RING) {
-        if (c + 1 < cx.NT) copy_round<S + 1>(cx, c + 1);
+        if (c + 1 < cx.NT) copy_round<S + 1, NL>(cx, c + 1);
     }
 }
 
+template <int NL = LOADS_PER_CHUNK>
 __device__ __forceinline__ void copy_wave(const Params& p, Ctx& cx, const SeqSpan& sp) {
     const int NT = cx.NT;
     uint8_t* recs = (cx.rev ? p.ws_bwd : p.ws) + sp.rec0 * REC_BYTES;
@@ -461,11 +470,11 @@ __device__ __forceinline__ void copy_wave(const Params& p, Ctx& cx, const SeqSpa
 #pragma unroll
     for (int d = 0; d < LEAD; ++d)
         if (d < NT)
-            issue_chunk(cx.rs, step_rec(cx, d), ring_lds() + d * SLOT, cx.u_off, cx.voff16);
+            issue_chunk<NL>(cx.rs, step_rec(cx, d), ring_lds() + d * SLOT, cx.u_off, cx.voff16);
     // chunks 0 and 1 (those that exist) before the first barrier
-    wait_chunk(NT >= 2 ? min(LEAD, NT) - 2 : 0);
+    wait_chunk<NL>(NT >= 2 ? min(LEAD, NT) - 2 : 0);
     copy_barrier();
-    for (int c = 0; c < NT; c += RING) copy_round<0>(cx, c);
+    for (int c = 0; c < NT; c += RING) copy_round<0, NL>(cx, c);
     copy_barrier();  // the output wave's last chunk
 }
 
@@ -1074,7 +1083,8 @@ __global__ __launch_bounds__(MODE == K2_FWD || MODE == K2_FWD_MS ? 192 : 256) vo
             __builtin_amdgcn_endpgm();
         }
     }
-    copy_wave(p, cx, sp);
+    // the recompute for the backward stores h and v_new, not o: no qg
+    copy_wave<MODE == K2_TRAIN ? LOADS_NO_QG : LOADS_PER_CHUNK>(p, cx, sp);
     __builtin_amdgcn_endpgm();
 }
 

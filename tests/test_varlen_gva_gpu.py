@@ -263,11 +263,14 @@ def test_fixed_length_batch_multi_sequence_work_groups(gpu_device):
         assert torch.equal(ht[b:b + 1], htb), f"row {b}: ht differs"
 
 
-def test_varlen_single_sequence_equals_fixed_length(gpu_device):
-    c = _dev(_inputs(300, 2, 2, seed=67), gpu_device)
+@pytest.mark.parametrize("T", [300, 64])
+def test_varlen_single_sequence_equals_fixed_length(T, gpu_device):
+    """T = 64: the fixed-length call runs stage 1's full-chunk variant and
+    the varlen call its general one; they must agree bit for bit."""
+    c = _dev(_inputs(T, 2, 2, seed=67), gpu_device)
     kw = dict(scale=0.1, initial_state=c["h0"], output_final_state=True, **_gated_kw(c))
     o, ht = kda_bt16_fwd(c["q"], c["k"], c["v"], c["g"], c["beta"], **kw)
-    cu = torch.tensor([0, 300], dtype=torch.int64, device=gpu_device)
+    cu = torch.tensor([0, T], dtype=torch.int64, device=gpu_device)
     o2, ht2 = kda_bt16_fwd(c["q"], c["k"], c["v"], c["g"], c["beta"], cu_seqlens=cu, **kw)
     assert torch.equal(o, o2) and torch.equal(ht, ht2)
 
