@@ -627,27 +627,31 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(GROUP ? 1 : 
         // ---- phase 8: the last row's dG (through kg and the state decay),
         // then per row the reverse cumsum of dG into dgate and the gate
         // (kernels.py:115-124) -------------------------------------------
+        // One pass per column: the last row's terms, then the suffix sums
+        // over the valid rows into the dead dw tile (all 16 rows of the
+        // column read first, so their reads overlap).
         if (t < DK) {
-            float s2 = 0.f;
+            float s2 = 0.f, col[BT];
 #pragma unroll
-            for (int r = 0; r < BT; ++r) s2 += sm.km[r][t];
-            sm.kp[last][t] += LN2 * (s2 + sm.el[t] * sm.del[t]);
+            for (int r = 0; r < BT; ++r) {
+                s2 += sm.km[r][t];
+                col[r] = sm.kp[r][t];
+            }
+            const float lastterm = LN2 * (s2 + sm.el[t] * sm.del[t]);
+            float run = 0.f;
+#pragma unroll
+            for (int r = BT - 1; r >= 0; --r) {
+                if (r == last) col[r] += lastterm;
+                if (r < nvalid) run += col[r];
+                sm.dw[r][t] = r < nvalid ? run : 0.f;
+                if (r == last) sm.kp[r][t] = col[r];
+            }
         }
         __syncthreads();
         {
             float dg[8], suf[8], own[8];
             lds_get8(&sm.kp[i][c0], own);  // dG with the last row's terms
-#pragma unroll
-            for (int j = 0; j < 8; ++j) suf[j] = 0.f;
-#pragma unroll
-            for (int r = 0; r < BT; ++r) {
-                if (r >= i && r < nvalid) {
-                    float row[8];
-                    lds_get8(&sm.kp[r][c0], row);
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) suf[j] += row[j];
-                }
-            }
+            lds_get8(&sm.dw[i][c0], suf);  // its suffix sum over rows >= i
             float pdt[8], pal[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
