@@ -20,8 +20,10 @@
 //                     q/k head: the three products over V on the matrix
 //                     cores (dqg = scale dO h^T, dw = -dv_new h^T,
 //                     dkg = v_new dh'^T), then the intra-chunk gradients
-//                     in fp32 (solve, grams, recentred gates, beta, the
-//                     gate and the l2norm), dq / dk summed over the group.
+//                     in fp32 (through A = (I + L)^-1 and the gram, both
+//                     read from stage 1's record; the recentred gates,
+//                     beta, the gate and the l2norm), dq / dk summed over
+//                     the group.
 //   gate_reduce       dA_log and ddt_bias from per-chunk partial sums, in
 //                     a fixed order (deterministic).
 //
@@ -51,7 +53,7 @@ constexpr int LD = DK + 4; // fp32 row stride of the [16][128] LDS matrices
 // 74 KiB, so that two work-groups share a CU.  Tiles are reused once dead:
 // dqg first holds the gate cumsum G, dw / dvn later hold dkb / dvb, kp /
 // km / qp / dqg end as dG and the gate's column sums, and the 16x16
-// scratch takes the grams' partial sums.
+// scratch takes dA's partial sums.
 constexpr int LDB = DK + 8;  // bf16 row stride of the kb / vb tiles
 struct ChunkSmem {
     float kp[BT][LD], km[BT][LD], qp[BT][LD];
@@ -121,6 +123,7 @@ struct HvRaw {
     f32x4 bias[2];
     uint32_t beta;       // bf16 in the low half, or fp32 bits
     float alog;
+    float lraw, ainv;    // Lraw[i][cb], A_inv[i][cb] as stage 1 formed them
 };
 
 __device__ __forceinline__ void unpack8(const u32x4& w, float (&out)[8]) {
@@ -197,6 +200,9 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(GROUP ? 1 : 
         if (p.beta_bf16) r.beta = static_cast<const uint16_t*>(p.beta)[bi];
         else r.beta = static_cast<const uint32_t*>(p.beta)[bi];
         r.alog = *(p.use_gate ? p.A_log + hv : kZeroCols);
+        const float* recf = reinterpret_cast<const float*>(p.ws + rec * REC_BYTES);
+        r.lraw = recf[REC_LRAW / 4 + (i + 16 * (cb >> 2)) * 4 + (cb & 3)];
+        r.ainv = recf[REC_AINV / 4 + (i + 16 * (cb >> 2)) * 4 + (cb & 3)];
         const float* biasp = has_bias ? p.dt_bias + hv * DK : kZeroCols;
         r.bias[0] = *reinterpret_cast<const f32x4*>(biasp + c0);
         r.bias[1] = *reinterpret_cast<const f32x4*>(biasp + c0 + 4);
@@ -455,56 +461,37 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(GROUP ? 1 : 
         }
         __syncthreads();
 
-        // ---- phase 3: the grams Lraw = kp km^T (waves 0, 1: 64 columns
-        // each) and dA = dw kb^T + du vb^T (waves 2, 3), partial sums in the
-        // 16x16 scratch (m1, dlr, ainv, da) --------------------------------
+        // ---- phase 3: dA = dw kb^T + du vb^T, four partial sums in the
+        // 16x16 scratch (wave w: dw (w < 2) or du, columns 64 (w & 1) ..
+        // +63).  The gram Lraw = kp km^T and A_inv = (I + L)^-1
+        // (kernels.py:157-167) come from stage 1's record, as the forward
+        // formed them, instead of a second gram and solve here ------------
         {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            const int c64 = 64 * (w & 1);
             if (w < 2) {
 #pragma unroll
                 for (int sl = 0; sl < 16; ++sl) {
-                    const int col = 64 * w + 4 * sl + q4;
-                    acc = mfma_f32_16x16x4(sm.kp[x][col], sm.km[x][col], acc);
-                }
-            } else if (w == 2) {
-#pragma unroll
-                for (int sl = 0; sl < 32; ++sl) {
-                    const int col = 4 * sl + q4;
+                    const int col = c64 + 4 * sl + q4;
                     acc = mfma_f32_16x16x4(sm.dw[x][col], bf2f(sm.kb[x][col]), acc);
                 }
             } else {
 #pragma unroll
-                for (int sl = 0; sl < 32; ++sl) {
-                    const int col = 4 * sl + q4;
+                for (int sl = 0; sl < 16; ++sl) {
+                    const int col = c64 + 4 * sl + q4;
                     acc = mfma_f32_16x16x4(sm.dvn[x][col], bf2f(sm.vb[x][col]), acc);
                 }
             }
-            float (*part)[BT + 1] = w == 0 ? sm.m1 : w == 1 ? sm.dlr : w == 2 ? sm.ainv : sm.da;
+            float (*part)[BT + 1] = w == 0 ? sm.m1 : w == 1 ? sm.dlr : w == 2 ? sm.da : sm.lraw;
 #pragma unroll
             for (int e = 0; e < 4; ++e) part[4 * q4 + e][x] = acc[e];
         }
         __syncthreads();
         {
-            const float lraw = sm.m1[i][cb] + sm.dlr[i][cb];
-            const float da = sm.ainv[i][cb] + sm.da[i][cb];
-            sm.lraw[i][cb] = lraw;
-            sm.m1[i][cb] = (i > cb) ? beta * lraw : 0.f;  // L, read by the solve
+            const float da = (sm.m1[i][cb] + sm.dlr[i][cb]) + (sm.da[i][cb] + sm.lraw[i][cb]);
             sm.da[i][cb] = da;
-        }
-        __syncthreads();
-        if (t < BT) {
-            // column s = t of A_inv = (I + L)^-1 (kernels.py:157-167):
-            // a[s] = 1, a[r > s] = -sum_{j<r} L[r][j] a[j]
-            float a[BT];
-#pragma unroll
-            for (int r = 0; r < BT; ++r) {
-                float acc = 0.f;
-#pragma unroll
-                for (int jj = 0; jj < r; ++jj) acc = fmaf(-sm.m1[r][jj], a[jj], acc);
-                a[r] = (r > t) ? acc : (r == t ? 1.f : 0.f);
-            }
-#pragma unroll
-            for (int r = 0; r < BT; ++r) sm.ainv[r][t] = a[r];
+            sm.lraw[i][cb] = hraw.lraw;
+            sm.ainv[i][cb] = hraw.ainv;
         }
         __syncthreads();
 
@@ -515,7 +502,7 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(GROUP ? 1 : 
             float s2 = 0.f;
 #pragma unroll
             for (int m = 0; m < BT; ++m) s2 = fmaf(sm.da[i][m], sm.ainv[cb][m], s2);
-            sm.m1[i][cb] = s2;  // (dA A^T)[i][cb]; L is dead after the solve
+            sm.m1[i][cb] = s2;  // (dA A^T)[i][cb]; m1 is free after the partial sums
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
                 const int col = 16 * (2 * w + tt) + x;

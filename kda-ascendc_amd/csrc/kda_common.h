@@ -48,6 +48,14 @@ constexpr int REC_DECAY = 12800;
 constexpr int REC_U = 13312;
 constexpr int REC_SHARED = 13312;  // bytes every value tile reads
 constexpr int REC_BYTES = 17408;
+// In the backward's copy of the forward record (written by the two-record
+// stage-1 pass) qg is not needed; its bytes hold what the per-chunk
+// gradient kernel would otherwise recompute, exactly as the forward formed
+// it: the raw gram Lraw[t][s] = kp_t . km_s (fp32, [lane][i] =
+// Lraw[r][4*q4+i]) and A_inv = (I + L)^-1 (fp32, [lane][i] =
+// A_inv[r][4*q4+i]).
+constexpr int REC_LRAW = REC_QG;
+constexpr int REC_AINV = REC_QG + 1024;
 
 // Backward record (kda_bt16_bwd_hip): what the reverse state chain feeds
 // its matrix cores, written by the backward's stage-1 pass next to the

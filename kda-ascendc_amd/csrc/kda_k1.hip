@@ -265,6 +265,11 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
 #pragma unroll
     for (int i = 0; i < 4; ++i) ainv[i] = s_X[(4 * q4 + i) * (BT + 1) + r];
     const u32x2 ainv_bf = pack4(ainv);  // A = bf16(A_inv), kernels.py:170
+    if constexpr (BOTH) {
+        // the gram and the inverse for the per-chunk gradients (kda_common.h)
+        __builtin_nontemporal_store(acc_kk, reinterpret_cast<f32x4*>(rec + REC_LRAW + lane * 16));
+        __builtin_nontemporal_store(ainv, reinterpret_cast<f32x4*>(rec + REC_AINV + lane * 16));
+    }
     const i16x4 A_op = as_i16x4(ainv_bf);
     const i16x4 A_neg = as_i16x4(ainv_bf ^ 0x80008000u);
 
