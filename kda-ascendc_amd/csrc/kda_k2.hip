@@ -759,12 +759,12 @@ __device__ __forceinline__ void state_wave(const Params& p, const Ctx& cx, int b
 // of its sequences as one stream of steps through the same ring: step j is
 // chunk c of sequence n in walk order.  At the first chunk of a sequence
 // the state wave finishes the previous sequence (its last update, its
-// final state stored), takes the new initial state (its loads issued
-// before that update, so their latency overlaps it) and runs the step
-// without the previous update.  The copy and output waves only follow the
-// walk to address records and o rows.  The state wave keeps no load in
-// flight across steps: a pending load would make the compiler's waits in
-// later steps cover the final-state stores too.
+// final state stored), loads the new initial state (one load latency per
+// sequence) and runs the step without the previous update.  The copy and
+// output waves only follow the walk to address records and o rows.  The
+// state wave keeps no load in flight across steps: a pending load would
+// make the compiler's waits in later steps cover the final-state stores
+// too.
 // ---------------------------------------------------------------------------
 
 // Position in the walk over the non-empty sequences [.., n_end) of a group.
@@ -801,9 +801,8 @@ struct MsCtx {
 // The state wave's step j in slot S.  At a sequence's first chunk a short
 // boundary block comes first (rare, kept off the hot path): the previous
 // sequence's last update (chunk j - 1) and its final state, then the new
-// initial state, whose loads are issued before that update so their
-// latency overlaps it.  v_new is then zeroed, so the step's own update of
-// chunk j - 1 adds exact zeros, and every step runs the one pipelined body.
+// initial state.  v_new is then zeroed, so the step's own update of chunk
+// j - 1 adds exact zeros, and every step runs the one pipelined body.
 template <int S, bool HAS_NEXT>
 __device__ __forceinline__ void state_step_ms(const Params& p, const Ctx& cx, const MsCtx& m,
                                               f32x4 (&St)[8], StateOps (&op)[2], i16x4& vn,
