@@ -192,6 +192,29 @@ size_t kda_bt16_bwd_workspace_bytes(const KdaBt16Args* fwd);
 
 int kda_bt16_bwd_hip(const KdaBt16BwdArgs* args, void* stream);
 
+/* Training forward that keeps its state for the backward (no counterpart in
+ * the reference, which is forward-only; FLA's chunk_kda forward saves its
+ * per-chunk states the same way, docs/KDA_ANALYSIS.md:134-165).  o and ht as
+ * kda_bt16_fwd_hip, bit for bit (args->workspace as there), and into `saved`
+ * (kda_bt16_saved_bytes(args) bytes, 256-byte aligned) what the backward
+ * would otherwise recompute: per 16-token record slot the backward record
+ * without dO (17 KiB), bf16 h (32 KiB), v_new (4 KiB) and the gram block
+ * (2 KiB), ~55 KiB (880 MiB at B=1 T=8192 H=32).  No debug outputs.
+ * Asynchronous on `stream`; allocates nothing. */
+size_t kda_bt16_saved_bytes(const KdaBt16Args* fwd);
+
+int kda_bt16_fwd_save_hip(const KdaBt16Args* args, void* saved, size_t saved_bytes, void* stream);
+
+/* Backward from the state kda_bt16_fwd_save_hip kept (same forward
+ * arguments): the gradients of kda_bt16_bwd_hip, bit for bit, without its
+ * recompute.  args->workspace: kda_bt16_bwd_saved_workspace_bytes() bytes
+ * (dh, dv_new, gate partial sums; ~36.5 KiB per slot).  dO is written into
+ * the saved backward records, so the saved state may serve several
+ * backward calls but not two at once. */
+size_t kda_bt16_bwd_saved_workspace_bytes(const KdaBt16Args* fwd);
+
+int kda_bt16_bwd_saved_hip(const KdaBt16BwdArgs* args, void* saved, size_t saved_bytes, void* stream);
+
 /* Static message for an error code. */
 const char* kda_bt16_strerror(int code);
 

@@ -200,9 +200,9 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(GROUP ? 1 : 
         if (p.beta_bf16) r.beta = static_cast<const uint16_t*>(p.beta)[bi];
         else r.beta = static_cast<const uint32_t*>(p.beta)[bi];
         r.alog = *(p.use_gate ? p.A_log + hv : kZeroCols);
-        const float* recf = reinterpret_cast<const float*>(p.ws + rec * REC_BYTES);
-        r.lraw = recf[REC_LRAW / 4 + (i + 16 * (cb >> 2)) * 4 + (cb & 3)];
-        r.ainv = recf[REC_AINV / 4 + (i + 16 * (cb >> 2)) * 4 + (cb & 3)];
+        const float* laf = reinterpret_cast<const float*>(p.la + rec * p.la_stride);
+        r.lraw = laf[LA_LRAW / 4 + (i + 16 * (cb >> 2)) * 4 + (cb & 3)];
+        r.ainv = laf[LA_AINV / 4 + (i + 16 * (cb >> 2)) * 4 + (cb & 3)];
         const float* biasp = has_bias ? p.dt_bias + hv * DK : kZeroCols;
         r.bias[0] = *reinterpret_cast<const f32x4*>(biasp + c0);
         r.bias[1] = *reinterpret_cast<const f32x4*>(biasp + c0 + 4);

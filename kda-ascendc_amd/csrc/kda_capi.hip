@@ -175,6 +175,92 @@ BwdLayout bwd_layout(int64_t R) {
     return L;
 }
 
+// The state a training forward keeps for its backward (kda_bt16_fwd_save_hip),
+// per record slot: the backward record, h, v_new and the gram block.
+struct SavedLayout {
+    size_t brec, h, vn, la, total;
+};
+
+SavedLayout saved_layout(int64_t R) {
+    SavedLayout L;
+    size_t off = 0;
+    L.brec = off;
+    off = align256(off + (size_t)R * kda::REC_BYTES);
+    L.h = off;
+    off = align256(off + (size_t)R * kda::TR_H_ELEMS * 2);
+    L.vn = off;
+    off = align256(off + (size_t)R * kda::TR_VN_ELEMS * 2);
+    L.la = off;
+    off = align256(off + (size_t)R * kda::LA_BYTES);
+    L.total = off;
+    return L;
+}
+
+// The backward's workspace when the state was saved: dh, dv_new and the
+// gate partial sums.
+struct BwdSavedLayout {
+    size_t dh, dvn, part, total;
+};
+
+BwdSavedLayout bwd_saved_layout(int64_t R) {
+    BwdSavedLayout L;
+    size_t off = 0;
+    L.dh = off;
+    off = align256(off + (size_t)R * kda::TR_H_ELEMS * 2);
+    L.dvn = off;
+    off = align256(off + (size_t)R * kda::TR_VN_ELEMS * 2);
+    L.part = off;
+    off = align256(off + (size_t)R * kda::PART_STRIDE * 4);
+    L.total = off;
+    return L;
+}
+
+// Checks of a backward call (both entry points) and its Params, without
+// the workspace.
+int bwd_params(const KdaBt16BwdArgs* b, Params& p) {
+    if (b == nullptr || b->fwd == nullptr) return KDA_BT16_EINVAL;
+    const KdaBt16Args* a = b->fwd;
+    int rc = check_common(a, p);
+    if (rc != KDA_BT16_OK) return rc;
+    if (a->flags & KDA_BT16_O_FP32) return KDA_BT16_EUNSUPPORTED;
+    const int64_t slots = a->cu_seqlens ? varlen_slots(a) : (int64_t)a->B * chunks_of(a->T);
+    if ((int64_t)a->HV * slots > I32_MAX || sequences(a) * a->HV * 8 > I32_MAX ||
+        chunks_of(a->T) * kda::REC_BYTES > I32_MAX)
+        return KDA_BT16_EUNSUPPORTED;
+    p.NS = a->cu_seqlens ? (int)varlen_slots(a) : 0;
+    if (!a->q || !a->k || !a->v || !a->g || !a->beta) return KDA_BT16_EINVAL;
+    if (p.use_gate && !a->A_log) return KDA_BT16_EINVAL;
+    if (a->dbg_Aqk || a->dbg_A_inv || a->dbg_w || a->dbg_u || a->dbg_g) return KDA_BT16_EINVAL;
+    if (!b->dout || !b->dq || !b->dk || !b->dv || !b->dg || !b->dbeta) return KDA_BT16_EINVAL;
+    if ((b->dA_log || b->ddt_bias) && !p.use_gate) return KDA_BT16_EINVAL;
+    if (b->ddt_bias && !a->dt_bias) return KDA_BT16_EINVAL;
+    const uintptr_t bsz = a->beta_dtype == KDA_BT16_DTYPE_BF16 ? 2 : 4;
+    if (misaligned(a->q, 16) || misaligned(a->k, 16) || misaligned(a->v, 16) ||
+        misaligned(a->g, 16) || misaligned(a->beta, bsz) || misaligned(a->dt_bias, 16) ||
+        misaligned(a->h0, 16) || misaligned(b->dout, 16) || misaligned(b->dht, 16) ||
+        misaligned(b->dq, 16) || misaligned(b->dk, 16) || misaligned(b->dv, 16) ||
+        misaligned(b->dg, 16) || misaligned(b->dbeta, bsz) || misaligned(b->dh0, 16) ||
+        misaligned(b->dA_log, 4) || misaligned(b->ddt_bias, 4))
+        return KDA_BT16_EINVAL;
+    p.o = nullptr;
+    p.ht = nullptr;
+    p.dout = static_cast<const uint16_t*>(b->dout);
+    p.dht = b->dht;
+    p.dq = static_cast<uint16_t*>(b->dq);
+    p.dk = static_cast<uint16_t*>(b->dk);
+    p.dv = static_cast<uint16_t*>(b->dv);
+    p.dg = b->dg;
+    p.dbeta = b->dbeta;
+    p.dA_log = b->dA_log;
+    p.ddt_bias = b->ddt_bias;
+    p.dh0 = b->dh0;
+    return KDA_BT16_OK;
+}
+
+bool bad_buffer(const void* buf, size_t bytes, size_t need) {
+    return buf == nullptr || bytes < need || (reinterpret_cast<uintptr_t>(buf) & 255u) != 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -232,57 +318,82 @@ size_t kda_bt16_bwd_workspace_bytes(const KdaBt16Args* a) {
 }
 
 int kda_bt16_bwd_hip(const KdaBt16BwdArgs* b, void* stream) {
-    if (b == nullptr || b->fwd == nullptr) return KDA_BT16_EINVAL;
-    const KdaBt16Args* a = b->fwd;
     Params p;
-    int rc = check_common(a, p);
+    int rc = bwd_params(b, p);
     if (rc != KDA_BT16_OK) return rc;
-    if (a->flags & KDA_BT16_O_FP32) return KDA_BT16_EUNSUPPORTED;
-    const int64_t slots = a->cu_seqlens ? varlen_slots(a) : (int64_t)a->B * chunks_of(a->T);
-    if ((int64_t)a->HV * slots > I32_MAX || sequences(a) * a->HV * 8 > I32_MAX ||
-        chunks_of(a->T) * kda::REC_BYTES > I32_MAX)
-        return KDA_BT16_EUNSUPPORTED;
-    p.NS = a->cu_seqlens ? (int)varlen_slots(a) : 0;
-    if (!a->q || !a->k || !a->v || !a->g || !a->beta) return KDA_BT16_EINVAL;
-    if (p.use_gate && !a->A_log) return KDA_BT16_EINVAL;
-    if (a->dbg_Aqk || a->dbg_A_inv || a->dbg_w || a->dbg_u || a->dbg_g) return KDA_BT16_EINVAL;
-    if (!b->dout || !b->dq || !b->dk || !b->dv || !b->dg || !b->dbeta) return KDA_BT16_EINVAL;
-    if ((b->dA_log || b->ddt_bias) && !p.use_gate) return KDA_BT16_EINVAL;
-    if (b->ddt_bias && !a->dt_bias) return KDA_BT16_EINVAL;
-    const uintptr_t bsz = a->beta_dtype == KDA_BT16_DTYPE_BF16 ? 2 : 4;
-    if (misaligned(a->q, 16) || misaligned(a->k, 16) || misaligned(a->v, 16) ||
-        misaligned(a->g, 16) || misaligned(a->beta, bsz) || misaligned(a->dt_bias, 16) ||
-        misaligned(a->h0, 16) || misaligned(b->dout, 16) || misaligned(b->dht, 16) ||
-        misaligned(b->dq, 16) || misaligned(b->dk, 16) || misaligned(b->dv, 16) ||
-        misaligned(b->dg, 16) || misaligned(b->dbeta, bsz) || misaligned(b->dh0, 16) ||
-        misaligned(b->dA_log, 4) || misaligned(b->ddt_bias, 4))
-        return KDA_BT16_EINVAL;
-    const BwdLayout L = bwd_layout(record_slots(a));
-    if (!b->workspace || b->workspace_bytes < L.total) return KDA_BT16_EWORKSPACE;
-    if ((reinterpret_cast<uintptr_t>(b->workspace) & 255u) != 0) return KDA_BT16_EWORKSPACE;
+    const BwdLayout L = bwd_layout(record_slots(b->fwd));
+    if (bad_buffer(b->workspace, b->workspace_bytes, L.total)) return KDA_BT16_EWORKSPACE;
     uint8_t* ws = static_cast<uint8_t*>(b->workspace);
     p.ws = ws + L.rec;
     p.ws_bwd = ws + L.brec;
+    p.la = ws + L.rec + kda::REC_QG;  // the gram blocks in qg's bytes
+    p.la_stride = kda::REC_BYTES;
     p.tr_h = reinterpret_cast<uint16_t*>(ws + L.h);
     p.tr_vn = reinterpret_cast<uint16_t*>(ws + L.vn);
     p.tr_dh = reinterpret_cast<uint16_t*>(ws + L.dh);
     p.tr_dvn = reinterpret_cast<uint16_t*>(ws + L.dvn);
     p.tr_part = (b->dA_log || b->ddt_bias) ? reinterpret_cast<float*>(ws + L.part) : nullptr;
-    p.o = nullptr;
-    p.ht = nullptr;
-    p.dout = static_cast<const uint16_t*>(b->dout);
-    p.dht = b->dht;
-    p.dq = static_cast<uint16_t*>(b->dq);
-    p.dk = static_cast<uint16_t*>(b->dk);
-    p.dv = static_cast<uint16_t*>(b->dv);
-    p.dg = b->dg;
-    p.dbeta = b->dbeta;
-    p.dA_log = b->dA_log;
-    p.ddt_bias = b->ddt_bias;
-    p.dh0 = b->dh0;
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (kda::launch_k1_both_records(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
     if (kda::launch_k2_train(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
+    if (kda::launch_k2_bwd(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
+    if (kda::launch_bwd_chunk(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
+    if (p.tr_part && kda::launch_bwd_gate_reduce(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
+    return KDA_BT16_OK;
+}
+
+size_t kda_bt16_saved_bytes(const KdaBt16Args* fwd) {
+    if (kda_bt16_workspace_bytes_args(fwd) == 0) return 0;
+    return saved_layout(record_slots(fwd)).total;
+}
+
+int kda_bt16_fwd_save_hip(const KdaBt16Args* args, void* saved, size_t saved_bytes, void* stream) {
+    Params p;
+    int rc = to_params(args, p, true, true);
+    if (rc != KDA_BT16_OK) return rc;
+    if (args->dbg_Aqk || args->dbg_A_inv || args->dbg_w || args->dbg_u || args->dbg_g)
+        return KDA_BT16_EINVAL;
+    const SavedLayout L = saved_layout(record_slots(args));
+    if (bad_buffer(saved, saved_bytes, L.total)) return KDA_BT16_EWORKSPACE;
+    uint8_t* sv = static_cast<uint8_t*>(saved);
+    p.ws_bwd = sv + L.brec;
+    p.tr_h = reinterpret_cast<uint16_t*>(sv + L.h);
+    p.tr_vn = reinterpret_cast<uint16_t*>(sv + L.vn);
+    p.la = sv + L.la;
+    p.la_stride = kda::LA_BYTES;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (kda::launch_k1_save(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
+    if (kda::launch_k2_train_o(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
+    return KDA_BT16_OK;
+}
+
+size_t kda_bt16_bwd_saved_workspace_bytes(const KdaBt16Args* fwd) {
+    if (kda_bt16_workspace_bytes_args(fwd) == 0) return 0;
+    return bwd_saved_layout(record_slots(fwd)).total;
+}
+
+int kda_bt16_bwd_saved_hip(const KdaBt16BwdArgs* b, void* saved, size_t saved_bytes, void* stream) {
+    Params p;
+    int rc = bwd_params(b, p);
+    if (rc != KDA_BT16_OK) return rc;
+    const int64_t R = record_slots(b->fwd);
+    const SavedLayout S = saved_layout(R);
+    const BwdSavedLayout L = bwd_saved_layout(R);
+    if (bad_buffer(saved, saved_bytes, S.total)) return KDA_BT16_EWORKSPACE;
+    if (bad_buffer(b->workspace, b->workspace_bytes, L.total)) return KDA_BT16_EWORKSPACE;
+    uint8_t* sv = static_cast<uint8_t*>(saved);
+    uint8_t* ws = static_cast<uint8_t*>(b->workspace);
+    p.ws = nullptr;
+    p.ws_bwd = sv + S.brec;
+    p.tr_h = reinterpret_cast<uint16_t*>(sv + S.h);
+    p.tr_vn = reinterpret_cast<uint16_t*>(sv + S.vn);
+    p.la = sv + S.la;
+    p.la_stride = kda::LA_BYTES;
+    p.tr_dh = reinterpret_cast<uint16_t*>(ws + L.dh);
+    p.tr_dvn = reinterpret_cast<uint16_t*>(ws + L.dvn);
+    p.tr_part = (b->dA_log || b->ddt_bias) ? reinterpret_cast<float*>(ws + L.part) : nullptr;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (kda::launch_k1_dout(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
     if (kda::launch_k2_bwd(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
     if (kda::launch_bwd_chunk(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
     if (p.tr_part && kda::launch_bwd_gate_reduce(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;

@@ -48,14 +48,16 @@ constexpr int REC_DECAY = 12800;
 constexpr int REC_U = 13312;
 constexpr int REC_SHARED = 13312;  // bytes every value tile reads
 constexpr int REC_BYTES = 17408;
-// In the backward's copy of the forward record (written by the two-record
-// stage-1 pass) qg is not needed; its bytes hold what the per-chunk
-// gradient kernel would otherwise recompute, exactly as the forward formed
-// it: the raw gram Lraw[t][s] = kp_t . km_s (fp32, [lane][i] =
-// Lraw[r][4*q4+i]) and A_inv = (I + L)^-1 (fp32, [lane][i] =
-// A_inv[r][4*q4+i]).
-constexpr int REC_LRAW = REC_QG;
-constexpr int REC_AINV = REC_QG + 1024;
+// Per record slot, what the per-chunk gradient kernel would otherwise
+// recompute, exactly as stage 1 formed it (the "gram block", 2 KiB): the
+// raw gram Lraw[t][s] = kp_t . km_s (fp32, [lane][i] = Lraw[r][4*q4+i])
+// and A_inv = (I + L)^-1 (fp32, [lane][i] = A_inv[r][4*q4+i]).  The
+// backward's recompute keeps it in the forward record's qg bytes (qg is not
+// needed there: stride REC_BYTES); a training forward that saves its state
+// keeps it in a region of its own (stride LA_BYTES).
+constexpr int LA_LRAW = 0;
+constexpr int LA_AINV = 1024;
+constexpr int LA_BYTES = 2048;
 
 // Backward record (kda_bt16_bwd_hip): what the reverse state chain feeds
 // its matrix cores, written by the backward's stage-1 pass next to the
@@ -148,6 +150,8 @@ struct Params {
     // dA_log [HV], ddt_bias [HV*128] and dh0 (state layout of h0), each
     // optional as its input is.
     uint8_t* ws_bwd;  // backward records (same slot indexing as ws)
+    uint8_t* la;      // gram blocks: slot x at la + x * la_stride
+    int64_t la_stride;
     uint16_t* tr_h;
     uint16_t* tr_vn;
     uint16_t* tr_dh;
@@ -354,6 +358,11 @@ hipError_t launch_recurrent(const Params& p, hipStream_t stream);
 // Backward (kda_bt16_bwd.hip, and the training variants of the stages).
 hipError_t launch_k1_both_records(const Params& p, hipStream_t stream);
 hipError_t launch_k2_train(const Params& p, hipStream_t stream);
+// Training forward that saves its state for the backward, and the
+// backward's completion of the saved backward records with dO.
+hipError_t launch_k1_save(const Params& p, hipStream_t stream);
+hipError_t launch_k2_train_o(const Params& p, hipStream_t stream);
+hipError_t launch_k1_dout(const Params& p, hipStream_t stream);
 hipError_t launch_k2_bwd(const Params& p, hipStream_t stream);
 hipError_t launch_bwd_chunk(const Params& p, hipStream_t stream);
 hipError_t launch_bwd_gate_reduce(const Params& p, hipStream_t stream);

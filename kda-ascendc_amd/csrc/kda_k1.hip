@@ -72,10 +72,11 @@ __device__ __forceinline__ u32x2 pack4(f32x4 v) { return pack4(v.x, v.y, v.z, v.
 // values): each wave spends most of its life waiting on its loads, and a
 // third wave per SIMD hides more of that than the two that 172 VGPRs allow.
 //
-// BOTH = true (the backward's recompute, two waves per SIMD: it holds more)
-// also writes the backward record
-// (kda_common.h) to p.ws_bwd: the same chunk quantities in the operand
-// orders of the reverse state chain, from one read of the inputs.
+// K1M (the record modes, below) other than K1_FWD also writes the backward
+// record (kda_common.h) to p.ws_bwd: the same chunk quantities in the
+// operand orders of the reverse state chain, from one read of the inputs,
+// and the gram block to p.la.  Those modes run two waves per SIMD: they
+// hold more.
 // LDS of a work-group (one wave): the transpose tile, L and the solve's
 // columns.
 __shared__ __attribute__((aligned(16))) uint16_t s_T[BT * LROW];
@@ -86,8 +87,18 @@ __shared__ float s_X[BT * (BT + 1)];
 // are tokens (every chunk but a sequence's partial last one), so the
 // row-validity selects and the rows mid = 8, last = 15 are compile-time.
 // GB16: g is bf16 (else fp32).
-template <bool BOTH, bool FULL, bool GB16>
+// Record modes.  K1_FWD: the forward record.  K1_BOTH (the backward's
+// recompute): the forward record without qg (no o is formed), the gram
+// block in qg's bytes, and the backward record with dO.  K1_SAVE (a
+// training forward that keeps its state for the backward): the forward
+// record, the gram block, and the backward record without dO, which the
+// backward adds (k1_dout_kernel) once dO exists.
+enum K1Mode { K1_FWD = 0, K1_BOTH = 1, K1_SAVE = 2 };
+
+template <int K1M, bool FULL, bool GB16>
 __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const SeqSpan& sp) {
+    constexpr bool BOTH = K1M != K1_FWD;
+    constexpr bool WITH_DO = K1M == K1_BOTH;
     const int lane = threadIdx.x;
     const int r = lane & 15;
     const int q4 = lane >> 4;
@@ -110,8 +121,8 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
     load_row(p.q + rowoff, valid, colbase, qp);
     load_row(p.k + rowoff, valid, colbase, kp);
     load_row(p.v + vrowoff, valid, colbase, vp);
-    Row32 dop;     // the backward's dO rows (BOTH)
-    if constexpr (BOTH) load_row(p.dout + vrowoff, valid, colbase, dop);
+    Row32 dop;     // the backward's dO rows (WITH_DO)
+    if constexpr (WITH_DO) load_row(p.dout + vrowoff, valid, colbase, dop);
     Row32 gp;      // g as bf16 (GB16)
     f32x4 gf[8];   // g as fp32
     if constexpr (GB16) {
@@ -267,8 +278,9 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
     const u32x2 ainv_bf = pack4(ainv);  // A = bf16(A_inv), kernels.py:170
     if constexpr (BOTH) {
         // the gram and the inverse for the per-chunk gradients (kda_common.h)
-        __builtin_nontemporal_store(acc_kk, reinterpret_cast<f32x4*>(rec + REC_LRAW + lane * 16));
-        __builtin_nontemporal_store(ainv, reinterpret_cast<f32x4*>(rec + REC_AINV + lane * 16));
+        uint8_t* la = p.la + (sp.rec0 + c) * p.la_stride;
+        __builtin_nontemporal_store(acc_kk, reinterpret_cast<f32x4*>(la + LA_LRAW + lane * 16));
+        __builtin_nontemporal_store(ainv, reinterpret_cast<f32x4*>(la + LA_AINV + lane * 16));
     }
     const i16x4 A_op = as_i16x4(ainv_bf);
     const i16x4 A_neg = as_i16x4(ainv_bf ^ 0x80008000u);
@@ -330,7 +342,7 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
         }
         // dO as the B operand of each value tile (T order, the layout of u
         // in the forward record): [vt][lane][i] = dO[4*q4 + i][16*vt + r].
-        {
+        if constexpr (WITH_DO) {
             __syncthreads();
 #pragma unroll
             for (int kt = 0; kt < 8; ++kt) lds_put(s_T, r, colbase, kt, dop.v[kt]);
@@ -419,7 +431,7 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
         qgp[kt] = pack4(qg[0], qg[1], qg[2], qg[3]);
     }
     // (the backward's recompute produces no o and never reads qg)
-    if constexpr (!BOTH) {
+    if constexpr (K1M != K1_BOTH) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const u32x4 qgj = {qgp[2 * j].x, qgp[2 * j].y, qgp[2 * j + 1].x, qgp[2 * j + 1].y};
@@ -490,53 +502,95 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
     }
 }
 
-// ALL_FULL: fixed-length batch with T a multiple of 16, so every chunk is
-// full.  Otherwise every chunk takes the general path: both variants in one
-// kernel would not fit the register budget of three waves per SIMD.
-template <bool BOTH, bool ALL_FULL, bool GB16>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(BOTH ? 2 : 3))) void k1_kernel(Params p) {
-    const int lane = threadIdx.x;
+// The (value head, chunk, sequence) of this work-group; false for a gap
+// slot (wave-uniform, before any barrier).  With cu_seqlens, slot x of
+// value head hv belongs to the sequence n with the largest
+// floor(bos_n / 16) + n <= x; slots past its last chunk are gaps.  Fixed
+// length: chunk-major, last chunk first, so the work-groups in flight
+// together read whole token rows, and the records of the first chunks,
+// which stage 2 starts with, are written last.
+__device__ __forceinline__ bool block_chunk(const Params& p, int lane, int& hv, int& c, SeqSpan& sp) {
     const int HV = p.HV;
-    int hv, c;
-    SeqSpan sp;
     if (p.cu_seqlens) {
-        // Slot x of value head hv belongs to the sequence n with the largest
-        // floor(bos_n / 16) + n <= x; slots past its last chunk are gaps.
         hv = blockIdx.x / p.NS;
         const int x = blockIdx.x - hv * p.NS;
         const int n = find_sequence(p, x, lane);
         sp = seq_span(p, n * HV + hv);
         c = (int)((int64_t)x - (sp.rec0 - (int64_t)hv * p.NS));
-        if (c < 0 || c >= sp.nt) return;  // wave-uniform: no barrier passed yet
-    } else {
-        // chunk-major, last chunk first: the work-groups in flight together
-        // read whole token rows of q/k/v/g, and the records of the first
-        // chunks, which stage 2 starts with, are written last
-        const int nbh = p.B * HV;
-        const int bh = blockIdx.x % nbh;
-        c = p.NT - 1 - (int)(blockIdx.x / nbh);
-        hv = bh - (bh / HV) * HV;
-        sp = seq_span(p, bh);
+        return c >= 0 && c < sp.nt;
     }
-    k1_chunk<BOTH, ALL_FULL, GB16>(p, hv, c, sp);
+    const int nbh = p.B * HV;
+    const int bh = blockIdx.x % nbh;
+    c = p.NT - 1 - (int)(blockIdx.x / nbh);
+    hv = bh - (bh / HV) * HV;
+    sp = seq_span(p, bh);
+    return true;
+}
+
+// ALL_FULL: fixed-length batch with T a multiple of 16, so every chunk is
+// full.  Otherwise every chunk takes the general path: both variants in one
+// kernel would not fit the register budget of three waves per SIMD.
+template <int K1M, bool ALL_FULL, bool GB16>
+__global__ __launch_bounds__(64)
+__attribute__((amdgpu_waves_per_eu(K1M != K1_FWD ? 2 : 3))) void k1_kernel(Params p) {
+    int hv, c;
+    SeqSpan sp;
+    if (!block_chunk(p, threadIdx.x, hv, c, sp)) return;
+    k1_chunk<K1M, ALL_FULL, GB16>(p, hv, c, sp);
+}
+
+// The dO operand of each backward record that a training forward saved
+// without it (K1_SAVE): [vt][lane][i] = dO[4*q4 + i][16*vt + r], rows past
+// the sequence zero, as K1_BOTH writes it.
+__global__ __launch_bounds__(64) void k1_dout_kernel(Params p) {
+    const int lane = threadIdx.x;
+    int hv, c;
+    SeqSpan sp;
+    if (!block_chunk(p, lane, hv, c, sp)) return;
+    const int r = lane & 15, q4 = lane >> 4, colbase = 4 * q4;
+    const int t0 = c * BT;
+    const bool valid = r < min(BT, sp.len - t0);
+    const int64_t tok = sp.tok0 + t0 + r;
+    Row32 dop;
+    load_row(p.dout + (tok * p.HV + hv) * DK, valid, colbase, dop);
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) lds_put(s_T, r, colbase, kt, dop.v[kt]);
+    __syncthreads();
+    i16x4 doT[8];
+    load_lds_T(s_T, r, q4, doT);
+    uint8_t* brec = p.ws_bwd + (sp.rec0 + c) * REC_BYTES;
+#pragma unroll
+    for (int vt = 0; vt < 8; ++vt)
+        __builtin_nontemporal_store(__builtin_bit_cast(u32x2, doT[vt]),
+                                    reinterpret_cast<u32x2*>(brec + BREC_DO + vt * 512 + lane * 8));
 }
 
 }  // namespace
 
 namespace {
-template <bool BOTH>
+int64_t k1_grid(const Params& p) {
+    return p.cu_seqlens ? (int64_t)p.HV * p.NS : (int64_t)p.B * p.HV * p.NT;
+}
+
+template <int K1M>
 hipError_t launch(const Params& p, hipStream_t stream) {
-    const int64_t grid = p.cu_seqlens ? (int64_t)p.HV * p.NS : (int64_t)p.B * p.HV * p.NT;
     const bool all_full = !p.cu_seqlens && p.T % BT == 0;
-    auto kern = all_full ? (p.g_bf16 ? k1_kernel<BOTH, true, true> : k1_kernel<BOTH, true, false>)
-                         : (p.g_bf16 ? k1_kernel<BOTH, false, true> : k1_kernel<BOTH, false, false>);
-    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64), 0, stream, p);
+    auto kern = all_full ? (p.g_bf16 ? k1_kernel<K1M, true, true> : k1_kernel<K1M, true, false>)
+                         : (p.g_bf16 ? k1_kernel<K1M, false, true> : k1_kernel<K1M, false, false>);
+    hipLaunchKernelGGL(kern, dim3((unsigned)k1_grid(p)), dim3(64), 0, stream, p);
     return hipGetLastError();
 }
 }  // namespace
 
-hipError_t launch_k1(const Params& p, hipStream_t stream) { return launch<false>(p, stream); }
+hipError_t launch_k1(const Params& p, hipStream_t stream) { return launch<K1_FWD>(p, stream); }
 
-hipError_t launch_k1_both_records(const Params& p, hipStream_t stream) { return launch<true>(p, stream); }
+hipError_t launch_k1_both_records(const Params& p, hipStream_t stream) { return launch<K1_BOTH>(p, stream); }
+
+hipError_t launch_k1_save(const Params& p, hipStream_t stream) { return launch<K1_SAVE>(p, stream); }
+
+hipError_t launch_k1_dout(const Params& p, hipStream_t stream) {
+    hipLaunchKernelGGL(k1_dout_kernel, dim3((unsigned)k1_grid(p)), dim3(64), 0, stream, p);
+    return hipGetLastError();
+}
 
 }  // namespace kda

@@ -350,7 +350,9 @@ __device__ __forceinline__ void state_step(const Ctx& cx, f32x4 (&St)[8], StateO
 // quad-transposed to one 8-byte row piece per lane.
 // Two store waves share that work (PART 0: k-tiles 0-3, PART 1: k-tiles
 // 4-7 and v_new); a single wave would fall behind the state wave.
-template <int S, bool TRAIN, int PART>
+// WITH_O (a training forward that saves its state): o as well, after the
+// training stores.
+template <int S, bool TRAIN, int PART, bool WITH_O = !TRAIN>
 __device__ __forceinline__ void output_step(const Ctx& cx, int c) {
     chunk_barrier();
     __builtin_amdgcn_sched_barrier(0);
@@ -373,7 +375,7 @@ __device__ __forceinline__ void output_step(const Ctx& cx, int c) {
             __builtin_nontemporal_store(
                 vt, reinterpret_cast<u32x2*>(cx.trvn + (int64_t)cs * TR_VN_ELEMS + (4 * cx.q4 + j4) * 16));
         }
-        return;
+        if constexpr (!WITH_O) return;
     }
     const uint8_t* slot = ring + S * SLOT;
     u32x4 hc[4], qg[4];
@@ -444,11 +446,11 @@ __device__ __forceinline__ void state_round_tail(const Ctx& cx, int c, f32x4 (&S
     if constexpr (N > 1) state_round_tail<(S + 1) % RING, N - 1>(cx, c + 1, St, op, vn);
 }
 
-template <int S, bool TRAIN, int PART>
+template <int S, bool TRAIN, int PART, bool WITH_O>
 __device__ __forceinline__ void output_round(const Ctx& cx, int c) {
-    output_step<S, TRAIN, PART>(cx, c);
+    output_step<S, TRAIN, PART, WITH_O>(cx, c);
     if constexpr (S + 1 < RING) {
-        if (c + 1 < cx.NT) output_round<S + 1, TRAIN, PART>(cx, c + 1);
+        if (c + 1 < cx.NT) output_round<S + 1, TRAIN, PART, WITH_O>(cx, c + 1);
     }
 }
 
@@ -478,7 +480,7 @@ __device__ __forceinline__ void copy_wave(const Params& p, Ctx& cx, const SeqSpa
     copy_barrier();  // the output wave's last chunk
 }
 
-template <bool TRAIN, int PART>
+template <bool TRAIN, int PART, bool WITH_O = !TRAIN>
 __device__ __forceinline__ void output_wave(const Params& p, Ctx& cx, const SeqSpan& sp, int hv) {
     const int x = cx.lane & 15;
     const int col = 16 * cx.vt + 4 * (x >> 2);
@@ -488,13 +490,14 @@ __device__ __forceinline__ void output_wave(const Params& p, Ctx& cx, const SeqS
         uint16_t* bv = cx.rev ? p.tr_dvn : p.tr_vn;
         cx.trh = bh + sp.rec0 * TR_H_ELEMS + cx.vt * TR_H_TILE + 4 * (x >> 2);
         cx.trvn = bv + sp.rec0 * TR_VN_ELEMS + cx.vt * TR_VN_TILE + 4 * (x >> 2);
-    } else {
+    }
+    if constexpr (WITH_O) {
         cx.obase = p.o + (sp.tok0 * p.HV + hv) * DK + col;
         cx.orow_stride = (int64_t)p.HV * DK;
     }
     chunk_barrier();
     chunk_barrier();
-    for (int c = 0; c < cx.NT; c += RING) output_round<0, TRAIN, PART>(cx, c);
+    for (int c = 0; c < cx.NT; c += RING) output_round<0, TRAIN, PART, WITH_O>(cx, c);
 }
 
 // ---------------------------------------------------------------------------
@@ -676,10 +679,21 @@ __device__ __forceinline__ void bwd_state_wave(const Params& p, const Ctx& cx, i
     read_bwd_ops(ring, lane, vt, op[0]);
     __builtin_amdgcn_s_waitcnt(WAITCNT_LGKM0);
     u32x4 bop;
-    if (cx.NT > 1) {
-        bwd_state_step<0, false, true>(cx, D, op, bop);
-    } else {
-        bwd_state_step<0, false, false>(cx, D, op, bop);
+    bwd_state_step<0, false, true>(cx, D, op, bop);
+    if (cx.NT == 1) {
+        // A single step: its own update, after the first step's code (the
+        // operands it reads for a next step come from the ring's unused slot
+        // 1 and are dropped).  The dedicated single-step instantiation of
+        // bwd_state_step gave garbage gradients for every one-chunk
+        // sequence, while this order matches the fp64 gold.
+        bwd_update<0>(D, op[0], bop);
+        bwd_update<1>(D, op[0], bop);
+        bwd_update<2>(D, op[0], bop);
+        bwd_update<3>(D, op[0], bop);
+        bwd_update<4>(D, op[0], bop);
+        bwd_update<5>(D, op[0], bop);
+        bwd_update<6>(D, op[0], bop);
+        bwd_update<7>(D, op[0], bop);
     }
     int c = 1;
     for (; c + RING < cx.NT; c += RING) bwd_round_full<1, RING>(cx, D, op, bop);
@@ -986,13 +1000,16 @@ enum Role { STATE = 0, OUTPUT = 1, COPY = 2, OUTPUT2 = 3 };
 // state-gradient chain (bwd_state_wave) over the backward records, in
 // reverse chunk order, its dh' and dv_new stored like the training buffers.
 // MODE K2_FWD_MS: the forward with several sequences per work-group
-// (above); grid seq_groups * HV * 8.
-enum K2Mode { K2_FWD = 0, K2_TRAIN = 1, K2_BWD = 2, K2_FWD_MS = 3 };
+// (above); grid seq_groups * HV * 8.  MODE K2_TRAIN_O: a training forward
+// that keeps its state for the backward: o and ht as K2_FWD (the same
+// arithmetic, so bit for bit), and h and v_new as K2_TRAIN; the first
+// store wave forms o.
+enum K2Mode { K2_FWD = 0, K2_TRAIN = 1, K2_BWD = 2, K2_FWD_MS = 3, K2_TRAIN_O = 4 };
 
 // The training modes run a fourth wave, OUTPUT2, the second store wave.
 template <int MODE>
 __global__ __launch_bounds__(MODE == K2_FWD || MODE == K2_FWD_MS ? 192 : 256) void k2_kernel(Params p) {
-    constexpr bool STORE_TR = MODE == K2_TRAIN || MODE == K2_BWD;
+    constexpr bool STORE_TR = MODE == K2_TRAIN || MODE == K2_BWD || MODE == K2_TRAIN_O;
     const int lane = threadIdx.x & 63;
     const int role = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if constexpr (MODE == K2_FWD_MS) {
@@ -1073,12 +1090,12 @@ __global__ __launch_bounds__(MODE == K2_FWD || MODE == K2_FWD_MS ? 192 : 256) vo
         __builtin_amdgcn_endpgm();
     }
     if (role == OUTPUT) {
-        output_wave<STORE_TR, 0>(p, cx, sp, hv);
+        output_wave<STORE_TR, 0, !STORE_TR || MODE == K2_TRAIN_O>(p, cx, sp, hv);
         __builtin_amdgcn_endpgm();
     }
     if constexpr (STORE_TR) {
         if (role == OUTPUT2) {
-            output_wave<STORE_TR, 1>(p, cx, sp, hv);
+            output_wave<STORE_TR, 1, false>(p, cx, sp, hv);
             __builtin_amdgcn_endpgm();
         }
     }
@@ -1124,6 +1141,12 @@ hipError_t launch_k2(const Params& p, hipStream_t stream) {
 hipError_t launch_k2_train(const Params& p, hipStream_t stream) {
     const int64_t grid = (int64_t)(p.cu_seqlens ? p.N : p.B) * p.HV * 8;
     hipLaunchKernelGGL(k2_kernel<K2_TRAIN>, dim3((unsigned)grid), dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_k2_train_o(const Params& p, hipStream_t stream) {
+    const int64_t grid = (int64_t)(p.cu_seqlens ? p.N : p.B) * p.HV * 8;
+    hipLaunchKernelGGL(k2_kernel<K2_TRAIN_O>, dim3((unsigned)grid), dim3(256), 0, stream, p);
     return hipGetLastError();
 }
 

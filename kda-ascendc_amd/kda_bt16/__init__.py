@@ -24,6 +24,7 @@ from .kernels import (
     kda_bt16_stage_launchers,
     kda_decode_step,
     kda_recurrent_fwd,
+    set_backward_recompute,
 )
 
 __all__ = [
@@ -34,6 +35,7 @@ __all__ = [
     "kda_bt16_stage_launchers",
     "kda_recurrent_fwd",
     "kda_decode_step",
+    "set_backward_recompute",
     "chunk_kda",
     "fused_recurrent_kda",
     "dispatch",

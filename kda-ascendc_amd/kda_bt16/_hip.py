@@ -35,6 +35,10 @@ EXPORTED_SYMBOLS = (
     "kda_recurrent_fwd_hip",
     "kda_bt16_bwd_workspace_bytes",
     "kda_bt16_bwd_hip",
+    "kda_bt16_saved_bytes",
+    "kda_bt16_fwd_save_hip",
+    "kda_bt16_bwd_saved_workspace_bytes",
+    "kda_bt16_bwd_saved_hip",
     "kda_bt16_strerror",
     "kda_bt16_abi_version",
 )
@@ -138,6 +142,15 @@ def lib() -> ctypes.CDLL:
         h.kda_bt16_bwd_workspace_bytes.argtypes = [ctypes.POINTER(KdaBt16Args)]
         h.kda_bt16_bwd_hip.restype = ctypes.c_int
         h.kda_bt16_bwd_hip.argtypes = [ctypes.POINTER(KdaBt16BwdArgs), ctypes.c_void_p]
+        for fn in (h.kda_bt16_saved_bytes, h.kda_bt16_bwd_saved_workspace_bytes):
+            fn.restype = ctypes.c_size_t
+            fn.argtypes = [ctypes.POINTER(KdaBt16Args)]
+        h.kda_bt16_fwd_save_hip.restype = ctypes.c_int
+        h.kda_bt16_fwd_save_hip.argtypes = [ctypes.POINTER(KdaBt16Args), ctypes.c_void_p,
+                                            ctypes.c_size_t, ctypes.c_void_p]
+        h.kda_bt16_bwd_saved_hip.restype = ctypes.c_int
+        h.kda_bt16_bwd_saved_hip.argtypes = [ctypes.POINTER(KdaBt16BwdArgs), ctypes.c_void_p,
+                                             ctypes.c_size_t, ctypes.c_void_p]
         h.kda_bt16_strerror.restype = ctypes.c_char_p
         h.kda_bt16_strerror.argtypes = [ctypes.c_int]
         h.kda_bt16_abi_version.restype = ctypes.c_int
@@ -162,6 +175,25 @@ def workspace_bytes_args(args: KdaBt16Args) -> int:
 def bwd_workspace_bytes(args: KdaBt16Args) -> int:
     """Backward workspace bytes (``kda_bt16_bwd_workspace_bytes``)."""
     return int(lib().kda_bt16_bwd_workspace_bytes(ctypes.byref(args)))
+
+
+def saved_bytes(args: KdaBt16Args) -> int:
+    """Bytes of a training forward's saved state (``kda_bt16_saved_bytes``)."""
+    return int(lib().kda_bt16_saved_bytes(ctypes.byref(args)))
+
+
+def bwd_saved_workspace_bytes(args: KdaBt16Args) -> int:
+    """Workspace bytes of the backward from saved state."""
+    return int(lib().kda_bt16_bwd_saved_workspace_bytes(ctypes.byref(args)))
+
+
+def call_saved(name: str, args, saved: int, nbytes: int, stream: int) -> None:
+    """``kda_bt16_fwd_save_hip`` / ``kda_bt16_bwd_saved_hip``: args, the
+    saved-state buffer, its size, the stream."""
+    rc = getattr(lib(), name)(ctypes.byref(args), ctypes.c_void_p(saved),
+                              ctypes.c_size_t(nbytes), ctypes.c_void_p(stream))
+    if rc != 0:
+        raise KdaHipError(name, rc, lib().kda_bt16_strerror(rc).decode())
 
 
 def call(name: str, args, stream: int) -> None:

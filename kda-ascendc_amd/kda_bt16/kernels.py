@@ -35,6 +35,7 @@ Differences from the reference, all supersets of its contract:
 from __future__ import annotations
 
 import ctypes
+import os
 
 import torch
 
@@ -44,6 +45,20 @@ from . import _hip, workspace
 # o / ht alias this cache and are overwritten by the next call with the
 # same geometry.  Not thread safe, like the reference's.
 _WORKSPACE_CACHE: dict[tuple, dict[str, torch.Tensor]] = {}
+
+# Training memory policy of the autograd node.  True (the default): the
+# forward keeps its per-chunk state (kda_bt16_fwd_save_hip, ~55 KiB per
+# 16-token chunk and value head) and the backward starts from it; False:
+# the forward keeps only its inputs and the backward recomputes the state.
+# The two give the same gradients, bit for bit.
+_SAVE_STATE = [os.environ.get("KDA_BT16_BWD_RECOMPUTE", "0") != "1"]
+
+
+def set_backward_recompute(recompute: bool) -> None:
+    """Choose the training memory policy: ``True`` recomputes the chunk
+    states in the backward (memory of the inputs only), ``False`` (the
+    default, or ``KDA_BT16_BWD_RECOMPUTE=0``) keeps them from the forward."""
+    _SAVE_STATE[0] = not recompute
 
 _RCP_LN2 = 1.4426950216
 _EPS = 1e-6
@@ -300,9 +315,14 @@ def _run(
     reuse_workspace: bool = False,
     cu_seqlens: torch.Tensor | None = None,
     g_log: bool = False,
+    save_state: bool = False,
 ):
     """Host driver, the counterpart of kernels.py:475-606: allocate outputs,
-    lease the workspace, launch stage 1 and stage 2 through the C ABI."""
+    lease the workspace, launch stage 1 and stage 2 through the C ABI.
+
+    ``save_state``: run the training forward (``kda_bt16_fwd_save_hip``)
+    and return ``(o, ht, saved)``, ``saved`` the uint8 state tensor the
+    backward starts from."""
     del use_fused  # one production path; see module docstring
     _require_gpu(q)
     q, k, v, g, initial_state, dt_bias = (
@@ -352,6 +372,11 @@ def _run(
         ws_bytes = _hip.workspace_bytes_args(args)
         ws = workspace.lease(dev, stream, ws_bytes)
         args.workspace, args.workspace_bytes = ws.data_ptr(), ws_bytes
+        if save_state:
+            nbytes = _hip.saved_bytes(args)
+            saved = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+            _hip.call_saved("kda_bt16_fwd_save_hip", args, saved.data_ptr(), nbytes, stream)
+            return o, ht, saved
         _hip.call("kda_bt16_fwd_hip", args, stream)
 
     if return_intermediates:
@@ -364,10 +389,11 @@ def _bwd_run(
     dht: torch.Tensor | None,
     q, k, v, g, beta, scale, initial_state, use_qk_l2norm_in_kernel, use_gate_in_kernel,
     use_beta_sigmoid_in_kernel, lower_bound, A_log, dt_bias, state_v_first, cu_seqlens, g_log,
-    need_gate_grads: bool = True, need_dh0: bool = True,
+    need_gate_grads: bool = True, need_dh0: bool = True, saved: torch.Tensor | None = None,
 ):
     """Host driver of the backward: allocate the gradients, lease the
-    workspace, launch ``kda_bt16_bwd_hip`` on the current stream.
+    workspace, launch ``kda_bt16_bwd_hip`` on the current stream (or
+    ``kda_bt16_bwd_saved_hip`` from a training forward's ``saved`` state).
 
     Returns ``(dq, dk, dv, dg, dbeta, dA_log, ddt_bias, dh0)``; dA_log /
     ddt_bias are None without the in-kernel gate (or dt_bias), dh0 is None
@@ -397,7 +423,8 @@ def _bwd_run(
                    state_v_first, g_log),
             None, cu_seqlens,
         )
-        ws_bytes = _hip.bwd_workspace_bytes(fa)
+        ws_bytes = (_hip.bwd_workspace_bytes(fa) if saved is None
+                    else _hip.bwd_saved_workspace_bytes(fa))
         ws = workspace.lease(dev, stream, ws_bytes)
         ba = _hip.KdaBt16BwdArgs()
         ba.fwd = ctypes.pointer(fa)
@@ -409,23 +436,32 @@ def _bwd_run(
         ba.ddt_bias = _ptr(ddt_bias)
         ba.dh0 = _ptr(dh0)
         ba.workspace, ba.workspace_bytes = ws.data_ptr(), ws_bytes
-        _hip.call("kda_bt16_bwd_hip", ba, stream)
+        if saved is None:
+            _hip.call("kda_bt16_bwd_hip", ba, stream)
+        else:
+            _hip.call_saved("kda_bt16_bwd_saved_hip", ba, saved.data_ptr(), saved.numel(), stream)
     return dq, dk, dv, dg, dbeta, dA_log, ddt_bias, dh0
 
 
 class _KdaBt16Fn(torch.autograd.Function):
-    """Autograd node of the chunked forward: the forward is :func:`_run`;
-    the backward recomputes the chunk states and runs the backward kernels
-    (``csrc/kda_bwd.hip``) through ``kda_bt16_bwd_hip``."""
+    """Autograd node of the chunked forward.  By default the forward is the
+    training forward (``kda_bt16_fwd_save_hip``: the same o and ht, plus
+    the per-chunk state) and the backward starts from that state
+    (``kda_bt16_bwd_saved_hip``).  With :func:`set_backward_recompute` the
+    forward is :func:`_run` and the backward recomputes the chunk states
+    (``kda_bt16_bwd_hip``)."""
 
     @staticmethod
     def forward(ctx, q, k, v, g, beta, A_log, dt_bias, initial_state, cu_seqlens, cfg):
         (scale, output_final_state, l2, use_gate, bsig, lower_bound, svf, g_log, reuse) = cfg
-        o, ht = _run(
+        save = _SAVE_STATE[0]
+        res = _run(
             q, k, v, g, beta, scale, initial_state, output_final_state, l2, use_gate, bsig,
             lower_bound, A_log, dt_bias, svf, return_intermediates=False,
-            reuse_workspace=reuse, cu_seqlens=cu_seqlens, g_log=g_log,
+            reuse_workspace=reuse, cu_seqlens=cu_seqlens, g_log=g_log, save_state=save,
         )
+        o, ht = res[0], res[1]
+        ctx.state = res[2] if save else None
         ctx.save_for_backward(q, k, v, g, beta, A_log, dt_bias, initial_state, cu_seqlens)
         ctx.cfg = cfg
         return o, ht
@@ -440,6 +476,7 @@ class _KdaBt16Fn(torch.autograd.Function):
         dq, dk, dv, dg, dbeta, dA_log, ddt_bias, dh0 = _bwd_run(
             do, dht, q, k, v, g, beta, scale, h0, l2, use_gate, bsig, lower_bound, A_log,
             dt_bias, svf, cu, g_log, need_gate_grads=need[5] or need[6], need_dh0=need[7],
+            saved=ctx.state,
         )
         return (dq, dk, dv, dg, dbeta, dA_log if need[5] else None,
                 ddt_bias if need[6] else None, dh0 if need[7] else None, None, None)

@@ -184,6 +184,23 @@ def test_bwd_varlen_equals_per_sequence(gpu_device, cu_dtype):
     assert _rel(packed["ddt_bias"], ddt) < 1e-5
 
 
+@pytest.mark.parametrize("T", [16, 5])
+def test_bwd_single_chunk(gpu_device, T):
+    """Sequences of one chunk (a full one and a partial one), with and
+    without h0 and dht, against the fp64 gold: the reverse chain then runs a
+    single step, which is both its first and its last."""
+    for h0, dht in ((True, True), (False, False), (True, False)):
+        x = _inputs(1, T, 1, 1, seed=5, h0=h0, dht=dht)
+        out = _hip_bwd(x, gpu_device)
+        gold = autograd_grads(x["q"], x["k"], x["v"], x["g"].float(), x["beta"].float(),
+                              x["do"].float(), 0.1, A_log=x["A_log"], dt_bias=x["dt_bias"],
+                              initial_state=x["h0"], dht=x["dht"])
+        for n in ("dq", "dk", "dv", "dg", "dbeta", "dh0"):
+            if gold.get(n) is None or out.get(n) is None:
+                continue
+            assert _rel(out[n], gold[n]) < 1e-2, (T, h0, dht, n)
+
+
 def test_autograd_matches_explicit_backward(gpu_device):
     """kda_bt16_fwd and chunk_kda record an autograd node whose backward is
     kda_bt16_bwd: the same bits."""
