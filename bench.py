@@ -255,9 +255,11 @@ def bwd_matmul_flops():
 
 def run_train(args, dev, inputs_cpu) -> dict:
     """One training step of the op: kda_bt16_fwd with inputs that require
-    grad, then the backward through autograd (kda_bt16_bwd: the recompute,
-    the state-gradient chain, the per-chunk gradients)."""
-    from kda_bt16 import kda_bt16_bwd
+    grad (the training forward, which keeps the per-chunk state), then the
+    backward through autograd (from that state: the state-gradient chain,
+    the per-chunk gradients).  The step with the recompute policy
+    (set_backward_recompute) is timed beside it."""
+    from kda_bt16 import set_backward_recompute
 
     ins = [x.to(dev) for x in inputs_cpu]
     leaves = [t.detach().clone().requires_grad_(True) for t in ins]
@@ -280,12 +282,26 @@ def run_train(args, dev, inputs_cpu) -> dict:
         step()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    q, k, v, g, beta, A_log, dt_bias = ins
     reps = max(args.steps, 10)
-    bwd_ms = time_events(lambda: kda_bt16_bwd(do, q, k, v, g, beta, A_log=A_log,
-                                              dt_bias=dt_bias, **flags), reps)
-    fwd_ms = time_events(lambda: kda_bt16_fwd(q, k, v, g, beta, A_log=A_log, dt_bias=dt_bias,
-                                              **flags), reps)
+    # the two halves, with HIP events: the training forward, and the
+    # backward over one saved state (torch.autograd.grad: no accumulation)
+    fwd = lambda: kda_bt16_fwd(*leaves[:5], A_log=leaves[5], dt_bias=leaves[6], **flags)
+    fwd_ms = time_events(fwd, reps)
+    o, _ = fwd()
+    bwd_ms = time_events(lambda: torch.autograd.grad(o, leaves, do, retain_graph=True), reps)
+    del o
+    try:
+        set_backward_recompute(True)
+        for _ in range(3):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            step()
+        torch.cuda.synchronize()
+        recompute_ms = (time.perf_counter() - t0) * 1e3 / reps
+    finally:
+        set_backward_recompute(False)
     by = bwd_algorithmic_bytes()
     fl = bwd_matmul_flops()
     achieved = by / bwd_ms / 1e6
@@ -300,7 +316,9 @@ def run_train(args, dev, inputs_cpu) -> dict:
         "config": {"workload": f"kda_bt16_fwd + autograd backward B={B} T={T} H={H} K=V={D}, "
                                "zero h0, all in-kernel flags, dO ~N(0,1)",
                    "global_batch": B, "seq_len": T, "heads": H, "parallelism": "none (1 GPU)"},
-        "roofline": {"bound": "hbm", "kernel": "backward (kda_bt16_bwd_hip, 5 launches)",
+        "recompute_ms_per_step": round(recompute_ms, 4),
+        "roofline": {"bound": "hbm",
+                     "kernel": "backward from the saved state (kda_bt16_bwd_saved_hip, 4 launches)",
                      "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None,
                      "bwd_ms": round(bwd_ms, 4), "fwd_ms": round(fwd_ms, 4),
