@@ -85,6 +85,7 @@ def matmul_flops(n_chunks: int | None = None):
 
 
 TRAFFIC_FILE = ROOT / "profiles" / "kda_fwd_B1_T8192_H32_traffic.json"
+TRAIN_TRAFFIC_FILE = ROOT / "profiles" / "kda_train_B1_T8192_H32_traffic.json"
 
 
 def measured_traffic():
@@ -305,6 +306,14 @@ def run_train(args, dev, inputs_cpu) -> dict:
     by = bwd_algorithmic_bytes()
     fl = bwd_matmul_flops()
     achieved = by / bwd_ms / 1e6
+    # HBM bytes of one saved-state backward (its four launches), from the
+    # FETCH_SIZE / WRITE_SIZE runs scaled by the copy calibration
+    traffic = None
+    if TRAIN_TRAFFIC_FILE.exists():
+        t = json.loads(TRAIN_TRAFFIC_FILE.read_text())
+        traffic = round(sum((t["kernels"][n]["FETCH_SIZE_KiB"] * t["fetch_scale"]
+                             + t["kernels"][n]["WRITE_SIZE_KiB"] * t["write_scale"]) * 1024
+                            for n in t["backward_kernels"]))
     return {
         "metric": "KDA training step (fwd + bwd) tokens/sec at B=1 T=8192 H=32 bf16",
         "value": round(B * T / (wall_ms / 1e3), 1),
@@ -320,7 +329,7 @@ def run_train(args, dev, inputs_cpu) -> dict:
         "roofline": {"bound": "hbm",
                      "kernel": "backward from the saved state (kda_bt16_bwd_saved_hip, 4 launches)",
                      "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic,
                      "bwd_ms": round(bwd_ms, 4), "fwd_ms": round(fwd_ms, 4),
                      "bwd_alg_bytes": by, "bwd_matmul_flops": fl,
                      "bwd_tflops": round(fl / bwd_ms / 1e9, 2),
