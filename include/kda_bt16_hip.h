@@ -90,6 +90,13 @@ extern "C" {
 #define KDA_BT16_ELAUNCH           -4 /* HIP launch error */
 #define KDA_BT16_EABI              -5 /* args->abi_version != KDA_BT16_ABI_VERSION */
 #define KDA_BT16_ERANGE            -6 /* lower_bound outside (-11, 0) with USE_GATE (kernels.py:733-744) */
+#define KDA_BT16_ESCRATCH          -7 /* kda_bt16_fwd_noalloc_hip: the geometry needs more than
+                                         KDA_BT16_NOALLOC_MAX_WORKSPACE bytes of records */
+
+/* Size of the static device scratch of kda_bt16_fwd_noalloc_hip (96 MiB:
+ * 5782 records of 17 KiB, e.g. B=2 T=4096 H=8, or 92.5k tokens of one
+ * value head). */
+#define KDA_BT16_NOALLOC_MAX_WORKSPACE ((size_t)96 << 20)
 
 typedef struct KdaBt16Args {
     int32_t abi_version; /* KDA_BT16_ABI_VERSION */
@@ -135,6 +142,22 @@ size_t kda_bt16_workspace_bytes_args(const KdaBt16Args* args);
 /* Full forward: stage 1 then stage 2 on `stream` (a hipStream_t; NULL is the
  * legacy default stream).  Replaces _run's two launches, kernels.py:581-602. */
 int kda_bt16_fwd_hip(const KdaBt16Args* args, void* stream);
+
+/* Full forward that allocates nothing and takes no workspace.  No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The same kernels as kda_bt16_fwd_hip,
+ * with the same results bit for bit; the records stage 1 hands to stage 2
+ * live in a file-scope device array of KDA_BT16_NOALLOC_MAX_WORKSPACE bytes
+ * that the library holds on every GPU it runs on until the process ends.
+ * args->workspace and args->workspace_bytes are ignored.  Returns
+ * KDA_BT16_ESCRATCH (before any HIP call) when kda_bt16_workspace_bytes_args
+ * exceeds that size.  Every call on one GPU uses that GPU's one array:
+ * calls that overlap on one GPU (two streams, two threads) race and give
+ * wrong results; calls in order on one stream are safe.  The array keeps
+ * the last call's contents; no part of it needs clearing (stage 1 writes
+ * every record stage 2 reads). */
+int kda_bt16_fwd_noalloc_hip(const KdaBt16Args* args, void* stream);
 
 /* Stage 1 only: per-chunk gates, grams, (I+L)^-1 solve and W/U into the
  * workspace, plus the debug outputs when given.  Replaces the

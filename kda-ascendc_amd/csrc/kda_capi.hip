@@ -6,6 +6,8 @@
 #include "../../include/kda_bt16_hip.h"
 #include "kda_common.h"
 
+#include <mutex>
+
 namespace {
 
 using kda::Params;
@@ -80,8 +82,8 @@ int check_common(const KdaBt16Args* a, Params& p) {
     return KDA_BT16_OK;
 }
 
-// The chunked entries (stage 1, stage 2, both).
-int to_params(const KdaBt16Args* a, Params& p, bool need_inputs, bool need_outputs) {
+// The chunked entries (stage 1, stage 2, both), all but the workspace.
+int to_params_core(const KdaBt16Args* a, Params& p, bool need_inputs, bool need_outputs) {
     int rc = check_common(a, p);
     if (rc != KDA_BT16_OK) return rc;
     if (a->flags & KDA_BT16_O_FP32) return KDA_BT16_EUNSUPPORTED;
@@ -110,15 +112,51 @@ int to_params(const KdaBt16Args* a, Params& p, bool need_inputs, bool need_outpu
         misaligned(a->dbg_Aqk, 8) || misaligned(a->dbg_A_inv, 8) || misaligned(a->dbg_w, 16) ||
         misaligned(a->dbg_u, 16) || misaligned(a->dbg_g, 16))
         return KDA_BT16_EINVAL;
-    const size_t need = kda_bt16_workspace_bytes_args(a);
-    if (!a->workspace || a->workspace_bytes < need) return KDA_BT16_EWORKSPACE;
-    if ((reinterpret_cast<uintptr_t>(a->workspace) & 255u) != 0) return KDA_BT16_EWORKSPACE;
-    p.ws = static_cast<uint8_t*>(a->workspace);
     p.dbg_Aqk = static_cast<uint16_t*>(a->dbg_Aqk);
     p.dbg_A_inv = static_cast<uint16_t*>(a->dbg_A_inv);
     p.dbg_w = static_cast<uint16_t*>(a->dbg_w);
     p.dbg_u = static_cast<uint16_t*>(a->dbg_u);
     p.dbg_g = a->dbg_g;
+    return KDA_BT16_OK;
+}
+
+// The chunked entries with the caller's workspace.
+int to_params(const KdaBt16Args* a, Params& p, bool need_inputs, bool need_outputs) {
+    int rc = to_params_core(a, p, need_inputs, need_outputs);
+    if (rc != KDA_BT16_OK) return rc;
+    const size_t need = kda_bt16_workspace_bytes_args(a);
+    if (!a->workspace || a->workspace_bytes < need) return KDA_BT16_EWORKSPACE;
+    if ((reinterpret_cast<uintptr_t>(a->workspace) & 255u) != 0) return KDA_BT16_EWORKSPACE;
+    p.ws = static_cast<uint8_t*>(a->workspace);
+    return KDA_BT16_OK;
+}
+
+// Scratch of kda_bt16_fwd_noalloc_hip: the records stage 1 hands to stage
+// 2, in a file-scope device array instead of a caller's workspace.  In host
+// code `scratch` names a host-side stand-in, never the device memory: the
+// device address comes from hipGetSymbolAddress, once per device (each GPU
+// holds its own copy of the array), and only that address is passed on.
+__device__ __align__(256) static uint8_t scratch[KDA_BT16_NOALLOC_MAX_WORKSPACE];
+
+constexpr int MAX_DEVICES = 64;
+std::mutex scratch_mu;
+uint8_t* scratch_dev[MAX_DEVICES] = {};
+
+// The current device's address of `scratch` (looked up on the first call
+// on that device, with that device current).
+int scratch_ptr(uint8_t** out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess) return KDA_BT16_ELAUNCH;
+    if (dev < 0 || dev >= MAX_DEVICES) return KDA_BT16_EUNSUPPORTED;
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (scratch_dev[dev] == nullptr) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr)
+            return KDA_BT16_ELAUNCH;
+        if ((reinterpret_cast<uintptr_t>(ptr) & 255u) != 0) return KDA_BT16_ELAUNCH;
+        scratch_dev[dev] = static_cast<uint8_t*>(ptr);
+    }
+    *out = scratch_dev[dev];
     return KDA_BT16_OK;
 }
 
@@ -303,6 +341,20 @@ int kda_bt16_fwd_hip(const KdaBt16Args* args, void* stream) {
     return KDA_BT16_OK;
 }
 
+int kda_bt16_fwd_noalloc_hip(const KdaBt16Args* args, void* stream) {
+    Params p;
+    int rc = to_params_core(args, p, true, true);
+    if (rc != KDA_BT16_OK) return rc;
+    if (kda_bt16_workspace_bytes_args(args) > KDA_BT16_NOALLOC_MAX_WORKSPACE)
+        return KDA_BT16_ESCRATCH;
+    rc = scratch_ptr(&p.ws);
+    if (rc != KDA_BT16_OK) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (kda::launch_k1(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
+    if (kda::launch_k2(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
+    return KDA_BT16_OK;
+}
+
 int kda_recurrent_fwd_hip(const KdaBt16Args* args, void* stream) {
     Params p;
     int rc = to_params_recurrent(args, p);
@@ -413,6 +465,10 @@ const char* kda_bt16_strerror(int code) {
         case KDA_BT16_ELAUNCH: return "HIP kernel launch failed";
         case KDA_BT16_EABI: return "abi_version mismatch";
         case KDA_BT16_ERANGE: return "lower_bound must be in (-11, 0) with the in-kernel gate";
+        case KDA_BT16_ESCRATCH:
+            return "kda_bt16_fwd_noalloc_hip: the geometry needs more records than its static "
+                   "scratch holds (kda_bt16_workspace_bytes_args() > KDA_BT16_NOALLOC_MAX_WORKSPACE, "
+                   "96 MiB); use kda_bt16_fwd_hip with a workspace";
         default: return "unknown error";
     }
 }

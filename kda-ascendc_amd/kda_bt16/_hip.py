@@ -21,6 +21,11 @@ STATE_V_FIRST = 1 << 3
 O_FP32 = 1 << 4  # token recurrence only
 G_LOG_DECAY = 1 << 5  # without USE_GATE: g is the per-token natural-log decay
 
+# Bytes of the static scratch of kda_bt16_fwd_noalloc_hip, and the code it
+# returns for a geometry whose records do not fit.
+NOALLOC_MAX_WORKSPACE = 96 << 20
+ESCRATCH = -7
+
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 DTYPE_I32 = 2
@@ -30,6 +35,7 @@ EXPORTED_SYMBOLS = (
     "kda_bt16_workspace_bytes",
     "kda_bt16_workspace_bytes_args",
     "kda_bt16_fwd_hip",
+    "kda_bt16_fwd_noalloc_hip",
     "kda_bt16_k1_hip",
     "kda_bt16_k2_hip",
     "kda_recurrent_fwd_hip",
@@ -133,8 +139,8 @@ def lib() -> ctypes.CDLL:
         h.kda_bt16_workspace_bytes.argtypes = [ctypes.c_int32] * 5
         h.kda_bt16_workspace_bytes_args.restype = ctypes.c_size_t
         h.kda_bt16_workspace_bytes_args.argtypes = [ctypes.POINTER(KdaBt16Args)]
-        for name in ("kda_bt16_fwd_hip", "kda_bt16_k1_hip", "kda_bt16_k2_hip",
-                     "kda_recurrent_fwd_hip"):
+        for name in ("kda_bt16_fwd_hip", "kda_bt16_fwd_noalloc_hip", "kda_bt16_k1_hip",
+                     "kda_bt16_k2_hip", "kda_recurrent_fwd_hip"):
             fn = getattr(h, name)
             fn.restype = ctypes.c_int
             fn.argtypes = [ctypes.POINTER(KdaBt16Args), ctypes.c_void_p]

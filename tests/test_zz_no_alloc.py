@@ -1,0 +1,107 @@
+"""kda_bt16_fwd_noalloc_hip: the forward whose records live in the library's
+static device scratch instead of a workspace.  It must give what
+kda_bt16_fwd_hip gives, bit for bit, on consecutive calls that leave the
+scratch holding the previous call's records (each call here is smaller than
+the one before), and refuse a geometry that does not fit before any launch.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import pytest
+import torch
+
+from kda_bt16 import _hip, kda_bt16_fwd
+from kda_bt16.kernels import _flags, _make_args
+
+
+def _args(**kw):
+    a = _hip.KdaBt16Args()
+    a.abi_version = _hip.ABI_VERSION
+    a.B, a.T, a.H, a.HV, a.K, a.V = 1, 16, 1, 1, 128, 128
+    a.scale = 0.1
+    a.lower_bound = -5.0
+    for name, val in kw.items():
+        setattr(a, name, val)
+    return a
+
+
+def test_noalloc_refuses_oversized_geometry_without_launching():
+    fake = 1 << 40  # never dereferenced: the size check fails before any HIP call
+    full = dict(q=fake, k=fake, v=fake, g=fake, beta=fake, o=fake)
+    f = _hip.lib().kda_bt16_fwd_noalloc_hip
+    # B=1 T=8192 HV=32 needs 272 MiB of records
+    a = _args(B=1, T=8192, H=32, HV=32, **full)
+    assert _hip.workspace_bytes_args(a) > _hip.NOALLOC_MAX_WORKSPACE
+    assert f(ctypes.byref(a), None) == _hip.ESCRATCH
+    assert b"static" in _hip.lib().kda_bt16_strerror(_hip.ESCRATCH)
+    # the ordinary argument checks come first
+    assert f(None, None) == -1
+    assert f(ctypes.byref(_args(K=64, **full)), None) == -2
+    assert f(ctypes.byref(_args()), None) == -1  # missing tensors
+
+
+def _case(B, T, H, HV, seed, *, h0, svf, varlen=None):
+    """q/k [B, T, H], the rest [B, T, HV] (the BASELINE generators); states
+    for B rows, or for the sequences of ``varlen``."""
+    gen = torch.Generator().manual_seed(seed)
+    S = B if varlen is None else len(varlen) - 1
+    c = dict(
+        q=torch.randn(B, T, H, 128, generator=gen).bfloat16(),
+        k=torch.randn(B, T, H, 128, generator=gen).bfloat16(),
+        v=torch.randn(B, T, HV, 128, generator=gen).bfloat16(),
+        g=torch.randn(B, T, HV, 128, generator=gen).bfloat16(),
+        beta=torch.randn(B, T, HV, generator=gen).bfloat16(),
+        A_log=torch.log(torch.rand(HV, generator=gen) * 15 + 1),
+        dt_bias=torch.randn(HV * 128, generator=gen) * 0.1,
+        h0=torch.randn(S, HV, 128, 128, generator=gen) * 0.05 if h0 else None,
+    )
+    c["cu"] = None if varlen is None else torch.tensor(varlen, dtype=torch.int32)
+    c["svf"] = svf
+    return c
+
+
+def _run_both(c, dev):
+    q, k, v, g, beta = (c[x].to(dev) for x in ("q", "k", "v", "g", "beta"))
+    A_log, dt_bias = c["A_log"].to(dev), c["dt_bias"].to(dev)
+    h0 = None if c.get("h0") is None else c["h0"].to(dev)
+    cu = None if c["cu"] is None else c["cu"].to(dev)
+    kw = dict(scale=0.1, initial_state=h0, output_final_state=True,
+              use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True,
+              use_beta_sigmoid_in_kernel=True, lower_bound=-5.0, A_log=A_log,
+              dt_bias=dt_bias, state_v_first=c["svf"], cu_seqlens=cu)
+    o_ref, ht_ref = kda_bt16_fwd(q, k, v, g, beta, **kw)
+    B, T, H, _ = q.shape
+    HV = v.shape[2]
+    S = B if cu is None else cu.numel() - 1
+    o = torch.full((B, T, HV, 128), float("nan"), dtype=torch.bfloat16, device=dev)
+    ht = torch.full((S, HV, 128, 128), float("nan"), dtype=torch.float32, device=dev)
+    args = _make_args(q, k, v, g, beta, 0.1, -5.0, A_log, dt_bias, h0, o, ht, None, 0,
+                      _flags(True, True, True, c["svf"]), None, cu)
+    assert _hip.workspace_bytes_args(args) <= _hip.NOALLOC_MAX_WORKSPACE
+    _hip.call("kda_bt16_fwd_noalloc_hip", args, torch.cuda.current_stream(dev).cuda_stream)
+    torch.cuda.synchronize(dev)
+    return (o_ref, ht_ref), (o, ht)
+
+
+@pytest.mark.gpu
+def test_noalloc_equals_fwd_on_consecutive_calls(gpu_device):
+    cases = [
+        # near the scratch's size: 4096 records (68 MiB), h0, V-first
+        ("B2_T4096_H8", _case(2, 4096, 8, 8, seed=3, h0=True, svf=True)),
+        # smaller: 8 rows x 8 value heads, so stage 2 runs several sequences
+        # per work-group
+        ("B8_T300_HV8", _case(8, 300, 2, 8, seed=6, h0=True, svf=True)),
+        # smaller, partial last chunk, K-first state
+        ("B2_T1037_H4_kfirst", _case(2, 1037, 4, 4, seed=4, h0=True, svf=False)),
+        # smaller again: grouped value heads, packed sequences with an empty one
+        ("varlen_gva", _case(1, 300, 2, 4, seed=5, h0=False, svf=True,
+                             varlen=[0, 37, 37, 160, 300])),
+    ]
+    for name, c in cases:
+        print(f"noalloc case {name}", flush=True)
+        (o_ref, ht_ref), (o, ht) = _run_both(c, gpu_device)
+        assert torch.isfinite(o_ref.float()).all(), name
+        assert torch.equal(o.view(torch.int16), o_ref.view(torch.int16)), f"{name}: o differs"
+        assert torch.equal(ht.view(torch.int32), ht_ref.view(torch.int32)), f"{name}: ht differs"
