@@ -1,18 +1,26 @@
 """Benchmark of the KDA BT=16 forward on one MI355X.
 
-Workload: BASELINE configs[2], B=1 T=8192 H=32 K=V=128, bf16 q/k/v/g/beta,
-A_log = log U(1,16), dt_bias ~N(0, 0.1), zero initial state, final state
-returned, all in-kernel flags on (lower_bound -5, scale 128^-0.5).  A step is
-one kda_bt16_fwd over that batch with inputs already resident in HBM.
+Workload (the headline): BASELINE configs[2], B=1 T=8192 H=32 K=V=128, bf16
+q/k/v/g/beta, A_log = log U(1,16), dt_bias ~N(0, 0.1), zero initial state,
+final state returned, all in-kernel flags on (lower_bound -5, scale
+128^-0.5).  A step is one kda_bt16_fwd over that batch with inputs already
+resident in HBM.
 
 Prints ONE JSON line with the throughput (tokens/s), the roofline of the
-dominant kernel measured with HIP events on the launch stream, and the CPU
-restatement of the reference chunked path timed on this host.
+forward (algorithmic bytes over its time from HIP events on the launch
+stream, with the per-kernel split, the HBM bytes and the matrix-op work
+that rocprofv3 counters measured), the precision of o and ht against the
+fp32 token recurrence, and the CPU restatement of the reference chunked
+path timed on this host.
 
   python bench.py [--gpus 1] [--steps 200] [--warmup 50] [--no-cpu-baseline]
 
 More workloads, each printing its own line in the same format (not the
 headline metric):
+  --workload config --config c0..c4
+                      any BASELINE config (c0 B=2 T=1024 H=4, c1 B=2
+                      T=4096 H=8 with h0, c2 the headline, c3 B=1 T=8192
+                      H=96, c4 B=16 T=2048 H=32 with h0 and g_raw std 2);
   --workload train    one training step of the op (forward, then the
                       backward through autograd) at the headline shape;
   --workload varlen   the same 8192 tokens and 32 heads as 16 packed
@@ -39,7 +47,8 @@ import torch
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "kda-ascendc_amd"))
 
-from kda_bt16 import kda_bt16_fwd, kda_bt16_stage_launchers, kda_decode_step  # noqa: E402
+from kda_bt16 import (  # noqa: E402
+    kda_bt16_fwd, kda_bt16_stage_launchers, kda_decode_step, kda_recurrent_fwd)
 
 METRIC = "KDA fwd tokens/sec and ms at B=1 T=8192 H=32 bf16; % HBM/MFMA roofline"
 B, T, H, D = 1, 8192, 32, 128
@@ -47,59 +56,122 @@ LOWER_BOUND = -5.0
 SCALE = D ** -0.5
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+F32_PEAK_TFLOPS = 157.3
 # Published reference latency for this shape (Ascend 910B3, README.md:53): 20.5 ms.
 REF_MS = 20.5
 
+# shape, initial state (None: not passed; "zeros": a
+# zero tensor passed; a float: ~N(0, std)) and the std of g_raw.
+CONFIGS = {
+    "c0": dict(B=2, T=1024, H=4, h0="zeros", g_std=1.0),
+    "c1": dict(B=2, T=4096, H=8, h0=0.05, g_std=1.0),
+    "c2": dict(B=1, T=8192, H=32, h0=None, g_std=1.0),
+    "c3": dict(B=1, T=8192, H=96, h0=None, g_std=1.0),
+    "c4": dict(B=16, T=2048, H=32, h0=0.05, g_std=2.0),
+}
 
-def make_inputs(seed: int = 42):
+
+def make_inputs(seed: int = 42, cfg: dict | None = None):
     """BASELINE.json generators on the CPU: seed 42, order q, k, v, g_raw,
-    beta_raw (N(0,1), stored bf16), A_log = log U(1,16), dt_bias ~N(0,0.1)."""
+    beta_raw (N(0,1), g_raw std ``g_std``, stored bf16), A_log = log U(1,16),
+    dt_bias ~N(0,0.1), then h0 ~N(0, std) when the config has one."""
+    c = CONFIGS["c2"] if cfg is None else cfg
+    b, t, h = c["B"], c["T"], c["H"]
     gen = torch.Generator().manual_seed(seed)
-    q = torch.randn(B, T, H, D, generator=gen).to(torch.bfloat16)
-    k = torch.randn(B, T, H, D, generator=gen).to(torch.bfloat16)
-    v = torch.randn(B, T, H, D, generator=gen).to(torch.bfloat16)
-    g = torch.randn(B, T, H, D, generator=gen).to(torch.bfloat16)
-    beta = torch.randn(B, T, H, generator=gen).to(torch.bfloat16)
-    A_log = torch.log(torch.rand(H, generator=gen) * 15.0 + 1.0)
-    dt_bias = torch.randn(H * D, generator=gen) * 0.1
-    return q, k, v, g, beta, A_log, dt_bias
+    q = torch.randn(b, t, h, D, generator=gen).to(torch.bfloat16)
+    k = torch.randn(b, t, h, D, generator=gen).to(torch.bfloat16)
+    v = torch.randn(b, t, h, D, generator=gen).to(torch.bfloat16)
+    g = (torch.randn(b, t, h, D, generator=gen) * c["g_std"]).to(torch.bfloat16)
+    beta = torch.randn(b, t, h, generator=gen).to(torch.bfloat16)
+    A_log = torch.log(torch.rand(h, generator=gen) * 15.0 + 1.0)
+    dt_bias = torch.randn(h * D, generator=gen) * 0.1
+    if cfg is None:
+        return q, k, v, g, beta, A_log, dt_bias
+    h0 = None
+    if c["h0"] == "zeros":
+        h0 = torch.zeros(b, h, D, D)
+    elif c["h0"] is not None:
+        h0 = torch.randn(b, h, D, D, generator=gen) * c["h0"]
+    return q, k, v, g, beta, A_log, dt_bias, h0
 
 
-def algorithmic_bytes(n_states: int = B):
+def algorithmic_bytes(n_states: int = B, b: int = B, t: int = T, h: int = H, h0: bool = False):
     """Algorithmic HBM bytes of one forward, split by the kernel that moves
     them: stage 1 reads q, k, v (2 B), g (2 B), beta (2 B) per token-head
-    element plus A_log/dt_bias; stage 2 writes o (2 B) and the fp32 final
-    state of each of ``n_states`` sequences.  Total = 1282 B per token-head
-    + states."""
-    nth = B * T * H
-    k1 = nth * (3 * D * 2 + D * 2 + 2) + H * (4 + 4 * D)
-    k2 = nth * D * 2 + n_states * H * D * D * 4
+    element plus A_log/dt_bias; stage 2 reads the fp32 initial state (when
+    one is passed) and writes o (2 B) and the fp32 final state of each of
+    ``n_states`` sequences.  Total = 1282 B per token-head + states."""
+    nth = b * t * h
+    k1 = nth * (3 * D * 2 + D * 2 + 2) + h * (4 + 4 * D)
+    k2 = nth * D * 2 + n_states * h * D * D * 4 * (1 + int(h0))
     return k1, k2
 
 
-def matmul_flops(n_chunks: int | None = None):
-    nch = B * H * math.ceil(T / 16) if n_chunks is None else H * n_chunks
+def matmul_flops(n_chunks: int | None = None, b: int = B, t: int = T, h: int = H):
+    """Matrix-op FLOPs of one forward per kernel: stage 1 the two fp32 grams
+    and the two bf16 products of w and u; stage 2 w @ hc^T, qg @ hc^T,
+    kg^T @ v_new and Aqk @ v_new."""
+    nch = b * h * math.ceil(t / 16) if n_chunks is None else h * n_chunks
     k1 = nch * 4 * (2 * 16 * 16 * D)
     k2 = nch * (3 * (2 * 16 * D * D) + 2 * 16 * 16 * D)
     return k1, k2
 
 
-TRAFFIC_FILE = ROOT / "profiles" / "kda_fwd_B1_T8192_H32_traffic.json"
 TRAIN_TRAFFIC_FILE = ROOT / "profiles" / "kda_train_B1_T8192_H32_traffic.json"
 
 
-def measured_traffic():
+def _profile(kind: str, b: int, t: int, h: int):
+    """A committed rocprofv3 summary (profiles/kda_fwd_B{b}_T{t}_H{h}_{kind}.json),
+    or None."""
+    try:
+        return json.loads((ROOT / "profiles" / f"kda_fwd_B{b}_T{t}_H{h}_{kind}.json").read_text())
+    except (OSError, ValueError):
+        return None
+
+
+def measured_traffic(b: int = B, t: int = T, h: int = H):
     """HBM bytes per launch of each kernel from the committed rocprofv3 PMC
     summary (FETCH_SIZE x fetch scale + WRITE_SIZE x write scale, KiB), or
     None when no summary is present."""
-    try:
-        d = json.loads(TRAFFIC_FILE.read_text())
-    except (OSError, ValueError):
+    d = _profile("traffic", b, t, h)
+    if d is None:
         return None
     out = {}
     for name, kb in d.get("kernels", {}).items():
         out[name] = int(round((kb["FETCH_SIZE_KiB"] * d["fetch_scale"]
                                + kb["WRITE_SIZE_KiB"] * d["write_scale"]) * 1024))
+    return out
+
+
+def measured_mfma(kern: dict, b: int = B, t: int = T, h: int = H):
+    """Matrix-op work of each kernel from the committed rocprofv3 counter
+    summary: SQ_INSTS_VALU_MFMA_MOPS_BF16 / _F32 count 512 FLOPs each, so
+    FLOPs per launch = MOPS x 512; divided by the kernel's time measured
+    here, that is the achieved rate and its fraction of the dense peak.
+    SQ_VALU_MFMA_BUSY_CYCLES (summed over every SIMD) over the kernel's cycles
+    times the SIMD count (GRBM_GUI_ACTIVE, summed over the XCDs, / XCDs x
+    CUs x 4) is the fraction of the matrix pipes' time they were busy.  None
+    when no summary is present."""
+    d = _profile("mfma", b, t, h)
+    if d is None:
+        return None
+    out = {}
+    for name, c in d.get("kernels", {}).items():
+        if name not in kern:
+            continue
+        ms = kern[name]["ms"]
+        bf = c["SQ_INSTS_VALU_MFMA_MOPS_BF16"] * 512
+        f32 = c["SQ_INSTS_VALU_MFMA_MOPS_F32"] * 512
+        out[name] = {
+            "bf16_flops": int(bf), "f32_flops": int(f32),
+            "bf16_tflops": round(bf / ms / 1e9, 2),
+            "bf16_frac": round(bf / ms / 1e9 / BF16_PEAK_TFLOPS, 5),
+            "f32_tflops": round(f32 / ms / 1e9, 2),
+            "f32_frac": round(f32 / ms / 1e9 / F32_PEAK_TFLOPS, 5),
+            "mfma_busy_frac": round(c["SQ_VALU_MFMA_BUSY_CYCLES"]
+                                    / (c["GRBM_GUI_ACTIVE"] / d["xcds"] * d["cus"]
+                                       * d["simds_per_cu"]), 5),
+        }
     return out
 
 
@@ -194,25 +266,30 @@ def run_varlen(args, dev, inputs_cpu) -> dict:
     def step():
         return kda_bt16_fwd(q, k, v, g, beta, cu_seqlens=cu, **kw)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
     k1, k2, _, _ = kda_bt16_stage_launchers(q, k, v, g, beta, output_final_state=True,
                                             A_log=A_log, dt_bias=dt_bias,
                                             lower_bound=LOWER_BOUND, cu_seqlens=cu)
     k1(); k2()
     reps = max(args.steps, 10)
     k1_ms, k2_ms = time_events(k1, reps), time_events(k2, reps)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(args.steps):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    fwd_ms = ev0.elapsed_time(ev1) / args.steps
     lens = [b - a for a, b in zip(offs[:-1], offs[1:])]
     n_chunks = sum(math.ceil(n / 16) for n in lens)
     by = algorithmic_bytes(VARLEN_N)
     kern, dom = _kernel_roofline(k1_ms, k2_ms, wall_ms, by, matmul_flops(n_chunks))
-    achieved = kern[dom]["alg_gbs"]
+    achieved = sum(by) / fwd_ms / 1e6
     return {
         "metric": "KDA varlen fwd tokens/sec, 8192 tokens in 16 packed sequences, H=32 bf16",
         "value": round(T / (wall_ms / 1e3), 1),
@@ -224,9 +301,12 @@ def run_varlen(args, dev, inputs_cpu) -> dict:
         "config": {"workload": f"kda_bt16_fwd cu_seqlens, {VARLEN_N} sequences over T={T}, "
                                f"H={H}, lengths {lens}", "seq_len": T, "heads": H,
                    "parallelism": "none (1 GPU)"},
-        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 2),
+        "roofline": {"bound": "hbm", "kernel": "forward: stage 1 + stage 2",
+                     "achieved": round(achieved, 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None,
+                     "alg_bytes": sum(by), "forward_ms_events": round(fwd_ms, 5),
+                     "slowest_kernel": dom,
                      "kernels": {n: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
                                      for kk, vv in d.items()} for n, d in kern.items()}},
     }
@@ -392,6 +472,148 @@ def run_decode(args, dev) -> dict:
     }
 
 
+def precision_vs_recurrence(fwd_out, ins, kw) -> dict:
+    """Max-abs error of o and ht against the token recurrence in fp32 on the
+    GPU (kda_recurrent_fwd with an fp32 o: no rounding between tokens, the
+    role of the reference tests' fused_recurrent_kda gold,
+    tests/test_kda_bt16.py:26-38).  The tests check that recurrence against
+    the CPU gold; the bar they apply at this shape is 1.5x the reference
+    chunked path's own error (about 1.05e-3 for o and 6.1e-3 for ht at B=1
+    T=8192 H=32)."""
+    o, ht = fwd_out
+    o_g, ht_g = kda_recurrent_fwd(*ins, output_dtype=torch.float32, **kw)
+    return {
+        "gold": "kda_recurrent_fwd, fp32 state and o, same inputs",
+        "o_maxabs": float((o.float() - o_g).abs().max()),
+        "ht_maxabs": float((ht - ht_g).abs().max()),
+        "o_rel_rms": float((o.float() - o_g).pow(2).mean().sqrt() / o_g.pow(2).mean().sqrt()),
+        "ht_rel_rms": float((ht - ht_g).pow(2).mean().sqrt() / ht_g.pow(2).mean().sqrt()),
+    }
+
+
+def run_forward(args, dev, name: str, *, cpu: bool, inputs_cpu=None) -> dict:
+    """One BASELINE config: precision against the fp32 recurrence, the two
+    stages timed with HIP events, then ``warmup`` forwards and exactly
+    ``steps`` timed forwards (synchronized on both sides; HIP events on the
+    launch stream bracket the same region)."""
+    c = CONFIGS[name]
+    b, t, h = c["B"], c["T"], c["H"]
+    ins_cpu = make_inputs(cfg=c)
+    q, k, v, g, beta, A_log, dt_bias, h0 = (None if x is None else x.to(dev) for x in ins_cpu)
+    flags = dict(scale=SCALE, use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True,
+                 use_beta_sigmoid_in_kernel=True, lower_bound=LOWER_BOUND, A_log=A_log,
+                 dt_bias=dt_bias)
+    kw = dict(initial_state=h0, output_final_state=True, **flags)
+
+    def step():
+        return kda_bt16_fwd(q, k, v, g, beta, **kw)
+
+    # Untimed measurements first: precision, then each stage on its own.
+    precision = precision_vs_recurrence(step(), (q, k, v, g, beta), kw)
+    k1, k2, _, _ = kda_bt16_stage_launchers(q, k, v, g, beta, initial_state=h0,
+                                            output_final_state=True, A_log=A_log,
+                                            dt_bias=dt_bias, lower_bound=LOWER_BOUND)
+    k1(); k2()
+    reps = max(args.steps, 10)
+    k1_ms = time_events(k1, reps)
+    k2_ms = time_events(k2, reps)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    # timed region: synchronize on both sides, exactly `steps` forwards
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(args.steps):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    fwd_ms = ev0.elapsed_time(ev1) / args.steps
+    # per-call latency distribution with HIP events
+    lat = sorted(time_events(step, 1) for _ in range(min(max(args.steps, 5), 50)))
+
+    by1, by2 = algorithmic_bytes(b, b, t, h, h0 is not None)
+    fl1, fl2 = matmul_flops(None, b, t, h)
+    kern = {
+        "k1": {"ms": k1_ms, "alg_bytes": by1, "alg_gbs": by1 / k1_ms / 1e6,
+               "alg_tflops": fl1 / k1_ms / 1e9},
+        "k2": {"ms": k2_ms, "alg_bytes": by2, "alg_gbs": by2 / k2_ms / 1e6,
+               "alg_tflops": fl2 / k2_ms / 1e9},
+    }
+    traffic = measured_traffic(b, t, h)
+    if traffic:
+        for n in kern:
+            if n in traffic:
+                kern[n]["hbm_bytes"] = traffic[n]
+                kern[n]["hbm_gbs"] = traffic[n] / kern[n]["ms"] / 1e6
+    mfma = measured_mfma(kern, b, t, h)
+    if mfma:
+        for n, m in mfma.items():
+            kern[n]["mfma"] = m
+    tot_bytes = by1 + by2
+    achieved = tot_bytes / fwd_ms / 1e6
+    roofline = {
+        "bound": "hbm",
+        "kernel": "forward: stage 1 (k1_kernel) + stage 2 (k2_kernel), one launch each",
+        "achieved": round(achieved, 2),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 5),
+        "traffic": (sum(traffic[n] for n in ("k1", "k2")) if traffic and "k1" in traffic
+                    and "k2" in traffic else None),
+        "alg_bytes": tot_bytes,
+        "alg_bytes_rule": "B*T*H*1282 + 65536*B*H*(h0 passed + ht) + 516*H",
+        "forward_ms_events": round(fwd_ms, 5),
+        "matmul_flops": fl1 + fl2,
+        "alg_tflops": round((fl1 + fl2) / fwd_ms / 1e9, 2),
+        "alg_mfma_frac": round((fl1 + fl2) / fwd_ms / 1e9 / BF16_PEAK_TFLOPS, 5),
+        "kernels": {n: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
+                        for kk, vv in d.items()} for n, d in kern.items()},
+    }
+    h0_txt = {None: "no initial state", "zeros": "zero initial state passed"}.get(
+        c["h0"], f"initial state ~N(0,{c['h0']})")
+    result = {
+        "metric": METRIC if name == "c2" else
+        f"KDA fwd tokens/sec and ms at B={b} T={t} H={h} bf16 (BASELINE {name})",
+        "value": round(b * t / (wall_ms / 1e3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"kda_bt16_fwd B={b} T={t} H={h} K=V={D} (BASELINE configs[{name[1]}]), "
+                        f"{h0_txt}, g_raw std {c['g_std']}, final state out, all in-kernel flags",
+            "global_batch": b,
+            "seq_len": t,
+            "heads": h,
+            "parallelism": "none (1 GPU)",
+        },
+        "latency_ms": {"p20": round(lat[len(lat) // 5], 4),
+                       "median": round(statistics.median(lat), 4),
+                       "p80": round(lat[(4 * len(lat)) // 5], 4)},
+        "roofline": roofline,
+        "precision": {kk: (float(f"{vv:.4g}") if isinstance(vv, float) else vv)
+                      for kk, vv in precision.items()},
+    }
+    if name == "c2":
+        result["vs_baseline"] = round((b * t / (wall_ms / 1e3)) / (b * t / (REF_MS / 1e3)), 2)
+        result["baseline_ref"] = ("reference kda_bt16_fwd 20.5 ms at this shape on Ascend "
+                                  "910B3 (README.md:53)")
+    if cpu:
+        result["cpu_baseline"] = cpu_baseline(inputs_cpu if inputs_cpu is not None
+                                              else make_inputs())
+    return result
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -403,8 +625,10 @@ def main() -> None:
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 256 MiB device copy (3 launches), the reference "
                          "kernel for scaling rocprof FETCH_SIZE / WRITE_SIZE to bytes")
-    ap.add_argument("--workload", choices=("headline", "varlen", "decode", "train"),
+    ap.add_argument("--workload", choices=("headline", "config", "varlen", "decode", "train"),
                     default="headline")
+    ap.add_argument("--config", choices=sorted(CONFIGS), default="c2",
+                    help="BASELINE config of --workload config")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the forward shards over (batch, head) with no "
@@ -434,98 +658,11 @@ def main() -> None:
     if args.workload == "train":
         print(json.dumps(run_train(args, dev, inputs_cpu)), flush=True)
         return
-    q, k, v, g, beta, A_log, dt_bias = (x.to(dev) for x in inputs_cpu)
-    kw = dict(scale=SCALE, output_final_state=True, use_qk_l2norm_in_kernel=True,
-              use_gate_in_kernel=True, use_beta_sigmoid_in_kernel=True,
-              lower_bound=LOWER_BOUND, A_log=A_log, dt_bias=dt_bias)
-
-    def step():
-        return kda_bt16_fwd(q, k, v, g, beta, **kw)
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    # timed region: synchronize on both sides, exactly `steps` forwards
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    # per-call latency distribution with HIP events
-    lat = []
-    for _ in range(min(max(args.steps, 5), 50)):
-        lat.append(time_events(step, 1))
-    lat.sort()
-
-    # per-kernel durations with HIP events on the launch stream
-    k1, k2, _, _ = kda_bt16_stage_launchers(q, k, v, g, beta, output_final_state=True,
-                                            A_log=A_log, dt_bias=dt_bias, lower_bound=LOWER_BOUND)
-    k1(); k2()
-    reps = max(args.steps, 10)
-    k1_ms = time_events(k1, reps)
-    k2_ms = time_events(k2, reps)
-    by1, by2 = algorithmic_bytes()
-    fl1, fl2 = matmul_flops()
-    kern = {
-        "k1": {"ms": k1_ms, "alg_bytes": by1, "alg_gbs": by1 / k1_ms / 1e6,
-               "tflops": fl1 / k1_ms / 1e9},
-        "k2": {"ms": k2_ms, "alg_bytes": by2, "alg_gbs": by2 / k2_ms / 1e6,
-               "tflops": fl2 / k2_ms / 1e9},
-    }
-    dom = "k1" if k1_ms >= k2_ms else "k2"
-    achieved = kern[dom]["alg_gbs"]
-    traffic = measured_traffic()
-    if traffic:
-        for n in kern:
-            if n in traffic:
-                kern[n]["hbm_bytes"] = traffic[n]
-                kern[n]["hbm_gbs"] = traffic[n] / kern[n]["ms"] / 1e6
-    tot_bytes = by1 + by2
-    roofline = {
-        "bound": "hbm",
-        "kernel": dom,
-        "achieved": round(achieved, 2),
-        "peak": HBM_PEAK_GBS,
-        "unit": "GB/s",
-        "frac": round(achieved / HBM_PEAK_GBS, 5),
-        "traffic": (traffic or {}).get(dom),
-        "forward_alg_bytes": tot_bytes,
-        "forward_alg_gbs": round(tot_bytes / wall_ms / 1e6, 2),
-        "forward_mfma_frac": round((fl1 + fl2) / wall_ms / 1e9 / BF16_PEAK_TFLOPS, 6),
-        "kernels": {n: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
-                        for kk, vv in d.items()} for n, d in kern.items()},
-    }
-
-    result = {
-        "metric": METRIC,
-        "value": round(B * T / (wall_ms / 1e3), 1),
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(wall_ms, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": round((B * T / (wall_ms / 1e3)) / (B * T / (REF_MS / 1e3)), 2),
-        "baseline_ref": "reference kda_bt16_fwd 20.5 ms at this shape on Ascend 910B3 (README.md:53)",
-        "dtype": "bf16",
-        "data": "synthetic",
-        "config": {
-            "workload": f"kda_bt16_fwd B={B} T={T} H={H} K=V={D} (BASELINE configs[2]), "
-                        "zero h0, final state out, all in-kernel flags",
-            "global_batch": B,
-            "seq_len": T,
-            "heads": H,
-            "parallelism": "none (1 GPU)",
-        },
-        "latency_ms": {"p20": round(lat[len(lat) // 5], 4),
-                       "median": round(statistics.median(lat), 4),
-                       "p80": round(lat[(4 * len(lat)) // 5], 4)},
-        "roofline": roofline,
-    }
-    if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(inputs_cpu)
-    print(json.dumps(result), flush=True)
+    if args.workload == "config":
+        print(json.dumps(run_forward(args, dev, args.config, cpu=False)), flush=True)
+        return
+    print(json.dumps(run_forward(args, dev, "c2", cpu=not args.no_cpu_baseline,
+                                 inputs_cpu=inputs_cpu)), flush=True)
 
 
 if __name__ == "__main__":
