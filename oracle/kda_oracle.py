@@ -35,6 +35,7 @@ How each part is pinned (tests/test_oracle.py):
 
 from __future__ import annotations
 
+import contextlib
 import math
 
 import torch
@@ -45,9 +46,67 @@ EPS = 1e-6  # kernels.py:39
 BT = 16  # kernels.py:40
 
 
+# How fp32 values are rounded to bf16: "rtne" (round to nearest, ties to
+# even) is what the reference's `.to(tl.bfloat16)` does on GPUs and NPUs;
+# "rtz" (truncation) is what Triton's CPU interpreter does for the same
+# cast (triton/runtime/interpreter.py, _convert_float with no rounding
+# mode), used only to compare with fixtures that interpreter wrote.
+_BF16_ROUNDING = ["rtne"]
+
+
+@contextlib.contextmanager
+def bf16_rounding(mode: str):
+    """Within the block, kernel mode rounds to bf16 by ``mode`` ("rtne" or
+    "rtz")."""
+    if mode not in ("rtne", "rtz"):
+        raise ValueError(mode)
+    old = _BF16_ROUNDING[0]
+    _BF16_ROUNDING[0] = mode
+    try:
+        yield
+    finally:
+        _BF16_ROUNDING[0] = old
+
+
 def _bf(x: torch.Tensor) -> torch.Tensor:
-    """Round to bf16 (nearest even) and return fp32."""
+    """Round to bf16 (nearest even, or toward zero under bf16_rounding("rtz"))
+    and return fp32."""
+    if _BF16_ROUNDING[0] == "rtz":
+        bits = x.to(torch.float32).contiguous().view(torch.int32) & -65536
+        return bits.view(torch.float32)
     return x.to(torch.bfloat16).to(torch.float32)
+
+
+# The bf16 rounding points of the reference's chunked path, by name:
+#   stage 1 (kernels.py:108-113, 153, 169-176): q_hat, k_hat (the l2norm
+#   outputs), Aqk (stored bf16), A (bf16(A_inv), the W/U operand), kb_beta
+#   (bf16(k_hat * beta)), kb (bf16(kb_beta * 2^G)), vb (bf16(v * beta)), w, u;
+#   stage 2 (kernels.py:261-291): hc (bf16(S)), v_new, qg (bf16(q_hat * 2^G)),
+#   o, kg (bf16(k_hat * 2^(G_last - G))).
+# `planted_mistake` leaves named points unrounded: the tests use it to show
+# which of them the fixtures written by the reference's own kernels pin.
+ROUNDING_POINTS = ("q_hat", "k_hat", "Aqk", "A", "kb_beta", "kb", "vb", "w", "u",
+                   "hc", "v_new", "qg", "o", "kg")
+_UNROUNDED: set = set()
+
+
+@contextlib.contextmanager
+def planted_mistake(*names: str):
+    """Within the block, kernel mode skips the named bf16 rounding points
+    (test use only: a planted mistake for mutation tests)."""
+    bad = set(names) - set(ROUNDING_POINTS)
+    if bad:
+        raise ValueError(f"unknown rounding points {sorted(bad)}")
+    _UNROUNDED.update(names)
+    try:
+        yield
+    finally:
+        _UNROUNDED.difference_update(names)
+
+
+def _rb(name: str, x: torch.Tensor) -> torch.Tensor:
+    """bf16 rounding at the named point (kernel mode)."""
+    return x if name in _UNROUNDED else _bf(x)
 
 
 def _chunks(x: torch.Tensor, NT: int) -> torch.Tensor:
@@ -109,7 +168,7 @@ def k1_reference(
         qn = qc * (1.0 / torch.sqrt((qc * qc).sum(-1, keepdim=True) + EPS))
         kn = kc * (1.0 / torch.sqrt((kc * kc).sum(-1, keepdim=True) + EPS))
         if not exact:
-            qn, kn = _bf(qn), _bf(kn)
+            qn, kn = _rb("q_hat", qn), _rb("k_hat", kn)
     else:
         qn, kn = qc, kc
 
@@ -158,12 +217,12 @@ def k1_reference(
         u = A @ vb
         Aqk_st = Aqk
     else:  # kernels.py:170-176: bf16 A, bf16 operands, fp32 accumulation, bf16 stores
-        A = _bf(A_inv)
-        kb = _bf(_bf(kn * bc[..., None]) * torch.exp2(G))
-        vb = _bf(vc * bc[..., None])
-        w = _bf(A @ kb)
-        u = _bf(A @ vb)
-        Aqk_st = _bf(Aqk)
+        A = _rb("A", A_inv)
+        kb = _rb("kb", _rb("kb_beta", kn * bc[..., None]) * torch.exp2(G))
+        vb = _rb("vb", vc * bc[..., None])
+        w = _rb("w", A @ kb)
+        u = _rb("u", A @ vb)
+        Aqk_st = _rb("Aqk", Aqk)
 
     return {
         "q_hat": qn, "k_hat": kn, "beta": bc, "G": G, "Aqk": Aqk_st, "Akk": Akk,
@@ -178,7 +237,7 @@ def k2_reference(st: dict, scale, *, h0=None, state_v_first=True, mode="kernel",
     """
     exact = mode == "exact"
     dt = torch.float64 if exact else torch.float32
-    rb = (lambda x: x) if exact else _bf
+    rb = (lambda name, x: x) if exact else _rb
     qn, kn, G = st["q_hat"], st["k_hat"], st["G"]
     w, u, Aqk, nvalid, T = st["w"], st["u"], st["Aqk"], st["nvalid"], st["T"]
     B, H, NT = qn.shape[:3]
@@ -193,17 +252,17 @@ def k2_reference(st: dict, scale, *, h0=None, state_v_first=True, mode="kernel",
         S = S.clone()
     o = torch.empty(B, H, NT, BT, V, dtype=dt)
     for c in range(NT):
-        hc = rb(S)
+        hc = rb("hc", S)
         hct = hc.transpose(-1, -2)
         Gc = G[:, :, c]
         vnew = u[:, :, c] - w[:, :, c] @ hct  # kernels.py:261-266
-        vb = rb(vnew)
-        qg = rb(qn[:, :, c] * torch.exp2(Gc))  # kernels.py:269
+        vb = rb("v_new", vnew)
+        qg = rb("qg", qn[:, :, c] * torch.exp2(Gc))  # kernels.py:269
         oc = (qg @ hct) * scale + Aqk[:, :, c] @ vb  # kernels.py:270-276
-        o[:, :, c] = rb(oc)
+        o[:, :, c] = rb("o", oc)
         last = int(nvalid[c]) - 1  # kernels.py:282
         Gl = Gc[:, :, last]  # [B, H, K]
-        kg = rb(kn[:, :, c] * torch.exp2(Gl[:, :, None, :] - Gc))  # kernels.py:285-286
+        kg = rb("kg", kn[:, :, c] * torch.exp2(Gl[:, :, None, :] - Gc))  # kernels.py:285-286
         S = S * torch.exp2(Gl)[:, :, None, :] + vb.transpose(-1, -2) @ kg  # kernels.py:288-290
     o = _unchunk(o, T)
     if out_dtype is not None:
