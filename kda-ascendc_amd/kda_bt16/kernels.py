@@ -126,10 +126,11 @@ def _validate_kda_inputs(
         raise TypeError(f"v must be bfloat16, got {v.dtype}")
     if use_gate_in_kernel and g.dtype not in (torch.float32, torch.bfloat16):
         raise TypeError(f"g must be float32 when use_gate_in_kernel=True, got {g.dtype}")
-    if g.dtype not in (torch.float32, torch.bfloat16):
-        raise TypeError(f"g must be float32 or bfloat16, got {g.dtype}")
+    # Without the in-kernel gate the reference takes g of any dtype and
+    # widens it to fp32 at load (kernels.py:673-674, 108); _gate_f32 does
+    # that on the host for dtypes other than fp32 / bf16.
     if beta.dtype not in (torch.float32, torch.bfloat16):
-        raise TypeError(f"beta must be float32, got {beta.dtype}")
+        raise TypeError(f"beta must be float32 or bfloat16, got {beta.dtype}")
 
     if k.shape != q.shape:
         raise ValueError(f"k.shape {k.shape} must match q.shape {q.shape}")
@@ -218,6 +219,15 @@ def _validate_kda_inputs(
             raise ValueError("use_gate_in_kernel requires A_log")
 
     return B, T, H, K, HV, V
+
+
+def _gate_f32(g: torch.Tensor) -> torch.Tensor:
+    """g as the kernels read it: fp32 or bf16 as given, any other dtype
+    widened to fp32 (the reference's ``.to(tl.float32)`` at load,
+    kernels.py:108)."""
+    if g.dtype in (torch.float32, torch.bfloat16):
+        return g
+    return g.to(torch.float32)
 
 
 def _require_gpu(q: torch.Tensor) -> None:
@@ -325,6 +335,7 @@ def _run(
     backward starts from."""
     del use_fused  # one production path; see module docstring
     _require_gpu(q)
+    g = _gate_f32(g)
     q, k, v, g, initial_state, dt_bias = (
         _aligned(x) for x in (q, k, v, g, initial_state, dt_bias))
     B, T, H, K = q.shape
@@ -399,6 +410,8 @@ def _bwd_run(
     ddt_bias are None without the in-kernel gate (or dt_bias), dh0 is None
     without an initial state."""
     _require_gpu(q)
+    g_dtype = g.dtype
+    g = _gate_f32(g)
     q, k, v, g, initial_state, dt_bias = (
         _aligned(x) for x in (q, k, v, g, initial_state, dt_bias))
     dev = q.device
@@ -425,7 +438,10 @@ def _bwd_run(
         )
         ws_bytes = (_hip.bwd_workspace_bytes(fa) if saved is None
                     else _hip.bwd_saved_workspace_bytes(fa))
-        ws = workspace.lease(dev, stream, ws_bytes)
+        # Not pooled: a backward's workspace (up to ~106 KiB per record slot)
+        # goes back to torch's caching allocator when the call's work is
+        # done, instead of staying leased to every later forward.
+        ws = workspace.scratch(dev, ws_bytes)
         ba = _hip.KdaBt16BwdArgs()
         ba.fwd = ctypes.pointer(fa)
         ba.dout = do.data_ptr()
@@ -440,7 +456,7 @@ def _bwd_run(
             _hip.call("kda_bt16_bwd_hip", ba, stream)
         else:
             _hip.call_saved("kda_bt16_bwd_saved_hip", ba, saved.data_ptr(), saved.numel(), stream)
-    return dq, dk, dv, dg, dbeta, dA_log, ddt_bias, dh0
+    return dq, dk, dv, dg.to(g_dtype), dbeta, dA_log, ddt_bias, dh0
 
 
 class _KdaBt16Fn(torch.autograd.Function):
@@ -461,14 +477,17 @@ class _KdaBt16Fn(torch.autograd.Function):
             reuse_workspace=reuse, cu_seqlens=cu_seqlens, g_log=g_log, save_state=save,
         )
         o, ht = res[0], res[1]
-        ctx.state = res[2] if save else None
-        ctx.save_for_backward(q, k, v, g, beta, A_log, dt_bias, initial_state, cu_seqlens)
+        # The per-chunk state goes through save_for_backward with the inputs:
+        # autograd frees it once the backward has run (and saved-tensor
+        # hooks such as checkpointing see it), while o may live on.
+        ctx.save_for_backward(q, k, v, g, beta, A_log, dt_bias, initial_state, cu_seqlens,
+                              res[2] if save else None)
         ctx.cfg = cfg
         return o, ht
 
     @staticmethod
     def backward(ctx, do, dht):
-        q, k, v, g, beta, A_log, dt_bias, h0, cu = ctx.saved_tensors
+        q, k, v, g, beta, A_log, dt_bias, h0, cu, state = ctx.saved_tensors
         (scale, _ofs, l2, use_gate, bsig, lower_bound, svf, g_log, _reuse) = ctx.cfg
         if do is None:
             do = torch.zeros(v.shape, dtype=torch.bfloat16, device=v.device)
@@ -476,7 +495,7 @@ class _KdaBt16Fn(torch.autograd.Function):
         dq, dk, dv, dg, dbeta, dA_log, ddt_bias, dh0 = _bwd_run(
             do, dht, q, k, v, g, beta, scale, h0, l2, use_gate, bsig, lower_bound, A_log,
             dt_bias, svf, cu, g_log, need_gate_grads=need[5] or need[6], need_dh0=need[7],
-            saved=ctx.state,
+            saved=state,
         )
         return (dq, dk, dv, dg, dbeta, dA_log if need[5] else None,
                 ddt_bias if need[6] else None, dh0 if need[7] else None, None, None)

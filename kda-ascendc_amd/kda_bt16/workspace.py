@@ -1,6 +1,9 @@
 """Workspace pool for the records stage 1 hands to stage 2.
 
-One grow-only device buffer per (device, stream).  Work on one stream runs
+One grow-only device buffer per (device, stream), for the forward's
+records only; the backward's larger workspace is taken per call from torch's
+caching allocator (:func:`scratch`), so a training step leaves no
+backward-sized lease behind for later forwards.  Work on one stream runs
 in order, so the next forward on the same stream may overwrite the records
 of the previous one; forwards on different streams never share a buffer.
 The buffer is sized exactly by ``kda_bt16_workspace_bytes`` (17 KiB per
@@ -36,6 +39,12 @@ def lease(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
             buf = torch.empty(size, dtype=torch.uint8, device=device)
             _pool[key] = buf
         return buf
+
+
+def scratch(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A uint8 device buffer of ``nbytes`` (rounded up to 256 B) for one
+    call, from torch's caching allocator (not pooled here)."""
+    return torch.empty(max(256, (nbytes + 255) // 256 * 256), dtype=torch.uint8, device=device)
 
 
 def clear() -> None:

@@ -98,3 +98,39 @@ def test_saved_state_matches_recompute(gpu_device, name, B, T, H, HV, cu, opts):
         for n, gr in recomputed[i].items():
             assert torch.isfinite(gr.float()).all(), (i, n)
             assert torch.equal(saved[i][n], gr), (i, n)
+
+
+def test_saved_state_is_freed_after_backward_while_o_lives(gpu_device):
+    """The per-chunk state goes through save_for_backward: autograd frees it
+    when the backward has run, although o (and its grad_fn) stay alive."""
+    from kda_bt16 import _hip, kda_bt16_fwd
+    from kda_bt16.kernels import _flags, _make_args
+
+    dev = gpu_device
+    B, T, H = 1, 2048, 8
+    c = make_inputs(B, T, H, seed=9)
+    leaves = {n: c[n].to(dev).requires_grad_(True) for n in ("q", "k", "v", "g", "beta", "A_log")}
+    args = _make_args(leaves["q"], leaves["k"], leaves["v"], leaves["g"], leaves["beta"], 0.1,
+                      -5.0, leaves["A_log"], None, None, leaves["v"], None, None, 0,
+                      _flags(True, True, True, True))
+    saved_bytes = _hip.saved_bytes(args)
+    assert saved_bytes > 32 << 20  # ~55 KiB per record slot, 1024 slots
+    torch.cuda.synchronize()
+    o, _ = kda_bt16_fwd(leaves["q"], leaves["k"], leaves["v"], leaves["g"], leaves["beta"], 0.1,
+                        use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True,
+                        use_beta_sigmoid_in_kernel=True, lower_bound=-5.0, A_log=leaves["A_log"])
+    torch.cuda.synchronize()
+    state = [t for t in o.grad_fn.saved_tensors if t is not None and t.dtype == torch.uint8]
+    assert len(state) == 1 and state[0].numel() == saved_bytes
+    del state
+    held = torch.cuda.memory_allocated(dev)
+    o.backward(torch.ones_like(o))
+    torch.cuda.synchronize()
+    after = torch.cuda.memory_allocated(dev)
+    # autograd has released what the node saved, the state included ...
+    with pytest.raises(RuntimeError, match="freed"):
+        _ = o.grad_fn.saved_tensors
+    # ... and its memory: the gradients were allocated, the state freed
+    # (2 MiB of slack for buffers torch keeps after a first backward)
+    grads = sum(t.grad.numel() * t.grad.element_size() for t in leaves.values())
+    assert held + grads - after >= saved_bytes - (1 << 21), (held, after, grads, saved_bytes)

@@ -269,3 +269,28 @@ def test_stream_ordering_on_side_stream(gpu_device):
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     assert torch.equal(o, o_ref) and torch.equal(ht, ht_ref)
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.float64])
+def test_precomputed_g_of_other_float_dtypes(dt, gpu_device):
+    """kernels.py:673-674, 108: without the in-kernel gate the reference
+    takes g of any dtype and widens it to fp32 at load.  The result equals
+    the call with that widening done by hand, bit for bit, and the gradient
+    comes back in g's dtype."""
+    c = make_inputs(1, 70, 2, seed=31, h0_std=0.05)
+    gen = torch.Generator().manual_seed(3)
+    gate = -5.0 * torch.sigmoid(torch.randn(1, 80, 2, 128, generator=gen))
+    g = (torch.cumsum(gate.view(1, 5, 16, 2, 128), 2) * 1.4426950216).view(1, 80, 2, 128)[:, :70]
+    g = g.contiguous().to(dt)
+    args, cfg = _hip(c, gpu_device, use_gate_in_kernel=False)
+    args[3] = g.to(gpu_device)
+    o1, ht1 = kda_bt16_fwd(*args, **cfg)
+    args2 = list(args)
+    args2[3] = g.to(gpu_device).float()
+    o2, ht2 = kda_bt16_fwd(*args2, **cfg)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(ht1, ht2)
+    gl = args[3].clone().requires_grad_(True)
+    o3, _ = kda_bt16_fwd(args[0], args[1], args[2], gl, args[4], **cfg)
+    o3.float().sum().backward()
+    assert gl.grad.dtype == dt and torch.isfinite(gl.grad.double()).all()

@@ -69,8 +69,23 @@ def test_dtype_errors():
         kda_bt16_fwd(q, k, v.float(), g, beta)
     with pytest.raises(TypeError, match="g must be float32 when use_gate_in_kernel=True"):
         kda_bt16_fwd(q, k, v, g.half(), beta, use_gate_in_kernel=True, A_log=torch.zeros(H))
-    with pytest.raises(TypeError, match="beta must be float32"):
+    with pytest.raises(TypeError, match="beta must be float32 or bfloat16"):
         kda_bt16_fwd(q, k, v, g, beta.double())
+    with pytest.raises(TypeError, match="beta must be float32 or bfloat16"):
+        kda_bt16_fwd(q, k, v, g, beta.half())
+
+
+def test_g_of_any_float_dtype_without_the_in_kernel_gate():
+    """kernels.py:673-674: only the in-kernel gate restricts g's dtype; the
+    kernels widen any other g to fp32.  Validation passes, and these CPU
+    tensors are then refused by the GPU check."""
+    q, k, v, g, beta = _inputs()
+    for dt in (torch.float16, torch.float64, torch.bfloat16):
+        with pytest.raises(ValueError, match="runs on a ROCm GPU"):
+            kda_bt16_fwd(q, k, v, g.to(dt), beta)
+    # bf16 beta is accepted too (a superset of the reference's fp32)
+    with pytest.raises(ValueError, match="runs on a ROCm GPU"):
+        kda_bt16_fwd(q, k, v, g, beta.bfloat16())
 
 
 def test_state_and_gate_parameter_errors():
