@@ -354,6 +354,11 @@ __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast
 namespace kda {
 hipError_t launch_k1(const Params& p, hipStream_t stream);
 hipError_t launch_k2(const Params& p, hipStream_t stream);
+// Stage 2 with several value tiles per work-group (kda_k2w.hip): the tile
+// count launch_k2 picks for a geometry on `ncu` CUs (0: one per work-group),
+// and the launch with `tpw` tiles (2, 4 or 8).
+int k2_wide_tiles(const Params& p, int ncu);
+hipError_t launch_k2_wide(const Params& p, int tpw, hipStream_t stream);
 hipError_t launch_recurrent(const Params& p, hipStream_t stream);
 // Backward (kda_bt16_bwd.hip, and the training variants of the stages).
 hipError_t launch_k1_both_records(const Params& p, hipStream_t stream);

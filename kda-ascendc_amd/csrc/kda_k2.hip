@@ -29,6 +29,7 @@
 #include <type_traits>
 
 #include "kda_common.h"
+#include "kda_k2_shared.h"
 
 namespace kda {
 
@@ -66,13 +67,6 @@ static_assert(REC_QG % 1024 == 0 && REC_KG - REC_QG == 4096, "qg is four whole l
 constexpr int HC_BYTES = 4 * 1024;
 constexpr int VN_BYTES = 512;
 
-typedef __attribute__((address_space(3))) uint8_t lds_u8;
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N));
-}
-
 // Copy wave: wait until the chunk followed by `n_after` issued chunks has
 // landed (0 <= n_after <= LEAD - 2).
 // NL: loads issued per chunk.
@@ -91,10 +85,6 @@ __device__ __forceinline__ void wait_chunk_ladder(int n_after) {
 
 template <int NL = LOADS_PER_CHUNK>
 __device__ __forceinline__ void wait_chunk(int n_after) { wait_chunk_ladder<LEAD - 2, NL>(n_after); }
-
-// Buffer descriptor word 3 for raw byte-addressed buffers on gfx9-family
-// parts (gfx950 included).
-constexpr int BUF_DWORD3 = 0x00020000;
 
 // One chunk's copy: 13 shared KiB, then the u pair.  Buffer loads with the
 // chunk offset in an SGPR and a fixed per-lane VGPR offset.
@@ -134,23 +124,8 @@ __device__ __forceinline__ void read_state_ops_a(const uint8_t* slot, int lane, 
         op.kg[j] = *reinterpret_cast<const u32x4*>(slot + REC_KG + j * 1024 + lane * 16);
 }
 
-// Lane (x, q4) reads 2^G_last at [kt = x/2][q4][i = 2*(x%2) .. +1].
-__device__ __forceinline__ uint32_t decay_offset(int lane) {
-    const int x = lane & 15, q4 = lane >> 4;
-    return REC_DECAY + (x >> 1) * 64 + q4 * 16 + (x & 1) * 8;
-}
-
 __device__ __forceinline__ void read_state_ops_b(const uint8_t* slot, int lane, StateOps& op) {
     op.dc = *reinterpret_cast<const f32x2*>(slot + decay_offset(lane));
-}
-
-// Scales the state tile kt by its decay: element i of lane (x, q4) takes
-// 2^G_last[16*kt + 4*q4 + i] from lane 2*kt + i/2 of its row (DPP
-// row_newbcast, row_bcast in kda_common.h), component i % 2.
-template <int KT>
-__device__ __forceinline__ f32x4 decay_tile(f32x4 st, f32x2 dc) {
-    return f32x4{st[0] * row_bcast<2 * KT>(dc.x), st[1] * row_bcast<2 * KT>(dc.y),
-                 st[2] * row_bcast<2 * KT + 1>(dc.x), st[3] * row_bcast<2 * KT + 1>(dc.y)};
 }
 
 // The record ring and the hand-off buffers of the work-group, referenced
@@ -162,23 +137,6 @@ __shared__ __attribute__((aligned(16))) uint8_t vn_buf[HANDOFF][VN_BYTES];
 
 __device__ __forceinline__ lds_u8* ring_lds() { return (lds_u8*)ring; }
 
-// s_waitcnt immediates on gfx9-family parts: vmcnt field (bits 3:0 and
-// 15:14) and expcnt (bits 6:4) at their maxima, lgkmcnt (bits 11:8) 0 or 15.
-constexpr int WAITCNT_LGKM0 = 0xC07F;
-constexpr int WAITCNT_LGKM15 = 0xCF7F;
-
-// Chunk barrier: the wave's LDS accesses are complete, then all three waves
-// meet.  The wait and barrier are one inline asm block whose memory clobber
-// keeps every LDS access on its side; as asm, the barrier carries no
-// implied wait on the output wave's stores.  The builtin wait after it
-// costs nothing (the count is already zero) but tells the compiler so,
-// which keeps it from adding conservative waits for LDS reads issued
-// before the barrier.
-__device__ __forceinline__ void chunk_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    __builtin_amdgcn_s_waitcnt(WAITCNT_LGKM0);
-}
-
 // The state wave's barrier after a chunk that is followed by another: its
 // last LDS accesses (the v_new hand-off, the next chunk's kg) need not be
 // complete yet.  The hand-off a chunk writes is read two barriers later;
@@ -188,10 +146,6 @@ __device__ __forceinline__ void chunk_barrier_nodrain() {
     asm volatile("s_waitcnt lgkmcnt(15)\n\ts_barrier" ::: "memory");
     __builtin_amdgcn_s_waitcnt(WAITCNT_LGKM15);
 }
-
-// The copy wave's side of the barrier: no clobber, so the compiler adds no
-// wait for its loads in flight.
-__device__ __forceinline__ void copy_barrier() { asm volatile("s_barrier"); }
 
 // Constants of the chunk loop.
 struct Ctx {
@@ -634,40 +588,6 @@ __device__ __forceinline__ void bwd_round_tail(const Ctx& cx, int c, f32x4 (&D)[
     if constexpr (N > 1) bwd_round_tail<(S + 1) % RING, N - 1>(cx, c + 1, D, op, bop);
 }
 
-// Fp32 state slice of this lane from `src` ([V, K] if v_first, else
-// [K, V]; null: zeros): St[kt][i] = S[v][16*kt + 4*q4 + i].
-__device__ __forceinline__ void load_state_from(const float* src, bool v_first, int v, int q4,
-                                                f32x4 (&St)[8]) {
-#pragma unroll
-    for (int kt = 0; kt < 8; ++kt) {
-        St[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (src) {
-            const int k0 = 16 * kt + 4 * q4;
-            if (v_first) {
-                St[kt] = *reinterpret_cast<const f32x4*>(src + (int64_t)v * DK + k0);
-            } else {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) St[kt][i] = src[(int64_t)(k0 + i) * DK + v];
-            }
-        }
-    }
-}
-
-__device__ __forceinline__ void store_state_to(float* dst, bool v_first, int v, int q4,
-                                               const f32x4 (&St)[8]) {
-    if (!dst) return;
-#pragma unroll
-    for (int kt = 0; kt < 8; ++kt) {
-        const int k0 = 16 * kt + 4 * q4;
-        if (v_first) {
-            *reinterpret_cast<f32x4*>(dst + (int64_t)v * DK + k0) = St[kt];
-        } else {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) dst[(int64_t)(k0 + i) * DK + v] = St[kt][i];
-        }
-    }
-}
-
 __device__ __forceinline__ void bwd_state_wave(const Params& p, const Ctx& cx, int bh) {
     const int lane = cx.lane, q4 = cx.q4, vt = cx.vt;
     const int v = 16 * vt + (lane & 15);
@@ -700,45 +620,6 @@ __device__ __forceinline__ void bwd_state_wave(const Params& p, const Ctx& cx, i
     bwd_round_tail<1 % RING, RING>(cx, c, D, op, bop);
     chunk_barrier();  // the output wave's last step
     store_state_to(p.dh0 ? p.dh0 + sbase : nullptr, p.h0_v_first != 0, v, q4, D);
-}
-
-// S^T tiles of this lane: St[kt][i] = S[v][16*kt + 4*q4 + i], v = 16*vt + lane%16.
-// (The layout and presence tests are outside the loads, so that all of them
-// are in flight before the first wait.)
-__device__ __forceinline__ void load_state(const Params& p, int64_t sbase, int v, int q4,
-                                           f32x4 (&St)[8]) {
-    if (!p.h0) {
-#pragma unroll
-        for (int kt = 0; kt < 8; ++kt) St[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    } else if (p.h0_v_first) {
-#pragma unroll
-        for (int kt = 0; kt < 8; ++kt)
-            St[kt] = *reinterpret_cast<const f32x4*>(p.h0 + sbase + (int64_t)v * DK + 16 * kt + 4 * q4);
-    } else {
-#pragma unroll
-        for (int kt = 0; kt < 8; ++kt) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                St[kt][i] = p.h0[sbase + (int64_t)(16 * kt + 4 * q4 + i) * DK + v];
-        }
-    }
-}
-
-__device__ __forceinline__ void store_state(const Params& p, int64_t sbase, int v, int q4,
-                                            const f32x4 (&St)[8]) {
-    if (!p.ht) return;
-    if (p.ht_v_first) {
-#pragma unroll
-        for (int kt = 0; kt < 8; ++kt)
-            *reinterpret_cast<f32x4*>(p.ht + sbase + (int64_t)v * DK + 16 * kt + 4 * q4) = St[kt];
-    } else {
-#pragma unroll
-        for (int kt = 0; kt < 8; ++kt) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                p.ht[sbase + (int64_t)(16 * kt + 4 * q4 + i) * DK + v] = St[kt][i];
-        }
-    }
 }
 
 __device__ __forceinline__ void state_wave(const Params& p, const Ctx& cx, int bh) {
@@ -1124,6 +1005,9 @@ hipError_t launch_k2(const Params& p, hipStream_t stream) {
     const int nseq = p.cu_seqlens ? p.N : p.B;
     const int64_t tiles = (int64_t)p.HV * 8;
     const int ncu = cu_count();
+    // More (sequence, head, value tile) triples than CUs: several tiles per
+    // work-group share one record stream (kda_k2w.hip).
+    if (const int tpw = k2_wide_tiles(p, ncu)) return launch_k2_wide(p, tpw, stream);
     if (nseq > 1 && nseq * tiles > ncu) {
         // several sequences per work-group, in as many groups as fill the
         // CUs once (at least one)

@@ -1,0 +1,331 @@
+// Stage 2 of the KDA BT=16 forward for throughput-bound shapes: several
+// value tiles per work-group sharing one record stream.
+//
+// Same recurrence as kda_k2.hip (kernels.py:225-302), per chunk
+//   hc    = bf16(S)
+//   v_new = bf16(u - w @ hc^T)
+//   o     = bf16(scale * (qg @ hc^T) + Aqk @ v_new)
+//   S     = S * 2^G_last[None, :] + (kg^T @ v_new)^T
+// with identical arithmetic, so o and ht are bit for bit those of
+// kda_k2.hip.  What changes is who does the work:
+//
+// kda_k2.hip gives each (sequence, head, 16 value columns) a work-group of
+// its own, which pulls the 13 KiB of the record that every value tile needs
+// through its CU's texture path: with more such work-groups than CUs, that
+// repeated pull (8x per head and chunk) is what paces the kernel.  Here a
+// work-group takes TPW value tiles of one (sequence, head):
+//   * one copy wave streams each chunk's record once -- the shared 13 KiB
+//     and the TPW u slices -- into an LDS ring (direct buffer->LDS loads);
+//   * TPW / 2 compute waves each own two value tiles.  A compute wave keeps
+//     both tiles' state slices in registers (S^T as eight 16x16 fp32
+//     accumulator tiles each, the layout of kda_k2.hip) and forms both
+//     v_new, both o and both state updates itself: no hand-off through LDS.
+//     The operands every tile shares (w, qg, kg, Aqk, the decay) are read
+//     from LDS once per wave for its two tiles, for the next chunk while
+//     this one is computed.
+// The waves meet at one barrier per chunk.
+#include <cstdlib>
+
+#include "kda_common.h"
+#include "kda_k2_shared.h"
+
+namespace kda {
+
+namespace {
+
+constexpr int SHARED_LOADS_W = REC_SHARED / 1024;  // 13
+
+// Ring geometry of a TPW-tile work-group.  A slot holds the shared 13 KiB
+// and the TPW u slices of this work-group's tiles (contiguous in the
+// record).  The copy wave issues chunk c + LEAD during chunk c and, before
+// the barrier that ends chunk c, waits for chunk c + 1, which the compute
+// waves read during chunk c + 1.  Chunk j's slot is read during chunk j and
+// refilled with chunk j + RING during chunk j + RING - LEAD = j + 1, after
+// that read.  Direct loads count in the 6-bit vmcnt: LEAD chunks of loads
+// must fit in 63.
+template <int TPW>
+struct WideGeom {
+    static_assert(TPW == 2 || TPW == 4 || TPW == 8, "two, four or eight value tiles");
+    static constexpr int NCW = TPW / 2;                    // compute waves
+    static constexpr int NL = SHARED_LOADS_W + TPW / 2;    // 1 KiB loads per chunk
+    static constexpr int LEAD = 4 * NL <= 63 ? 4 : 3;
+    static constexpr int RING = LEAD + 1;
+    static constexpr int SLOT = REC_SHARED + TPW * 512;
+    static constexpr int THREADS = 64 * (NCW + 1);
+    static_assert(LEAD * NL <= 63, "vmcnt is a 6-bit count");
+};
+
+// The operands a compute wave reads for one chunk.
+struct WideOps {
+    u32x4 w[4];   // -w, 16x16x32 A operands (k-tile pairs)
+    u32x4 qg[4];  // qg, likewise
+    u32x4 kg[4];  // kg, 16x16x16 A operands of the update (two k-tiles each)
+    u32x2 aqk;    // Aqk, 16x16x16 A operand
+    f32x2 dc;     // 2^G_last for the decay broadcast
+    u32x2 u[2];   // u of the two tiles, fp32 accumulator start (bf16 pairs)
+};
+
+__device__ __forceinline__ void read_wide_ops(const uint8_t* slot, int lane, int ut, WideOps& op) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        op.w[j] = *reinterpret_cast<const u32x4*>(slot + REC_W + j * 1024 + lane * 16);
+        op.qg[j] = *reinterpret_cast<const u32x4*>(slot + REC_QG + j * 1024 + lane * 16);
+        op.kg[j] = *reinterpret_cast<const u32x4*>(slot + REC_KG + j * 1024 + lane * 16);
+    }
+    op.aqk = *reinterpret_cast<const u32x2*>(slot + REC_AQK + lane * 8);
+    op.dc = *reinterpret_cast<const f32x2*>(slot + decay_offset(lane));
+    op.u[0] = *reinterpret_cast<const u32x2*>(slot + REC_SHARED + ut * 512 + lane * 8);
+    op.u[1] = *reinterpret_cast<const u32x2*>(slot + REC_SHARED + (ut + 1) * 512 + lane * 8);
+}
+
+__device__ __forceinline__ f32x4 unpack_u(u32x2 u) {
+    return f32x4{__builtin_bit_cast(float, u.x << 16), __builtin_bit_cast(float, u.x & 0xffff0000u),
+                 __builtin_bit_cast(float, u.y << 16), __builtin_bit_cast(float, u.y & 0xffff0000u)};
+}
+
+// bf16(S^T) of k-tiles 2j, 2j+1 of one value tile: a 16x16x32 B operand.
+__device__ __forceinline__ u32x4 pack_hc(const f32x4 (&St)[8], int j) {
+    return u32x4{pack2(St[2 * j][0], St[2 * j][1]), pack2(St[2 * j][2], St[2 * j][3]),
+                 pack2(St[2 * j + 1][0], St[2 * j + 1][1]),
+                 pack2(St[2 * j + 1][2], St[2 * j + 1][3])};
+}
+
+// k-tile KT of both tiles' state update: S = S * 2^G_last + kg^T v_new (the
+// decay a VALU product on the accumulator input, as kda_k2.hip forms it).
+template <int KT>
+__device__ __forceinline__ void wide_update(f32x4 (&SA)[8], f32x4 (&SB)[8], const WideOps& op,
+                                            u32x2 vna, u32x2 vnb) {
+    const u32x4 kg = op.kg[KT >> 1];
+    const i16x4 a = as_i16x4((KT & 1) ? u32x2{kg.z, kg.w} : u32x2{kg.x, kg.y});
+    SA[KT] = mfma_bf16_16x16x16(a, as_i16x4(vna), decay_tile<KT>(SA[KT], op.dc));
+    SB[KT] = mfma_bf16_16x16x16(a, as_i16x4(vnb), decay_tile<KT>(SB[KT], op.dc));
+}
+
+// Constants of a compute wave.
+struct WideCtx {
+    uint16_t* obase[2];   // o of the sequence's first token, this lane's 4 columns of each tile
+    int64_t orow_stride;  // elements between consecutive tokens of o
+    float scale;
+    int NT, T, lane, q4;
+};
+
+// One chunk of a compute wave: both tiles' v_new, o and state update, with
+// chunk c's operands read from its ring slot at the start.  The reads are
+// covered by the packing of hc, which needs only the state; one operand set
+// is live at a time.
+__device__ __forceinline__ void wide_step(const WideCtx& cx, int c, f32x4 (&SA)[8], f32x4 (&SB)[8],
+                                          const uint8_t* slot, int ut) {
+    WideOps cur;
+    read_wide_ops(slot, cx.lane, ut, cur);
+    u32x4 ha[4], hb[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        ha[j] = pack_hc(SA, j);
+        hb[j] = pack_hc(SB, j);
+    }
+    // v_new = u - w @ hc^T: one accumulation chain per tile, from u
+    f32x4 va = unpack_u(cur.u[0]);
+    f32x4 vb = unpack_u(cur.u[1]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        va = mfma_bf16_16x16x32(as_bf16x8(cur.w[j]), as_bf16x8(ha[j]), va);
+        vb = mfma_bf16_16x16x32(as_bf16x8(cur.w[j]), as_bf16x8(hb[j]), vb);
+    }
+    // o = scale * qg @ hc^T + Aqk @ v_new
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    f32x4 oa = zero, ob = zero;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        oa = mfma_bf16_16x16x32(as_bf16x8(cur.qg[j]), as_bf16x8(ha[j]), oa);
+        ob = mfma_bf16_16x16x32(as_bf16x8(cur.qg[j]), as_bf16x8(hb[j]), ob);
+    }
+    const u32x2 vna = {pack2(va[0], va[1]), pack2(va[2], va[3])};
+    const u32x2 vnb = {pack2(vb[0], vb[1]), pack2(vb[2], vb[3])};
+    oa = oa * cx.scale;
+    ob = ob * cx.scale;
+    oa = mfma_bf16_16x16x16(as_i16x4(cur.aqk), as_i16x4(vna), oa);
+    ob = mfma_bf16_16x16x16(as_i16x4(cur.aqk), as_i16x4(vnb), ob);
+    // state update: S = S * 2^G_last + kg^T v_new, tile by tile
+    wide_update<0>(SA, SB, cur, vna, vnb);
+    wide_update<1>(SA, SB, cur, vna, vnb);
+    wide_update<2>(SA, SB, cur, vna, vnb);
+    wide_update<3>(SA, SB, cur, vna, vnb);
+    wide_update<4>(SA, SB, cur, vna, vnb);
+    wide_update<5>(SA, SB, cur, vna, vnb);
+    wide_update<6>(SA, SB, cur, vna, vnb);
+    wide_update<7>(SA, SB, cur, vna, vnb);
+    // Lane (x, q4) holds o rows 4*q4 .. +3 of column x; after the quad
+    // transpose it holds row 4*q4 + x%4, columns 4*(x/4) .. +3.
+    const int j4 = cx.lane & 3;
+    const u32x2 ota = quad_transpose(pack2(oa[0], oa[1]), pack2(oa[2], oa[3]), j4);
+    const u32x2 otb = quad_transpose(pack2(ob[0], ob[1]), pack2(ob[2], ob[3]), j4);
+    const int t = c * BT + 4 * cx.q4 + j4;
+    if (t < cx.T) {
+        const int64_t off = (int64_t)t * cx.orow_stride;
+        __builtin_nontemporal_store(ota, reinterpret_cast<u32x2*>(cx.obase[0] + off));
+        __builtin_nontemporal_store(otb, reinterpret_cast<u32x2*>(cx.obase[1] + off));
+    }
+    chunk_barrier();
+}
+
+// Chunks c .. c + N - 1 (those below NT), with the ring slot of chunk c as
+// the compile-time S (every LDS offset a constant).
+template <int TPW, int S, int N>
+__device__ __forceinline__ void wide_round(const WideCtx& cx, int c, f32x4 (&SA)[8], f32x4 (&SB)[8],
+                                           const uint8_t* ring, int ut) {
+    using G = WideGeom<TPW>;
+    if (c >= cx.NT) return;
+    wide_step(cx, c, SA, SB, ring + S * G::SLOT, ut);
+    if constexpr (N > 1) wide_round<TPW, (S + 1) % G::RING, N - 1>(cx, c + 1, SA, SB, ring, ut);
+}
+
+// Copy wave: the NL loads of one chunk, the shared part then this
+// work-group's u slices.
+template <int NL>
+__device__ __forceinline__ void issue_wide_chunk(__amdgpu_buffer_rsrc_t rs, uint32_t chunk_off,
+                                                 lds_u8* slot, uint32_t u_off, uint32_t voff16) {
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+        const uint32_t src = i < SHARED_LOADS_W ? chunk_off + i * 1024
+                                                : chunk_off + u_off + (i - SHARED_LOADS_W) * 1024;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_u8*)(slot + i * 1024), 16, voff16, src,
+                                                 0, 0);
+    }
+}
+
+// Wait until the chunk followed by `n_after` issued chunks has landed.
+template <int N, int NL>
+__device__ __forceinline__ void wide_wait_ladder(int n_after) {
+    if constexpr (N == 0) {
+        wait_vmcnt<0>();
+    } else {
+        if (n_after >= N) {
+            wait_vmcnt<N * NL>();
+        } else {
+            wide_wait_ladder<N - 1, NL>(n_after);
+        }
+    }
+}
+
+template <int TPW, int S>
+__device__ __forceinline__ void wide_copy_round(__amdgpu_buffer_rsrc_t rs, lds_u8* ring, int c,
+                                                int NT, uint32_t u_off, uint32_t voff16) {
+    using G = WideGeom<TPW>;
+    if (c >= NT) return;
+    if (c + G::LEAD < NT)
+        issue_wide_chunk<G::NL>(rs, (uint32_t)(c + G::LEAD) * REC_BYTES,
+                                ring + ((S + G::LEAD) % G::RING) * G::SLOT, u_off, voff16);
+    // chunk c + 1 is read by the compute waves after this barrier
+    if (c + 1 < NT) wide_wait_ladder<G::LEAD - 1, G::NL>(min(G::LEAD - 1, NT - 2 - c));
+    copy_barrier();
+    if constexpr (S + 1 < G::RING) wide_copy_round<TPW, S + 1>(rs, ring, c + 1, NT, u_off, voff16);
+}
+
+// Work-group (sequence, value head, slice of TPW value tiles): grid padded
+// to a multiple of 8 * (8 / TPW) and mapped XCD-aware, so that the slices
+// of one (sequence, head) share an XCD and its L2 for the records.
+template <int TPW>
+__global__ __launch_bounds__(WideGeom<TPW>::THREADS) void k2w_kernel(Params p) {
+    using G = WideGeom<TPW>;
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[G::RING * G::SLOT];
+    constexpr int NSL = 8 / TPW;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nbh = (p.cu_seqlens ? p.N : p.B) * p.HV;
+    const int total = nbh * NSL;
+    const int padded = (total + 8 * NSL - 1) / (8 * NSL) * (8 * NSL);
+    const int wg = blockIdx.x;
+    const int lin = (wg & 7) * (padded >> 3) + (wg >> 3);
+    if (lin >= total) return;  // padding: the whole work-group leaves before any barrier
+    const int bh = lin / NSL;
+    const int slice = lin - bh * NSL;
+    const int hv = bh - (bh / p.HV) * p.HV;
+    const SeqSpan sp = seq_span(p, bh);
+    const int64_t sbase = (int64_t)bh * DK * DK;
+
+    if (wave < G::NCW) {
+        const int ut = 2 * wave;               // first of this wave's two tiles in the slice
+        const int vt = slice * TPW + ut;       // its value tile
+        const int q4 = lane >> 4;
+        const int va = 16 * vt + (lane & 15);  // this lane's state row (V index) of tile A
+        f32x4 SA[8], SB[8];
+        load_state(p, sbase, va, q4, SA);
+        load_state(p, sbase, va + 16, q4, SB);
+        if (sp.nt == 0) {  // an empty sequence: the final state is the initial state
+            store_state(p, sbase, va, q4, SA);
+            store_state(p, sbase, va + 16, q4, SB);
+            __builtin_amdgcn_endpgm();
+        }
+        WideCtx cx;
+        cx.scale = p.scale;
+        cx.NT = sp.nt;
+        cx.T = sp.len;
+        cx.lane = lane;
+        cx.q4 = q4;
+        const int col = 4 * ((lane & 15) >> 2);
+        cx.obase[0] = p.o + (sp.tok0 * p.HV + hv) * DK + 16 * vt + col;
+        cx.obase[1] = cx.obase[0] + 16;
+        cx.orow_stride = (int64_t)p.HV * DK;
+        chunk_barrier();  // chunk 0 is in the ring
+        for (int c = 0; c < cx.NT; c += G::RING) wide_round<TPW, 0, G::RING>(cx, c, SA, SB, ring, ut);
+        store_state(p, sbase, va, q4, SA);
+        store_state(p, sbase, va + 16, q4, SB);
+        __builtin_amdgcn_endpgm();
+    }
+    // copy wave
+    if (sp.nt == 0) __builtin_amdgcn_endpgm();
+    const int NT = sp.nt;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        p.ws + sp.rec0 * REC_BYTES, (short)0, NT * REC_BYTES, BUF_DWORD3);
+    const uint32_t voff16 = lane * 16;
+    const uint32_t u_off = REC_U + slice * TPW * 512;
+    lds_u8* rl = (lds_u8*)ring;
+#pragma unroll
+    for (int d = 0; d < G::LEAD; ++d)
+        if (d < NT) issue_wide_chunk<G::NL>(rs, (uint32_t)d * REC_BYTES, rl + d * G::SLOT, u_off, voff16);
+    // chunk 0 before the first barrier
+    wide_wait_ladder<G::LEAD - 1, G::NL>(min(G::LEAD, NT) - 1);
+    copy_barrier();
+    for (int c = 0; c < NT; c += G::RING) wide_copy_round<TPW, 0>(rs, rl, c, NT, u_off, voff16);
+    __builtin_amdgcn_endpgm();
+}
+
+}  // namespace
+
+// Value tiles per work-group of the wide stage 2, or 0 for kda_k2.hip's one
+// tile per work-group: several tiles once (sequences x heads x 8 tiles)
+// exceed the CUs, as many as still leave about one work-group per CU.
+int k2_wide_tiles(const Params& p, int ncu) {
+    const int64_t nbh = (int64_t)(p.cu_seqlens ? p.N : p.B) * p.HV;
+    if (const char* e = getenv("KDA_BT16_K2_TILES")) {
+        const int t = atoi(e);
+        if (t == 1) return 0;
+        if (t == 2 || t == 4 || t == 8) return t;
+    }
+    if (nbh * 8 <= ncu) return 0;
+    if (nbh * 2 >= ncu) return 8;
+    return 4;
+}
+
+hipError_t launch_k2_wide(const Params& p, int tpw, hipStream_t stream) {
+    const int64_t nbh = (int64_t)(p.cu_seqlens ? p.N : p.B) * p.HV;
+    const int64_t nsl = 8 / tpw;
+    const int64_t padded = (nbh * nsl + 8 * nsl - 1) / (8 * nsl) * (8 * nsl);
+    switch (tpw) {
+        case 2:
+            hipLaunchKernelGGL(k2w_kernel<2>, dim3((unsigned)padded), dim3(WideGeom<2>::THREADS), 0,
+                               stream, p);
+            break;
+        case 4:
+            hipLaunchKernelGGL(k2w_kernel<4>, dim3((unsigned)padded), dim3(WideGeom<4>::THREADS), 0,
+                               stream, p);
+            break;
+        default:
+            hipLaunchKernelGGL(k2w_kernel<8>, dim3((unsigned)padded), dim3(WideGeom<8>::THREADS), 0,
+                               stream, p);
+            break;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace kda

@@ -17,8 +17,9 @@ CSRC = PKG_DIR.parent / "csrc"
 INCLUDE = PKG_DIR.parents[1] / "include"
 LIB_NAME = "libkda_bt16_hip.so"
 LIB_PATH = PKG_DIR / LIB_NAME
-SOURCES = ["kda_capi.hip", "kda_k1.hip", "kda_k2.hip", "kda_recurrent.hip", "kda_bwd.hip"]
-HEADERS = ["kda_common.h"]
+SOURCES = ["kda_capi.hip", "kda_k1.hip", "kda_k2.hip", "kda_k2w.hip", "kda_recurrent.hip",
+           "kda_bwd.hip"]
+HEADERS = ["kda_common.h", "kda_k2_shared.h"]
 
 ARCH = "gfx950"
 HIPCC_FLAGS = [

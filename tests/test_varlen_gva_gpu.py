@@ -215,7 +215,17 @@ MS_LENS = [0, 33, 16, 0, 0, 129, 1, 47, 0, 200, 15, 17, 0, 64, 3, 90, 31, 0, 48,
 @pytest.mark.parametrize("with_h0,with_ht,vfirst",
                          [(True, True, True), (False, True, True), (True, False, True),
                           (True, True, False)])
-def test_varlen_multi_sequence_work_groups(with_h0, with_ht, vfirst, gpu_device):
+@pytest.mark.parametrize("k2_tiles", ["1", None], ids=["one_tile_ms", "default"])
+def test_varlen_multi_sequence_work_groups(with_h0, with_ht, vfirst, k2_tiles, gpu_device,
+                                           monkeypatch):
+    """Several sequences per stage-2 work-group (KDA_BT16_K2_TILES=1 forces
+    the one-tile kernel, which then groups sequences) and the default, which
+    takes several value tiles per work-group here; each sequence equals its
+    own call."""
+    if k2_tiles is None:
+        monkeypatch.delenv("KDA_BT16_K2_TILES", raising=False)
+    else:
+        monkeypatch.setenv("KDA_BT16_K2_TILES", k2_tiles)
     cu_list = [0]
     for n in MS_LENS:
         cu_list.append(cu_list[-1] + n)
@@ -248,9 +258,15 @@ def test_varlen_multi_sequence_work_groups(with_h0, with_ht, vfirst, gpu_device)
             assert torch.equal(ht[n:n + 1], htn), f"sequence {n}: ht differs"
 
 
-def test_fixed_length_batch_multi_sequence_work_groups(gpu_device):
+@pytest.mark.parametrize("k2_tiles", ["1", None], ids=["one_tile_ms", "default"])
+def test_fixed_length_batch_multi_sequence_work_groups(k2_tiles, gpu_device, monkeypatch):
     """B = 8 rows of 300 tokens, HV = 8: 512 triples, so stage 2 takes two
-    or more rows per work-group; each row equals its own call."""
+    or more rows per work-group (KDA_BT16_K2_TILES=1), or several value
+    tiles per work-group (the default); each row equals its own call."""
+    if k2_tiles is None:
+        monkeypatch.delenv("KDA_BT16_K2_TILES", raising=False)
+    else:
+        monkeypatch.setenv("KDA_BT16_K2_TILES", k2_tiles)
     B, T, HV = 8, 300, 8
     c = _inputs(T, 2, HV, seed=73, B=B)
     d = _dev(c, gpu_device)
