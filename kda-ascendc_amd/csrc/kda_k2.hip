@@ -511,7 +511,8 @@ __device__ __forceinline__ void bwd_state_step(const Ctx& cx, f32x4 (&D)[8], Bwd
     uint8_t* hbuf = hc_buf[S % HANDOFF] + cx.lane * 16;
 #define KDA_FENCE() __builtin_amdgcn_sched_barrier(0)
     const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-    f32x4 dvn = mfma_bf16_16x16x16(as_i16x4(cur.aqkT), as_i16x4(cur.dop), zero);
+    // Aqk^T dO in the 16x16x32 shape of the chain it starts
+    f32x4 dvn = mfma_bf16_16x16x16_in_x32(cur.aqkT, cur.dop, zero);
     if (HAS_PREV) {
         bwd_update<0>(D, oth, bop);
         bwd_update<1>(D, oth, bop);
@@ -599,21 +600,10 @@ __device__ __forceinline__ void bwd_state_wave(const Params& p, const Ctx& cx, i
     read_bwd_ops(ring, lane, vt, op[0]);
     __builtin_amdgcn_s_waitcnt(WAITCNT_LGKM0);
     u32x4 bop;
-    bwd_state_step<0, false, true>(cx, D, op, bop);
-    if (cx.NT == 1) {
-        // A single step: its own update, after the first step's code (the
-        // operands it reads for a next step come from the ring's unused slot
-        // 1 and are dropped).  The dedicated single-step instantiation of
-        // bwd_state_step gave garbage gradients for every one-chunk
-        // sequence, while this order matches the fp64 gold.
-        bwd_update<0>(D, op[0], bop);
-        bwd_update<1>(D, op[0], bop);
-        bwd_update<2>(D, op[0], bop);
-        bwd_update<3>(D, op[0], bop);
-        bwd_update<4>(D, op[0], bop);
-        bwd_update<5>(D, op[0], bop);
-        bwd_update<6>(D, op[0], bop);
-        bwd_update<7>(D, op[0], bop);
+    if (cx.NT > 1) {
+        bwd_state_step<0, false, true>(cx, D, op, bop);
+    } else {
+        bwd_state_step<0, false, false>(cx, D, op, bop);
     }
     int c = 1;
     for (; c + RING < cx.NT; c += RING) bwd_round_full<1, RING>(cx, D, op, bop);

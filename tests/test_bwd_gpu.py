@@ -201,6 +201,36 @@ def test_bwd_single_chunk(gpu_device, T):
             assert _rel(out[n], gold[n]) < 1e-2, (T, h0, dht, n)
 
 
+@pytest.mark.parametrize("fill", [0x7F, 0xFF])
+def test_bwd_single_chunk_on_poisoned_workspace(gpu_device, monkeypatch, fill):
+    """One-chunk sequences (a full and a partial chunk; two heads; one and
+    two batch rows) on a workspace whose bytes all start as `fill` (0x7f: a
+    huge finite pattern, 0xff: NaN), each run twice: the same bits, finite,
+    and the fp64 gold.  The reverse chain's single step once accumulated a
+    16x16x32 MFMA onto a 16x16x16 one with no wait state between and read
+    two stale accumulator registers, whose values depend on what ran before
+    (the shapes are now never mixed in one chain, kda_common.h)."""
+    from kda_bt16 import workspace
+
+    def poisoned(device, nbytes):
+        return torch.full((max(256, (nbytes + 255) // 256 * 256),), fill, dtype=torch.uint8,
+                          device=device)
+
+    monkeypatch.setattr(workspace, "scratch", poisoned)
+    for B, T in ((1, 16), (2, 5)):
+        x = _inputs(B, T, 2, 2, seed=7 + T)
+        a = _hip_bwd(x, gpu_device)
+        b = _hip_bwd(x, gpu_device)
+        gold = autograd_grads(x["q"], x["k"], x["v"], x["g"].float(), x["beta"].float(),
+                              x["do"].float(), 0.1, A_log=x["A_log"], dt_bias=x["dt_bias"],
+                              initial_state=x["h0"], dht=x["dht"])
+        for n in GRADS:
+            assert torch.equal(a[n], b[n]), (B, T, n)
+            assert torch.isfinite(a[n]).all(), (B, T, n)
+        for n in ("dq", "dk", "dv", "dg", "dbeta", "dh0"):
+            assert _rel(a[n], gold[n]) < 1e-2, (B, T, n)
+
+
 def test_autograd_matches_explicit_backward(gpu_device):
     """kda_bt16_fwd and chunk_kda record an autograd node whose backward is
     kda_bt16_bwd: the same bits."""
