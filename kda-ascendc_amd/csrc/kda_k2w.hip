@@ -21,8 +21,8 @@
 //     accumulator tiles each, the layout of kda_k2.hip) and forms both
 //     v_new, both o and both state updates itself: no hand-off through LDS.
 //     The operands every tile shares (w, qg, kg, Aqk, the decay) are read
-//     from LDS once per wave for its two tiles, for the next chunk while
-//     this one is computed.
+//     from LDS once per wave for its two tiles, at the start of the chunk
+//     (behind the packing of hc, which needs only the state).
 // The waves meet at one barrier per chunk.
 #include <cstdlib>
 
