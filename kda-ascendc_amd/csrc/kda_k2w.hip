@@ -16,13 +16,14 @@
 // work-group takes TPW value tiles of one (sequence, head):
 //   * one copy wave streams each chunk's record once -- the shared 13 KiB
 //     and the TPW u slices -- into an LDS ring (direct buffer->LDS loads);
-//   * TPW / 2 compute waves each own two value tiles.  A compute wave keeps
-//     both tiles' state slices in registers (S^T as eight 16x16 fp32
-//     accumulator tiles each, the layout of kda_k2.hip) and forms both
-//     v_new, both o and both state updates itself: no hand-off through LDS.
-//     The operands every tile shares (w, qg, kg, Aqk, the decay) are read
-//     from LDS once per wave for its two tiles, at the start of the chunk
-//     (behind the packing of hc, which needs only the state).
+//   * TPW / TW compute waves each own TW (1 or 2) value tiles.  A compute
+//     wave keeps its tiles' state slices in registers (S^T as eight 16x16
+//     fp32 accumulator tiles each, the layout of kda_k2.hip) and forms their
+//     v_new, o and state updates itself: no hand-off through LDS.  The
+//     operands every tile shares (w, qg, kg, Aqk, the decay) are read from
+//     LDS once per wave, at the start of the chunk (behind the packing of
+//     hc, which needs only the state): with two tiles a wave reads them once
+//     for both, with one tile twice the waves issue the work.
 // The waves meet at one barrier per chunk.
 #include <cstdlib>
 
@@ -43,10 +44,11 @@ constexpr int SHARED_LOADS_W = REC_SHARED / 1024;  // 13
 // refilled with chunk j + RING during chunk j + RING - LEAD = j + 1, after
 // that read.  Direct loads count in the 6-bit vmcnt: LEAD chunks of loads
 // must fit in 63.
-template <int TPW>
+template <int TPW, int TW>
 struct WideGeom {
     static_assert(TPW == 2 || TPW == 4 || TPW == 8, "two, four or eight value tiles");
-    static constexpr int NCW = TPW / 2;                    // compute waves
+    static_assert(TW == 1 || TW == 2, "one or two value tiles per compute wave");
+    static constexpr int NCW = TPW / TW;                   // compute waves
     static constexpr int NL = SHARED_LOADS_W + TPW / 2;    // 1 KiB loads per chunk
     static constexpr int LEAD = 4 * NL <= 63 ? 4 : 3;
     static constexpr int RING = LEAD + 1;
@@ -171,15 +173,71 @@ __device__ __forceinline__ void wide_step(const WideCtx& cx, int c, f32x4 (&SA)[
     chunk_barrier();
 }
 
+// k-tile KT of a single tile's state update (TW = 1).
+template <int KT>
+__device__ __forceinline__ void wide1_update(f32x4 (&S)[8], const u32x4 (&kg)[4], f32x2 dc, u32x2 vn) {
+    const u32x4 k2 = kg[KT >> 1];
+    const i16x4 a = as_i16x4((KT & 1) ? u32x2{k2.z, k2.w} : u32x2{k2.x, k2.y});
+    S[KT] = mfma_bf16_16x16x16(a, as_i16x4(vn), decay_tile<KT>(S[KT], dc));
+}
+
+// One chunk of a compute wave that owns a single value tile (TW = 1): the
+// arithmetic of wide_step for one of its tiles.
+__device__ __forceinline__ void wide1_step(const WideCtx& cx, int c, f32x4 (&S)[8], const uint8_t* slot,
+                                           int ut) {
+    u32x4 w[4], qg[4], kg[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        w[j] = *reinterpret_cast<const u32x4*>(slot + REC_W + j * 1024 + cx.lane * 16);
+        qg[j] = *reinterpret_cast<const u32x4*>(slot + REC_QG + j * 1024 + cx.lane * 16);
+        kg[j] = *reinterpret_cast<const u32x4*>(slot + REC_KG + j * 1024 + cx.lane * 16);
+    }
+    const u32x2 aqk = *reinterpret_cast<const u32x2*>(slot + REC_AQK + cx.lane * 8);
+    const f32x2 dc = *reinterpret_cast<const f32x2*>(slot + decay_offset(cx.lane));
+    const u32x2 u = *reinterpret_cast<const u32x2*>(slot + REC_SHARED + ut * 512 + cx.lane * 8);
+    u32x4 hc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) hc[j] = pack_hc(S, j);
+    // v_new = u - w @ hc^T, one accumulation chain from u
+    f32x4 v = unpack_u(u);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v = mfma_bf16_16x16x32(as_bf16x8(w[j]), as_bf16x8(hc[j]), v);
+    // o = scale * qg @ hc^T + Aqk @ v_new
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    f32x4 o = zero;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o = mfma_bf16_16x16x32(as_bf16x8(qg[j]), as_bf16x8(hc[j]), o);
+    const u32x2 vn = {pack2(v[0], v[1]), pack2(v[2], v[3])};
+    o = o * cx.scale;
+    o = mfma_bf16_16x16x16(as_i16x4(aqk), as_i16x4(vn), o);
+    wide1_update<0>(S, kg, dc, vn);
+    wide1_update<1>(S, kg, dc, vn);
+    wide1_update<2>(S, kg, dc, vn);
+    wide1_update<3>(S, kg, dc, vn);
+    wide1_update<4>(S, kg, dc, vn);
+    wide1_update<5>(S, kg, dc, vn);
+    wide1_update<6>(S, kg, dc, vn);
+    wide1_update<7>(S, kg, dc, vn);
+    const int j4 = cx.lane & 3;
+    const u32x2 ot = quad_transpose(pack2(o[0], o[1]), pack2(o[2], o[3]), j4);
+    const int t = c * BT + 4 * cx.q4 + j4;
+    if (t < cx.T) *reinterpret_cast<u32x2*>(cx.obase[0] + (int64_t)t * cx.orow_stride) = ot;
+    chunk_barrier();
+}
+
 // Chunks c .. c + N - 1 (those below NT), with the ring slot of chunk c as
 // the compile-time S (every LDS offset a constant).
-template <int TPW, int S, int N>
+template <int TPW, int TW, int S, int N>
 __device__ __forceinline__ void wide_round(const WideCtx& cx, int c, f32x4 (&SA)[8], f32x4 (&SB)[8],
                                            const uint8_t* ring, int ut) {
-    using G = WideGeom<TPW>;
+    using G = WideGeom<TPW, TW>;
     if (c >= cx.NT) return;
-    wide_step(cx, c, SA, SB, ring + S * G::SLOT, ut);
-    if constexpr (N > 1) wide_round<TPW, (S + 1) % G::RING, N - 1>(cx, c + 1, SA, SB, ring, ut);
+    if constexpr (TW == 2) {
+        wide_step(cx, c, SA, SB, ring + S * G::SLOT, ut);
+    } else {
+        wide1_step(cx, c, SA, ring + S * G::SLOT, ut);
+    }
+    if constexpr (N > 1) wide_round<TPW, TW, (S + 1) % G::RING, N - 1>(cx, c + 1, SA, SB, ring, ut);
 }
 
 // Copy wave: the NL loads of one chunk, the shared part then this
@@ -210,10 +268,10 @@ __device__ __forceinline__ void wide_wait_ladder(int n_after) {
     }
 }
 
-template <int TPW, int S>
+template <int TPW, int TW, int S>
 __device__ __forceinline__ void wide_copy_round(__amdgpu_buffer_rsrc_t rs, lds_u8* ring, int c,
                                                 int NT, uint32_t u_off, uint32_t voff16) {
-    using G = WideGeom<TPW>;
+    using G = WideGeom<TPW, TW>;
     if (c >= NT) return;
     if (c + G::LEAD < NT)
         issue_wide_chunk<G::NL>(rs, (uint32_t)(c + G::LEAD) * REC_BYTES,
@@ -221,15 +279,15 @@ __device__ __forceinline__ void wide_copy_round(__amdgpu_buffer_rsrc_t rs, lds_u
     // chunk c + 1 is read by the compute waves after this barrier
     if (c + 1 < NT) wide_wait_ladder<G::LEAD - 1, G::NL>(min(G::LEAD - 1, NT - 2 - c));
     copy_barrier();
-    if constexpr (S + 1 < G::RING) wide_copy_round<TPW, S + 1>(rs, ring, c + 1, NT, u_off, voff16);
+    if constexpr (S + 1 < G::RING) wide_copy_round<TPW, TW, S + 1>(rs, ring, c + 1, NT, u_off, voff16);
 }
 
 // Work-group (sequence, value head, slice of TPW value tiles): grid padded
 // to a multiple of 8 * (8 / TPW) and mapped XCD-aware, so that the slices
 // of one (sequence, head) share an XCD and its L2 for the records.
-template <int TPW>
-__global__ __launch_bounds__(WideGeom<TPW>::THREADS) void k2w_kernel(Params p) {
-    using G = WideGeom<TPW>;
+template <int TPW, int TW>
+__global__ __launch_bounds__((WideGeom<TPW, TW>::THREADS)) void k2w_kernel(Params p) {
+    using G = WideGeom<TPW, TW>;
     __shared__ __attribute__((aligned(1024))) uint8_t ring[G::RING * G::SLOT];
     constexpr int NSL = 8 / TPW;
     const int lane = threadIdx.x & 63;
@@ -247,16 +305,16 @@ __global__ __launch_bounds__(WideGeom<TPW>::THREADS) void k2w_kernel(Params p) {
     const int64_t sbase = (int64_t)bh * DK * DK;
 
     if (wave < G::NCW) {
-        const int ut = 2 * wave;               // first of this wave's two tiles in the slice
+        const int ut = TW * wave;              // first of this wave's tiles in the slice
         const int vt = slice * TPW + ut;       // its value tile
         const int q4 = lane >> 4;
         const int va = 16 * vt + (lane & 15);  // this lane's state row (V index) of tile A
         f32x4 SA[8], SB[8];
         load_state(p, sbase, va, q4, SA);
-        load_state(p, sbase, va + 16, q4, SB);
+        if (TW == 2) load_state(p, sbase, va + 16, q4, SB);
         if (sp.nt == 0) {  // an empty sequence: the final state is the initial state
             store_state(p, sbase, va, q4, SA);
-            store_state(p, sbase, va + 16, q4, SB);
+            if (TW == 2) store_state(p, sbase, va + 16, q4, SB);
             __builtin_amdgcn_endpgm();
         }
         WideCtx cx;
@@ -270,9 +328,9 @@ __global__ __launch_bounds__(WideGeom<TPW>::THREADS) void k2w_kernel(Params p) {
         cx.obase[1] = cx.obase[0] + 16;
         cx.orow_stride = (int64_t)p.HV * DK;
         chunk_barrier();  // chunk 0 is in the ring
-        for (int c = 0; c < cx.NT; c += G::RING) wide_round<TPW, 0, G::RING>(cx, c, SA, SB, ring, ut);
+        for (int c = 0; c < cx.NT; c += G::RING) wide_round<TPW, TW, 0, G::RING>(cx, c, SA, SB, ring, ut);
         store_state(p, sbase, va, q4, SA);
-        store_state(p, sbase, va + 16, q4, SB);
+        if (TW == 2) store_state(p, sbase, va + 16, q4, SB);
         __builtin_amdgcn_endpgm();
     }
     // copy wave
@@ -289,7 +347,7 @@ __global__ __launch_bounds__(WideGeom<TPW>::THREADS) void k2w_kernel(Params p) {
     // chunk 0 before the first barrier
     wide_wait_ladder<G::LEAD - 1, G::NL>(min(G::LEAD, NT) - 1);
     copy_barrier();
-    for (int c = 0; c < NT; c += G::RING) wide_copy_round<TPW, 0>(rs, rl, c, NT, u_off, voff16);
+    for (int c = 0; c < NT; c += G::RING) wide_copy_round<TPW, TW, 0>(rs, rl, c, NT, u_off, voff16);
     __builtin_amdgcn_endpgm();
 }
 
@@ -310,23 +368,31 @@ int k2_wide_tiles(const Params& p, int ncu) {
     return 4;
 }
 
+namespace {
+template <int TPW, int TW>
+void launch_w(const Params& p, int64_t grid, hipStream_t stream) {
+    hipLaunchKernelGGL((k2w_kernel<TPW, TW>), dim3((unsigned)grid), dim3(WideGeom<TPW, TW>::THREADS), 0,
+                       stream, p);
+}
+}  // namespace
+
 hipError_t launch_k2_wide(const Params& p, int tpw, hipStream_t stream) {
     const int64_t nbh = (int64_t)(p.cu_seqlens ? p.N : p.B) * p.HV;
     const int64_t nsl = 8 / tpw;
     const int64_t padded = (nbh * nsl + 8 * nsl - 1) / (8 * nsl) * (8 * nsl);
-    switch (tpw) {
-        case 2:
-            hipLaunchKernelGGL(k2w_kernel<2>, dim3((unsigned)padded), dim3(WideGeom<2>::THREADS), 0,
-                               stream, p);
-            break;
-        case 4:
-            hipLaunchKernelGGL(k2w_kernel<4>, dim3((unsigned)padded), dim3(WideGeom<4>::THREADS), 0,
-                               stream, p);
-            break;
-        default:
-            hipLaunchKernelGGL(k2w_kernel<8>, dim3((unsigned)padded), dim3(WideGeom<8>::THREADS), 0,
-                               stream, p);
-            break;
+    // One tile per compute wave issues the work of 2 or 4 tiles from twice
+    // the waves (B=1 T=8192 H=96, 4 tiles: stage 2 284 against 354 us);
+    // with 8 tiles, 9 waves gained nothing over 5 (B=16 T=2048 H=32: 317 us
+    // both), so two tiles per wave there.
+    int tw = tpw == 8 ? 2 : 1;
+    if (const char* e = getenv("KDA_BT16_K2_WAVE_TILES")) tw = atoi(e) == 1 ? 1 : 2;
+    switch (tpw * 4 + tw) {
+        case 2 * 4 + 1: launch_w<2, 1>(p, padded, stream); break;
+        case 4 * 4 + 1: launch_w<4, 1>(p, padded, stream); break;
+        case 8 * 4 + 1: launch_w<8, 1>(p, padded, stream); break;
+        case 2 * 4 + 2: launch_w<2, 2>(p, padded, stream); break;
+        case 4 * 4 + 2: launch_w<4, 2>(p, padded, stream); break;
+        default: launch_w<8, 2>(p, padded, stream); break;
     }
     return hipGetLastError();
 }

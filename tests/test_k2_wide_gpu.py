@@ -5,7 +5,9 @@ only the division of the work differs.
 
 ``KDA_BT16_K2_TILES`` forces the tiles per work-group (1: kda_k2.hip; 2, 4,
 8: kda_k2w.hip) over the launch heuristic, which picks several tiles only
-when (sequences x heads x 8) exceeds the CU count.
+when (sequences x heads x 8) exceeds the CU count, and
+``KDA_BT16_K2_WAVE_TILES`` the tiles per compute wave of kda_k2w.hip (1 or
+2).
 """
 
 from __future__ import annotations
@@ -20,6 +22,7 @@ from kda_bt16 import kda_bt16_fwd
 pytestmark = pytest.mark.gpu
 
 ENV = "KDA_BT16_K2_TILES"
+ENV_WAVE = "KDA_BT16_K2_WAVE_TILES"
 
 # name, B, T, H, HV, cu_seqlens, state_v_first, h0
 CASES = [
@@ -48,9 +51,13 @@ def _inputs(B, T, H, HV, S, seed):
     )
 
 
-def _run(c, dev, cu, svf, h0, tiles):
-    old = os.environ.get(ENV)
+def _run(c, dev, cu, svf, h0, tiles, wave_tiles=None):
+    old = {e: os.environ.get(e) for e in (ENV, ENV_WAVE)}
     os.environ[ENV] = str(tiles)
+    if wave_tiles is None:
+        os.environ.pop(ENV_WAVE, None)
+    else:
+        os.environ[ENV_WAVE] = str(wave_tiles)
     try:
         init = None
         if h0:
@@ -65,10 +72,11 @@ def _run(c, dev, cu, svf, h0, tiles):
         torch.cuda.synchronize()
         return o, ht
     finally:
-        if old is None:
-            os.environ.pop(ENV, None)
-        else:
-            os.environ[ENV] = old
+        for e, v in old.items():
+            if v is None:
+                os.environ.pop(e, None)
+            else:
+                os.environ[e] = v
 
 
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
@@ -80,9 +88,11 @@ def test_wide_stage2_equals_one_tile_stage2(case, gpu_device):
     o1, ht1 = _run(c, gpu_device, cu, svf, h0, 1)
     assert torch.isfinite(o1.float()).all() and torch.isfinite(ht1).all()
     for tiles in (2, 4, 8):
-        o, ht = _run(c, gpu_device, cu, svf, h0, tiles)
-        assert torch.equal(o.view(torch.int16), o1.view(torch.int16)), f"{name}: o, {tiles} tiles"
-        assert torch.equal(ht.view(torch.int32), ht1.view(torch.int32)), f"{name}: ht, {tiles} tiles"
+        for wt in (1, 2):
+            o, ht = _run(c, gpu_device, cu, svf, h0, tiles, wt)
+            what = f"{name}: {tiles} tiles, {wt} per wave"
+            assert torch.equal(o.view(torch.int16), o1.view(torch.int16)), f"{what}: o"
+            assert torch.equal(ht.view(torch.int32), ht1.view(torch.int32)), f"{what}: ht"
 
 
 def test_heuristic_takes_the_wide_kernel_for_many_heads(gpu_device):
