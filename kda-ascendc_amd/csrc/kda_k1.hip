@@ -78,10 +78,16 @@ __device__ __forceinline__ u32x2 pack4(f32x4 v) { return pack4(v.x, v.y, v.z, v.
 // and the gram block to p.la.  Those modes run two waves per SIMD: they
 // hold more.
 // LDS of a work-group (one wave): the transpose tile, L and the solve's
-// columns.
+// columns.  k1_chunk takes its scratch as pointers, so that several waves
+// of one work-group can each have their own (the fused forward).
 __shared__ __attribute__((aligned(16))) uint16_t s_T[BT * LROW];
 __shared__ __attribute__((aligned(16))) float s_L[BT * BT];
 __shared__ float s_X[BT * (BT + 1)];
+
+// The wave's own LDS writes are complete before its next LDS read: the
+// scratch of k1_chunk belongs to one wave, so no work-group barrier is
+// needed between its phases.
+__device__ __forceinline__ void wave_lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 // One chunk (value head hv, chunk c of sequence sp).  FULL: all 16 rows
 // are tokens (every chunk but a sequence's partial last one), so the
@@ -96,7 +102,8 @@ __shared__ float s_X[BT * (BT + 1)];
 enum K1Mode { K1_FWD = 0, K1_BOTH = 1, K1_SAVE = 2 };
 
 template <int K1M, bool FULL, bool GB16>
-__device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const SeqSpan& sp) {
+__device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const SeqSpan& sp, uint16_t* sT,
+                                         float* sL, float* sX, uint8_t* rec) {
     constexpr bool BOTH = K1M != K1_FWD;
     constexpr bool WITH_DO = K1M == K1_BOTH;
     const int lane = threadIdx.x;
@@ -230,11 +237,11 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
         }
     });
 
-    // This chunk's record, written with ordinary stores: the grid runs the
-    // chunks last to first (k1_kernel), so the records stage 2 reads first
-    // are the ones written last, still in L2 and the infinity cache.  (The
-    // backward record below is streamed out with non-temporal stores.)
-    uint8_t* rec = p.ws + (sp.rec0 + c) * REC_BYTES;
+    // This chunk's record goes to `rec` with ordinary stores: in the
+    // workspace, the grid runs the chunks last to first (k1_kernel), so the
+    // records stage 2 reads first are the ones written last, still in L2 and
+    // the infinity cache; in the fused forward, `rec` is a ring slot in LDS.
+    // (The backward record below is streamed out with non-temporal stores.)
 
     f32x4 aqk, L;
 #pragma unroll
@@ -249,8 +256,8 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
     // ---- (I + L)^-1 by forward substitution (kernels.py:157-167) ---------
     // Lane r solves column s = r: a[t] = A_inv[t][s], with a[s] = 1,
     // a[t < s] = 0 and a[t > s] = -sum_{j<t} L[t][j] a[j].
-    *reinterpret_cast<f32x4*>(s_L + r * BT + 4 * q4) = L;
-    __syncthreads();
+    *reinterpret_cast<f32x4*>(sL + r * BT + 4 * q4) = L;
+    wave_lds_fence();
     {
         float a[BT];
 #pragma unroll
@@ -258,7 +265,7 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
             float acc = 0.f;
 #pragma unroll
             for (int j4 = 0; j4 < (t + 3) / 4; ++j4) {
-                const f32x4 lr = *reinterpret_cast<const f32x4*>(s_L + t * BT + 4 * j4);
+                const f32x4 lr = *reinterpret_cast<const f32x4*>(sL + t * BT + 4 * j4);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     if (4 * j4 + i < t) acc = fmaf(-lr[i], a[4 * j4 + i], acc);
@@ -268,13 +275,13 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
         }
         if (q4 == 0) {
 #pragma unroll
-            for (int t = 0; t < BT; ++t) s_X[r * (BT + 1) + t] = a[t];
+            for (int t = 0; t < BT; ++t) sX[r * (BT + 1) + t] = a[t];
         }
     }
-    __syncthreads();
+    wave_lds_fence();
     f32x4 ainv;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ainv[i] = s_X[(4 * q4 + i) * (BT + 1) + r];
+    for (int i = 0; i < 4; ++i) ainv[i] = sX[(4 * q4 + i) * (BT + 1) + r];
     const u32x2 ainv_bf = pack4(ainv);  // A = bf16(A_inv), kernels.py:170
     if constexpr (BOTH) {
         // the gram and the inverse for the per-chunk gradients (kda_common.h)
@@ -289,13 +296,13 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
         // ---- backward record ---------------------------------------------
         uint8_t* brec = p.ws_bwd + (sp.rec0 + c) * REC_BYTES;
         // Aqk^T as an A operand: lane (r, q4) takes Aqk[4*q4 + i][r], the
-        // transpose of what it holds, through s_L (free after the solve).
-        *reinterpret_cast<f32x4*>(s_L + r * BT + 4 * q4) = aqk;
-        __syncthreads();
+        // transpose of what it holds, through sL (free after the solve).
+        *reinterpret_cast<f32x4*>(sL + r * BT + 4 * q4) = aqk;
+        wave_lds_fence();
         {
             f32x4 at;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) at[i] = s_L[(4 * q4 + i) * BT + r];
+            for (int i = 0; i < 4; ++i) at[i] = sL[(4 * q4 + i) * BT + r];
             __builtin_nontemporal_store(pack4(at),
                                         reinterpret_cast<u32x2*>(brec + BREC_AQKT + lane * 8));
         }
@@ -312,26 +319,26 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
                 kb[i] = round_bf(elem(kp, 4 * kt + i) * beta) * e;
                 qs[i] = p.scale * (elem(qp, 4 * kt + i) * e);
             }
-            lds_put(s_T, r, colbase, kt, pack4(kb[0], kb[1], kb[2], kb[3]));
+            lds_put(sT, r, colbase, kt, pack4(kb[0], kb[1], kb[2], kb[3]));
             qsF[kt] = pack4(qs[0], qs[1], qs[2], qs[3]);
         }
-        __syncthreads();
+        wave_lds_fence();
         {
             i16x4 kbT[8];
-            load_lds_T(s_T, r, q4, kbT);
+            load_lds_T(sT, r, q4, kbT);
 #pragma unroll
             for (int kt = 0; kt < 8; ++kt) {
                 const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
                 wT[kt] = pack4(mfma_bf16_16x16x16(A_neg, kbT[kt], zero));
             }
         }
-        __syncthreads();
+        wave_lds_fence();
 #pragma unroll
-        for (int kt = 0; kt < 8; ++kt) lds_put(s_T, r, colbase, kt, qsF[kt]);
-        __syncthreads();
+        for (int kt = 0; kt < 8; ++kt) lds_put(sT, r, colbase, kt, qsF[kt]);
+        wave_lds_fence();
         {
             i16x4 qsT[8];
-            load_lds_T(s_T, r, q4, qsT);
+            load_lds_T(sT, r, q4, qsT);
 #pragma unroll
             for (int kt = 0; kt < 8; ++kt) {
                 const u32x2 qv = __builtin_bit_cast(u32x2, qsT[kt]);
@@ -343,12 +350,12 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
         // dO as the B operand of each value tile (T order, the layout of u
         // in the forward record): [vt][lane][i] = dO[4*q4 + i][16*vt + r].
         if constexpr (WITH_DO) {
-            __syncthreads();
+            wave_lds_fence();
 #pragma unroll
-            for (int kt = 0; kt < 8; ++kt) lds_put(s_T, r, colbase, kt, dop.v[kt]);
-            __syncthreads();
+            for (int kt = 0; kt < 8; ++kt) lds_put(sT, r, colbase, kt, dop.v[kt]);
+            wave_lds_fence();
             i16x4 doT[8];
-            load_lds_T(s_T, r, q4, doT);
+            load_lds_T(sT, r, q4, doT);
 #pragma unroll
             for (int vt = 0; vt < 8; ++vt)
                 __builtin_nontemporal_store(__builtin_bit_cast(u32x2, doT[vt]),
@@ -378,7 +385,7 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
             __builtin_nontemporal_store(
                 u32x4{kgF[2 * j].x, kgF[2 * j].y, kgF[2 * j + 1].x, kgF[2 * j + 1].y},
                 reinterpret_cast<u32x4*>(brec + BREC_KG + j * 1024 + lane * 16));
-        __syncthreads();
+        wave_lds_fence();
     }
 
     // ---- u = A @ bf16(v * beta) (kernels.py:173-174) ----------------------
@@ -386,13 +393,13 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
     // u[4*q4 + i][16*vt + r], the order stage 2 subtracts it in.
 #pragma unroll
     for (int kt = 0; kt < 8; ++kt)
-        lds_put(s_T, r, colbase, kt,
+        lds_put(sT, r, colbase, kt,
                 pack4(elem(vp, 4 * kt) * beta, elem(vp, 4 * kt + 1) * beta,
                       elem(vp, 4 * kt + 2) * beta, elem(vp, 4 * kt + 3) * beta));
-    __syncthreads();
+    wave_lds_fence();
     {
         i16x4 vbT[8];
-        load_lds_T(s_T, r, q4, vbT);
+        load_lds_T(sT, r, q4, vbT);
 #pragma unroll
         for (int vt = 0; vt < 8; ++vt) {
             const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
@@ -411,7 +418,7 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
             }
         }
     }
-    __syncthreads();
+    wave_lds_fence();
 
     // ---- w = A @ bf16(bf16(k^ * beta) * 2^G) (kernels.py:171-172), and
     // qg = bf16(q^ * 2^G), the gated query stage 2 multiplies the state by
@@ -427,7 +434,7 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
             kb[i] = round_bf(elem(kp, 4 * kt + i) * beta) * e;
             qg[i] = elem(qp, 4 * kt + i) * e;
         }
-        lds_put(s_T, r, colbase, kt, pack4(kb[0], kb[1], kb[2], kb[3]));
+        lds_put(sT, r, colbase, kt, pack4(kb[0], kb[1], kb[2], kb[3]));
         qgp[kt] = pack4(qg[0], qg[1], qg[2], qg[3]);
     }
     // (the backward's recompute produces no o and never reads qg)
@@ -438,14 +445,14 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
             *reinterpret_cast<u32x4*>(rec + REC_QG + j * 1024 + lane * 16) = qgj;
         }
     }
-    __syncthreads();
+    wave_lds_fence();
     // The record holds -w (stage 2 forms u - w @ hc^T as one accumulation
     // that starts at u): the product with -A, exact since negation commutes
     // with the bf16 products, the fp32 sums and the rounding.
     u32x2 wpk[8];
     {
         i16x4 kbT[8];
-        load_lds_T(s_T, r, q4, kbT);
+        load_lds_T(sT, r, q4, kbT);
 #pragma unroll
         for (int kt = 0; kt < 8; ++kt) {
             const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
@@ -457,7 +464,7 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
         const u32x4 wj = {wpk[2 * j].x, wpk[2 * j].y, wpk[2 * j + 1].x, wpk[2 * j + 1].y};
         *reinterpret_cast<u32x4*>(rec + REC_W + j * 1024 + lane * 16) = wj;
     }
-    __syncthreads();
+    wave_lds_fence();
 
     // ---- kg = bf16(k^ * 2^(G_last - G)) and the decay 2^G_last of the state
     // (kernels.py:282-290), kg stored in T order (stage 2's A operand).
@@ -470,16 +477,16 @@ __device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const S
                 gl[i] = from_last(G[4 * kt + i]);
                 kg[i] = elem(kp, 4 * kt + i) * fast_exp2(gl[i] - G[4 * kt + i]);
             }
-            lds_put(s_T, r, colbase, kt, pack4(kg[0], kg[1], kg[2], kg[3]));
+            lds_put(sT, r, colbase, kt, pack4(kg[0], kg[1], kg[2], kg[3]));
             if (r == 0)
                 *reinterpret_cast<f32x4*>(rec + REC_DECAY + kt * 64 + q4 * 16) =
                     f32x4{fast_exp2(gl[0]), fast_exp2(gl[1]), fast_exp2(gl[2]), fast_exp2(gl[3])};
         }
     });
-    __syncthreads();
+    wave_lds_fence();
     {
         i16x4 kgT[8];
-        load_lds_T(s_T, r, q4, kgT);
+        load_lds_T(sT, r, q4, kgT);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const u32x2 a = __builtin_bit_cast(u32x2, kgT[2 * j]);
@@ -536,7 +543,7 @@ __attribute__((amdgpu_waves_per_eu(K1M != K1_FWD ? 2 : 3))) void k1_kernel(Param
     int hv, c;
     SeqSpan sp;
     if (!block_chunk(p, threadIdx.x, hv, c, sp)) return;
-    k1_chunk<K1M, ALL_FULL, GB16>(p, hv, c, sp);
+    k1_chunk<K1M, ALL_FULL, GB16>(p, hv, c, sp, s_T, s_L, s_X, p.ws + (sp.rec0 + c) * REC_BYTES);
 }
 
 // The dO operand of each backward record that a training forward saved
