@@ -335,9 +335,7 @@ int kda_bt16_fwd_hip(const KdaBt16Args* args, void* stream) {
     Params p;
     int rc = to_params(args, p, true, true);
     if (rc != KDA_BT16_OK) return rc;
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    if (kda::launch_k1(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
-    if (kda::launch_k2(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
+    if (kda::launch_fwd(p, static_cast<hipStream_t>(stream)) != hipSuccess) return KDA_BT16_ELAUNCH;
     return KDA_BT16_OK;
 }
 
@@ -349,9 +347,7 @@ int kda_bt16_fwd_noalloc_hip(const KdaBt16Args* args, void* stream) {
         return KDA_BT16_ESCRATCH;
     rc = scratch_ptr(&p.ws);
     if (rc != KDA_BT16_OK) return rc;
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    if (kda::launch_k1(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
-    if (kda::launch_k2(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
+    if (kda::launch_fwd(p, static_cast<hipStream_t>(stream)) != hipSuccess) return KDA_BT16_ELAUNCH;
     return KDA_BT16_OK;
 }
 

@@ -375,6 +375,12 @@ hipError_t launch_k2(const Params& p, hipStream_t stream);
 // and the launch with `tpw` tiles (2, 4 or 8).
 int k2_wide_tiles(const Params& p, int ncu);
 hipError_t launch_k2_wide(const Params& p, int tpw, hipStream_t stream);
+// The forward as one kernel (kda_fused.hip): whether it is taken for a
+// geometry on `ncu` CUs, and its launch.
+bool fused_forward(const Params& p, int ncu);
+hipError_t launch_fused(const Params& p, hipStream_t stream);
+// The forward: fused, or stage 1 then stage 2 (kda_k2.hip).
+hipError_t launch_fwd(const Params& p, hipStream_t stream);
 hipError_t launch_recurrent(const Params& p, hipStream_t stream);
 // Backward (kda_bt16_bwd.hip, and the training variants of the stages).
 hipError_t launch_k1_both_records(const Params& p, hipStream_t stream);

@@ -1012,6 +1012,12 @@ hipError_t launch_k2(const Params& p, hipStream_t stream) {
     return hipGetLastError();
 }
 
+hipError_t launch_fwd(const Params& p, hipStream_t stream) {
+    if (fused_forward(p, cu_count())) return launch_fused(p, stream);
+    const hipError_t e = launch_k1(p, stream);
+    return e != hipSuccess ? e : launch_k2(p, stream);
+}
+
 hipError_t launch_k2_train(const Params& p, hipStream_t stream) {
     const int64_t grid = (int64_t)(p.cu_seqlens ? p.N : p.B) * p.HV * 8;
     hipLaunchKernelGGL(k2_kernel<K2_TRAIN>, dim3((unsigned)grid), dim3(256), 0, stream, p);

@@ -17,9 +17,9 @@ CSRC = PKG_DIR.parent / "csrc"
 INCLUDE = PKG_DIR.parents[1] / "include"
 LIB_NAME = "libkda_bt16_hip.so"
 LIB_PATH = PKG_DIR / LIB_NAME
-SOURCES = ["kda_capi.hip", "kda_k1.hip", "kda_k2.hip", "kda_k2w.hip", "kda_recurrent.hip",
-           "kda_bwd.hip"]
-HEADERS = ["kda_common.h", "kda_k2_shared.h"]
+SOURCES = ["kda_capi.hip", "kda_k1.hip", "kda_k2.hip", "kda_k2w.hip", "kda_fused.hip",
+           "kda_recurrent.hip", "kda_bwd.hip"]
+HEADERS = ["kda_common.h", "kda_k2_shared.h", "kda_k1_chunk.h", "kda_k2w_step.h"]
 
 ARCH = "gfx950"
 HIPCC_FLAGS = [

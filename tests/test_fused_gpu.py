@@ -1,0 +1,118 @@
+"""The fused forward (csrc/kda_fused.hip) against the two-stage forward
+(csrc/kda_k1.hip, then csrc/kda_k2.hip or csrc/kda_k2w.hip), bit for bit:
+the fused kernel runs stage 1's per-chunk code and the wide stage 2's step
+(kernels.py:53-302) on records kept in LDS instead of HBM, so only where the
+record lives differs.
+
+``KDA_BT16_FUSED`` forces the choice over the launch heuristic (0: two
+stages; 1: fused), which fuses when the (sequence, head) pairs are at least
+as many as the CUs.  The cases cover what the record ring has edges at:
+fewer chunks than ring slots, counts that are and are not multiples of the
+ring and of the producer count, partial last chunks, empty sequences in a
+varlen batch, grouped value heads, both state layouts, fp32 and bf16 gates,
+and the precomputed-gate mode.
+"""
+
+from __future__ import annotations
+
+import os
+
+import pytest
+import torch
+
+from kda_bt16 import kda_bt16_fwd
+
+pytestmark = pytest.mark.gpu
+
+ENV = "KDA_BT16_FUSED"
+
+# name, B, T, H, HV, cu_seqlens, state_v_first, h0, g dtype, in-kernel gate
+CASES = [
+    ("one_token", 1, 1, 1, 1, None, True, True, "bf16", True),
+    ("one_chunk", 1, 16, 1, 2, None, True, True, "bf16", True),
+    ("five_chunks", 2, 80, 1, 1, None, True, False, "bf16", True),
+    ("six_chunks", 1, 96, 2, 2, None, False, True, "bf16", True),
+    ("seven_chunks_partial", 1, 100, 1, 1, None, True, True, "fp32", True),
+    ("partial_T300", 1, 300, 2, 2, None, True, False, "bf16", True),
+    ("gva_kfirst_T1037", 2, 1037, 2, 4, None, False, True, "bf16", True),
+    ("long_T2500_fp32g", 1, 2500, 1, 1, None, True, True, "fp32", True),
+    ("precomputed_gate", 2, 333, 2, 2, None, True, True, "fp32", False),
+    ("varlen_empty", 1, 400, 2, 2, [0, 0, 37, 53, 53, 120, 400], True, True, "bf16", True),
+    ("varlen_kfirst", 1, 700, 1, 2, [0, 17, 300, 301, 700], False, True, "bf16", True),
+    ("batch16_H32", 16, 160, 32, 32, None, True, True, "bf16", True),
+]
+
+
+def _inputs(B, T, H, HV, S, seed, gdt, in_kernel_gate):
+    gen = torch.Generator().manual_seed(seed)
+    if in_kernel_gate:
+        g = torch.randn(B, T, HV, 128, generator=gen)
+    else:
+        # chunk-local log2 cumsum of a decay in (-1, 0) per token
+        g = -torch.rand(B, T, HV, 128, generator=gen)
+        pos = torch.arange(T) % 16
+        g = torch.stack([g[:, t - int(pos[t]):t + 1].sum(1) for t in range(T)], 1)
+    return dict(
+        q=torch.randn(B, T, H, 128, generator=gen).bfloat16(),
+        k=torch.randn(B, T, H, 128, generator=gen).bfloat16(),
+        v=torch.randn(B, T, HV, 128, generator=gen).bfloat16(),
+        g=g.bfloat16() if gdt == "bf16" else g.float(),
+        beta=torch.randn(B, T, HV, generator=gen).bfloat16(),
+        A_log=torch.log(torch.rand(HV, generator=gen) * 15 + 1),
+        dt_bias=torch.randn(HV * 128, generator=gen) * 0.1,
+        h0=torch.randn(S, HV, 128, 128, generator=gen) * 0.05,
+    )
+
+
+def _run(c, dev, cu, svf, h0, gate, fused):
+    old = os.environ.get(ENV)
+    if fused is None:
+        os.environ.pop(ENV, None)
+    else:
+        os.environ[ENV] = str(fused)
+    try:
+        init = None
+        if h0:
+            init = c["h0"] if svf else c["h0"].transpose(-1, -2).contiguous()
+            init = init.to(dev)
+        o, ht = kda_bt16_fwd(
+            *(c[x].to(dev) for x in ("q", "k", "v", "g", "beta")), scale=0.1,
+            initial_state=init, output_final_state=True, use_qk_l2norm_in_kernel=True,
+            use_gate_in_kernel=gate, use_beta_sigmoid_in_kernel=True, lower_bound=-5.0,
+            A_log=c["A_log"].to(dev) if gate else None,
+            dt_bias=c["dt_bias"].to(dev) if gate else None, state_v_first=svf,
+            cu_seqlens=None if cu is None else torch.tensor(cu, dtype=torch.int32, device=dev))
+        torch.cuda.synchronize()
+        return o, ht
+    finally:
+        if old is None:
+            os.environ.pop(ENV, None)
+        else:
+            os.environ[ENV] = old
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_fused_forward_equals_two_stage(case, gpu_device):
+    name, B, T, H, HV, cu, svf, h0, gdt, gate = case
+    S = B if cu is None else len(cu) - 1
+    c = _inputs(B, T, H, HV, S, seed=sum(map(ord, name)), gdt=gdt, in_kernel_gate=gate)
+    print(f"[fused] {name}", flush=True)
+    o2, ht2 = _run(c, gpu_device, cu, svf, h0, gate, 0)
+    assert torch.isfinite(o2.float()).all() and torch.isfinite(ht2).all()
+    o1, ht1 = _run(c, gpu_device, cu, svf, h0, gate, 1)
+    assert torch.equal(o1.view(torch.int16), o2.view(torch.int16)), f"{name}: o"
+    assert torch.equal(ht1.view(torch.int32), ht2.view(torch.int32)), f"{name}: ht"
+    # a second call on the same inputs gives the same bits (no state kept
+    # between calls in the LDS ring or its flags)
+    o3, ht3 = _run(c, gpu_device, cu, svf, h0, gate, 1)
+    assert torch.equal(o3.view(torch.int16), o1.view(torch.int16)), f"{name}: o, second call"
+    assert torch.equal(ht3.view(torch.int32), ht1.view(torch.int32)), f"{name}: ht, second call"
+
+
+def test_heuristic_fuses_when_pairs_fill_the_cus(gpu_device):
+    """B=16 T=64 H=32 (512 (sequence, head) pairs) runs fused by default and
+    gives the two-stage result."""
+    c = _inputs(16, 64, 32, 32, 16, seed=5, gdt="bf16", in_kernel_gate=True)
+    o2, ht2 = _run(c, gpu_device, None, True, True, True, 0)
+    o, ht = _run(c, gpu_device, None, True, True, True, None)
+    assert torch.equal(o, o2) and torch.equal(ht, ht2)
