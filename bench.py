@@ -24,7 +24,7 @@ headline metric):
   --workload train    one training step of the op (forward, then the
                       backward through autograd) at the headline shape;
   --workload varlen   the same 8192 tokens and 32 heads as 16 packed
-                      sequences of uneven lengths (cu_seqlens), both stages;
+                      sequences of uneven lengths (cu_seqlens);
   --workload decode   one decode step (T = 1, state updated in place) for
                       B = 128 sequences of 32 heads: the token recurrence,
                       bound by reading and writing the fp32 states.
@@ -288,8 +288,25 @@ def run_varlen(args, dev, inputs_cpu) -> dict:
     lens = [b - a for a, b in zip(offs[:-1], offs[1:])]
     n_chunks = sum(math.ceil(n / 16) for n in lens)
     by = algorithmic_bytes(VARLEN_N)
-    kern, dom = _kernel_roofline(k1_ms, k2_ms, wall_ms, by, matmul_flops(n_chunks))
+    fl = matmul_flops(n_chunks)
+    kern, dom = _kernel_roofline(k1_ms, k2_ms, wall_ms, by, fl)
+    fused = k1.forward_plan == "fused"
+    stage_ms = None
+    if fused:
+        stage_ms = {n: round(d["ms"], 4) for n, d in kern.items()}
+        kern = {"fused": {"ms": fwd_ms, "alg_bytes": sum(by), "alg_gbs": sum(by) / fwd_ms / 1e6,
+                          "tflops": sum(fl) / fwd_ms / 1e9}}
+        dom = "fused"
     achieved = sum(by) / fwd_ms / 1e6
+    traffic = None
+    try:
+        t = json.loads((ROOT / "profiles" / "kda_varlen_T8192_N16_H32_traffic.json").read_text())
+        names = ("fused",) if fused else ("k1", "k2")
+        traffic = int(round(sum((t["kernels"][n]["FETCH_SIZE_KiB"] * t["fetch_scale"]
+                                 + t["kernels"][n]["WRITE_SIZE_KiB"] * t["write_scale"]) * 1024
+                                for n in names)))
+    except (OSError, ValueError, KeyError):
+        pass
     return {
         "metric": "KDA varlen fwd tokens/sec, 8192 tokens in 16 packed sequences, H=32 bf16",
         "value": round(T / (wall_ms / 1e3), 1),
@@ -301,10 +318,13 @@ def run_varlen(args, dev, inputs_cpu) -> dict:
         "config": {"workload": f"kda_bt16_fwd cu_seqlens, {VARLEN_N} sequences over T={T}, "
                                f"H={H}, lengths {lens}", "seq_len": T, "heads": H,
                    "parallelism": "none (1 GPU)"},
-        "roofline": {"bound": "hbm", "kernel": "forward: stage 1 + stage 2",
+        "roofline": {"bound": "hbm",
+                     "kernel": ("forward: fused_kernel (stage 1's records kept in LDS), one launch"
+                                if fused else "forward: stage 1 + stage 2"),
+                     **({"two_stage_kernels_ms": stage_ms} if fused else {}),
                      "achieved": round(achieved, 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic,
                      "alg_bytes": sum(by), "forward_ms_events": round(fwd_ms, 5),
                      "slowest_kernel": dom,
                      "kernels": {n: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
@@ -537,12 +557,16 @@ def run_forward(args, dev, name: str, *, cpu: bool, inputs_cpu=None) -> dict:
 
     by1, by2 = algorithmic_bytes(b, b, t, h, h0 is not None)
     fl1, fl2 = matmul_flops(None, b, t, h)
-    kern = {
+    fused = k1.forward_plan == "fused"
+    stage_kern = {
         "k1": {"ms": k1_ms, "alg_bytes": by1, "alg_gbs": by1 / k1_ms / 1e6,
                "alg_tflops": fl1 / k1_ms / 1e9},
         "k2": {"ms": k2_ms, "alg_bytes": by2, "alg_gbs": by2 / k2_ms / 1e6,
                "alg_tflops": fl2 / k2_ms / 1e9},
     }
+    # The forward's kernels: one fused launch, or the two stages.
+    kern = ({"fused": {"ms": fwd_ms, "alg_bytes": by1 + by2, "alg_gbs": (by1 + by2) / fwd_ms / 1e6,
+                       "alg_tflops": (fl1 + fl2) / fwd_ms / 1e9}} if fused else stage_kern)
     traffic = measured_traffic(b, t, h)
     if traffic:
         for n in kern:
@@ -557,13 +581,14 @@ def run_forward(args, dev, name: str, *, cpu: bool, inputs_cpu=None) -> dict:
     achieved = tot_bytes / fwd_ms / 1e6
     roofline = {
         "bound": "hbm",
-        "kernel": "forward: stage 1 (k1_kernel) + stage 2 (k2_kernel), one launch each",
+        "kernel": ("forward: fused_kernel (stage 1's records kept in LDS), one launch" if fused else
+                   "forward: stage 1 (k1_kernel) + stage 2 (k2_kernel or k2w_kernel), one launch each"),
         "achieved": round(achieved, 2),
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 5),
-        "traffic": (sum(traffic[n] for n in ("k1", "k2")) if traffic and "k1" in traffic
-                    and "k2" in traffic else None),
+        "traffic": (sum(traffic[n] for n in kern) if traffic and all(n in traffic for n in kern)
+                    else None),
         "alg_bytes": tot_bytes,
         "alg_bytes_rule": "B*T*H*1282 + 65536*B*H*(h0 passed + ht) + 516*H",
         "forward_ms_events": round(fwd_ms, 5),
@@ -573,6 +598,10 @@ def run_forward(args, dev, name: str, *, cpu: bool, inputs_cpu=None) -> dict:
         "kernels": {n: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
                         for kk, vv in d.items()} for n, d in kern.items()},
     }
+    if fused:
+        # the two stages on the same inputs, each timed on its own (the
+        # forward does not run them here)
+        roofline["two_stage_kernels_ms"] = {n: round(d["ms"], 4) for n, d in stage_kern.items()}
     h0_txt = {None: "no initial state", "zeros": "zero initial state passed"}.get(
         c["h0"], f"initial state ~N(0,{c['h0']})")
     result = {

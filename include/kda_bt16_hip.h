@@ -139,16 +139,30 @@ size_t kda_bt16_workspace_bytes(int32_t B, int32_t T, int32_t HV, int32_t K, int
  * presence, never the device memory. */
 size_t kda_bt16_workspace_bytes_args(const KdaBt16Args* args);
 
-/* Full forward: stage 1 then stage 2 on `stream` (a hipStream_t; NULL is the
- * legacy default stream).  Replaces _run's two launches, kernels.py:581-602. */
+/* Full forward on `stream` (a hipStream_t; NULL is the legacy default
+ * stream).  Replaces _run's two launches, kernels.py:581-602: stage 1 then
+ * stage 2 (kda_bt16_k1_hip, kda_bt16_k2_hip), or, when there are at least as
+ * many (sequence, value head) pairs as the device has CUs and no debug
+ * output is asked for, one fused kernel that keeps stage 1's per-chunk
+ * records in LDS instead of the workspace (same results bit for bit).  The
+ * environment variable KDA_BT16_FUSED=0 keeps the two stages, =1 fuses
+ * whenever no debug output is asked for.  The workspace is required either
+ * way. */
 int kda_bt16_fwd_hip(const KdaBt16Args* args, void* stream);
+
+/* Which kernels kda_bt16_fwd_hip (and kda_bt16_fwd_noalloc_hip) run for
+ * these arguments on the current device: 1 the fused kernel, 0 stage 1 then
+ * stage 2, or a negative KDA_BT16_E* code for invalid arguments.  Reads no
+ * device memory and needs no workspace.  No counterpart in the reference,
+ * whose _run always launches its two stages (kernels.py:581-602). */
+int kda_bt16_fwd_plan(const KdaBt16Args* args);
 
 /* Full forward that allocates nothing and takes no workspace.  No
  * counterpart in the reference: it is for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  The same kernels as kda_bt16_fwd_hip,
  * with the same results bit for bit; the records stage 1 hands to stage 2
- * live in a file-scope device array of KDA_BT16_NOALLOC_MAX_WORKSPACE bytes
+ * (when the forward is not fused) live in a file-scope device array of KDA_BT16_NOALLOC_MAX_WORKSPACE bytes
  * that the library holds on every GPU it runs on until the process ends.
  * args->workspace and args->workspace_bytes are ignored.  Returns
  * KDA_BT16_ESCRATCH (before any HIP call) when kda_bt16_workspace_bytes_args

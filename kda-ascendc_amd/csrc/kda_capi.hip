@@ -339,6 +339,13 @@ int kda_bt16_fwd_hip(const KdaBt16Args* args, void* stream) {
     return KDA_BT16_OK;
 }
 
+int kda_bt16_fwd_plan(const KdaBt16Args* args) {
+    Params p;
+    const int rc = to_params_core(args, p, true, true);
+    if (rc != KDA_BT16_OK) return rc;
+    return kda::fwd_plan(p);
+}
+
 int kda_bt16_fwd_noalloc_hip(const KdaBt16Args* args, void* stream) {
     Params p;
     int rc = to_params_core(args, p, true, true);

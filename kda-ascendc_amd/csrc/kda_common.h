@@ -379,8 +379,10 @@ hipError_t launch_k2_wide(const Params& p, int tpw, hipStream_t stream);
 // geometry on `ncu` CUs, and its launch.
 bool fused_forward(const Params& p, int ncu);
 hipError_t launch_fused(const Params& p, hipStream_t stream);
-// The forward: fused, or stage 1 then stage 2 (kda_k2.hip).
+// The forward: fused, or stage 1 then stage 2 (kda_k2.hip); fwd_plan says
+// which on the current device (1 fused, 0 two stages).
 hipError_t launch_fwd(const Params& p, hipStream_t stream);
+int fwd_plan(const Params& p);
 hipError_t launch_recurrent(const Params& p, hipStream_t stream);
 // Backward (kda_bt16_bwd.hip, and the training variants of the stages).
 hipError_t launch_k1_both_records(const Params& p, hipStream_t stream);

@@ -249,12 +249,36 @@ __device__ __forceinline__ void producer_wave(const Params& p, int pw, int hv, c
     }
 }
 
+// The (sequence or batch row, value head) of work-group wg.  A work-group
+// runs as long as its sequence, and work-groups start in id order as CUs
+// free up: with cu_seqlens (up to 64 sequences) the ids go to the sequences
+// longest first, each sequence's heads together, so that the longest chains
+// start at once and the short ones fill in around them.  Otherwise the
+// natural order.
+__device__ __forceinline__ int fused_pair(const Params& p, int wg) {
+    if (!p.cu_seqlens || p.N > 64) return wg;
+    const int lane = threadIdx.x & 63;
+    const int len = lane < p.N ? cu_at(p, lane + 1) - cu_at(p, lane) : -1;
+    // rank of this lane's sequence: the sequences longer, or as long with a
+    // lower index
+    int rank = 0;
+    for (int m = 0; m < p.N; ++m) {
+        const int lm = __builtin_amdgcn_readlane(len, m);
+        rank += (lm > len || (lm == len && m < lane)) ? 1 : 0;
+    }
+    const int s = wg / p.HV;
+    const uint64_t hit = __ballot(lane < p.N && rank == s);
+    if (hit == 0) return wg;  // (the ranks are a permutation: never taken)
+    const int n = __builtin_amdgcn_readfirstlane((int)__builtin_ctzll(hit));
+    return n * p.HV + (wg - s * p.HV);
+}
+
 // One work-group per (sequence or batch row, value head).
 template <bool GB16>
 __global__ __launch_bounds__(F_THREADS) void fused_kernel(Params p) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int bh = blockIdx.x;
+    const int bh = fused_pair(p, blockIdx.x);
     const int hv = bh - (bh / p.HV) * p.HV;
     const SeqSpan sp = seq_span(p, bh);
     const int64_t sbase = (int64_t)bh * DK * DK;

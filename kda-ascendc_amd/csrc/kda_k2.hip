@@ -1012,6 +1012,8 @@ hipError_t launch_k2(const Params& p, hipStream_t stream) {
     return hipGetLastError();
 }
 
+int fwd_plan(const Params& p) { return fused_forward(p, cu_count()) ? 1 : 0; }
+
 hipError_t launch_fwd(const Params& p, hipStream_t stream) {
     if (fused_forward(p, cu_count())) return launch_fused(p, stream);
     const hipError_t e = launch_k1(p, stream);

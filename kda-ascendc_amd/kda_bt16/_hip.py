@@ -35,6 +35,7 @@ EXPORTED_SYMBOLS = (
     "kda_bt16_workspace_bytes",
     "kda_bt16_workspace_bytes_args",
     "kda_bt16_fwd_hip",
+    "kda_bt16_fwd_plan",
     "kda_bt16_fwd_noalloc_hip",
     "kda_bt16_k1_hip",
     "kda_bt16_k2_hip",
@@ -157,6 +158,8 @@ def lib() -> ctypes.CDLL:
         h.kda_bt16_bwd_saved_hip.restype = ctypes.c_int
         h.kda_bt16_bwd_saved_hip.argtypes = [ctypes.POINTER(KdaBt16BwdArgs), ctypes.c_void_p,
                                              ctypes.c_size_t, ctypes.c_void_p]
+        h.kda_bt16_fwd_plan.restype = ctypes.c_int
+        h.kda_bt16_fwd_plan.argtypes = [ctypes.POINTER(KdaBt16Args)]
         h.kda_bt16_strerror.restype = ctypes.c_char_p
         h.kda_bt16_strerror.argtypes = [ctypes.c_int]
         h.kda_bt16_abi_version.restype = ctypes.c_int
@@ -176,6 +179,15 @@ def workspace_bytes(B: int, T: int, HV: int, K: int, V: int) -> int:
 def workspace_bytes_args(args: KdaBt16Args) -> int:
     """Workspace bytes for any arguments, varlen included."""
     return int(lib().kda_bt16_workspace_bytes_args(ctypes.byref(args)))
+
+
+def fwd_plan(args: KdaBt16Args) -> int:
+    """``kda_bt16_fwd_plan``: 1 if the forward runs fused on the current
+    device, 0 if stage 1 then stage 2; raises on invalid arguments."""
+    rc = int(lib().kda_bt16_fwd_plan(ctypes.byref(args)))
+    if rc < 0:
+        raise RuntimeError(f"kda_bt16_fwd_plan: {lib().kda_bt16_strerror(rc).decode()}")
+    return rc
 
 
 def bwd_workspace_bytes(args: KdaBt16Args) -> int:

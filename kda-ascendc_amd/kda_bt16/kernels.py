@@ -714,6 +714,9 @@ def kda_bt16_stage_launchers(
         _ = keep
         _hip.call("kda_bt16_k1_hip", args, torch.cuda.current_stream(dev).cuda_stream)
 
+    # which kernels kda_bt16_fwd runs for these arguments: "fused" or "two-stage"
+    k1.forward_plan = "fused" if _hip.fwd_plan(args) == 1 else "two-stage"
+
     def k2():
         _ = keep
         _hip.call("kda_bt16_k2_hip", args, torch.cuda.current_stream(dev).cuda_stream)

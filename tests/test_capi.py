@@ -117,6 +117,25 @@ def test_argument_checks_return_codes_without_launching(fn):
         _hip.call(fn, _args(), 0)
 
 
+def test_forward_plan_reads_no_device_memory(monkeypatch):
+    """kda_bt16_fwd_plan: argument checks, the KDA_BT16_FUSED override, and
+    the two stages whenever debug outputs are asked for (they come from
+    stage 1).  Pointers are never dereferenced."""
+    f = _hip.lib().kda_bt16_fwd_plan
+    fake = 1 << 40
+    ten = dict(q=fake, k=fake, v=fake, g=fake, beta=fake, o=fake)
+    assert f(None) == -1
+    assert f(ctypes.byref(_args(K=64, **ten))) == -2
+    assert f(ctypes.byref(_args())) == -1  # missing tensors
+    monkeypatch.setenv("KDA_BT16_FUSED", "0")
+    assert f(ctypes.byref(_args(B=16, H=32, HV=32, **ten))) == 0
+    monkeypatch.setenv("KDA_BT16_FUSED", "1")
+    assert f(ctypes.byref(_args(**ten))) == 1
+    dbg = dict(dbg_Aqk=fake, dbg_A_inv=fake, dbg_w=fake, dbg_u=fake, dbg_g=fake)
+    assert f(ctypes.byref(_args(**ten, **dbg))) == 0
+    assert _hip.fwd_plan(_args(**ten)) == 1
+
+
 def test_workspace_checked_before_launch():
     fake = 1 << 40  # never dereferenced: the size check fails first
     a = _args(q=fake, k=fake, v=fake, g=fake, beta=fake, o=fake, workspace=fake, workspace_bytes=100)
