@@ -69,6 +69,12 @@ extern "C" {
  * chunk-local log2 cumsum, as kda_gate_chunk_cumsum does for the gate
  * (tests/test_kda_bt16.py:16).  No effect with USE_GATE. */
 #define KDA_BT16_G_LOG_DECAY       (1u << 5)
+/* The forward entries (kda_bt16_fwd_hip, kda_bt16_fwd_noalloc_hip,
+ * kda_bt16_fwd_plan): run the fused kernel whatever the (sequence, value
+ * head) count, the reference's use_fused_kernel=True (kernels.py:769-810,
+ * its single-kernel variant kernels.py:305-472).  Debug outputs still take
+ * the two stages; the other entries ignore it. */
+#define KDA_BT16_FUSED_KERNEL      (1u << 6)
 
 /* Element types of g and beta, and of cu_seqlens. */
 #define KDA_BT16_DTYPE_F32  0
@@ -144,10 +150,11 @@ size_t kda_bt16_workspace_bytes_args(const KdaBt16Args* args);
  * stage 2 (kda_bt16_k1_hip, kda_bt16_k2_hip), or, when there are at least as
  * many (sequence, value head) pairs as the device has CUs and no debug
  * output is asked for, one fused kernel that keeps stage 1's per-chunk
- * records in LDS instead of the workspace (same results bit for bit).  The
- * environment variable KDA_BT16_FUSED=0 keeps the two stages, =1 fuses
- * whenever no debug output is asked for.  The workspace is required either
- * way. */
+ * records in LDS instead of the workspace (same results bit for bit).
+ * KDA_BT16_FUSED_KERNEL in args->flags fuses whatever the count; without
+ * it, the environment variable KDA_BT16_FUSED=0 keeps the two stages and =1
+ * fuses.  Debug outputs always take the two stages.  The workspace is
+ * required either way. */
 int kda_bt16_fwd_hip(const KdaBt16Args* args, void* stream);
 
 /* Which kernels kda_bt16_fwd_hip (and kda_bt16_fwd_noalloc_hip) run for

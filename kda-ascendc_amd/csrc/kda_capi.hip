@@ -75,6 +75,7 @@ int check_common(const KdaBt16Args* a, Params& p) {
     p.use_l2norm = (a->flags & KDA_BT16_USE_QK_L2NORM) != 0;
     p.use_beta_sigmoid = (a->flags & KDA_BT16_USE_BETA_SIGMOID) != 0;
     p.g_log = (a->flags & KDA_BT16_G_LOG_DECAY) != 0;
+    p.force_fused = (a->flags & KDA_BT16_FUSED_KERNEL) != 0;
     p.h0_v_first = p.ht_v_first = (a->flags & KDA_BT16_STATE_V_FIRST) != 0;
     p.cu_seqlens = a->cu_seqlens;
     p.cu_i64 = a->cu_seqlens_dtype == KDA_BT16_DTYPE_I64;

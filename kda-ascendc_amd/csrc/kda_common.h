@@ -133,6 +133,7 @@ struct Params {
     int g_log;  // without use_gate: g is the per-token natural-log decay
     int h0_v_first, ht_v_first;  // layouts of h0 / ht: [V, K] if set, else [K, V]
     int o_fp32;                  // token recurrence only: o in fp32
+    int force_fused;             // forward: the fused kernel whatever the geometry
     // Varlen: N sequences packed along T (B == 1), sequence n holding tokens
     // [cu_seqlens[n], cu_seqlens[n+1]); states are [N, HV, ...].  NS is the
     // number of record slots per value head.  Null cu_seqlens: fixed length.

@@ -336,12 +336,14 @@ __global__ __launch_bounds__(F_THREADS) void fused_kernel(Params p) {
 
 }  // namespace
 
-// Whether the forward runs as one fused kernel: at least as many (sequence,
-// head) pairs as CUs, and none of the reference-layout intermediates asked
-// for (those come from stage 1).  KDA_BT16_FUSED=0 keeps the two stages,
-// =1 fuses whenever no intermediates are asked for.
+// Whether the forward runs as one fused kernel: never when the
+// reference-layout intermediates are asked for (those come from stage 1);
+// always when the caller asks for it (the reference's use_fused_kernel);
+// else KDA_BT16_FUSED=0 keeps the two stages and =1 fuses; else at least as
+// many (sequence, head) pairs as CUs.
 bool fused_forward(const Params& p, int ncu) {
     if (p.dbg_w || p.dbg_u || p.dbg_Aqk || p.dbg_A_inv || p.dbg_g) return false;
+    if (p.force_fused) return true;
     const int64_t nbh = (int64_t)(p.cu_seqlens ? p.N : p.B) * p.HV;
     if (const char* e = getenv("KDA_BT16_FUSED")) {
         if (atoi(e) == 0) return false;

@@ -20,6 +20,7 @@ USE_BETA_SIGMOID = 1 << 2
 STATE_V_FIRST = 1 << 3
 O_FP32 = 1 << 4  # token recurrence only
 G_LOG_DECAY = 1 << 5  # without USE_GATE: g is the per-token natural-log decay
+FUSED_KERNEL = 1 << 6  # forward entries: the fused kernel whatever the geometry
 
 # Bytes of the static scratch of kda_bt16_fwd_noalloc_hip, and the code it
 # returns for a geometry whose records do not fit.

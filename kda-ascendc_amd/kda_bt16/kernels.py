@@ -17,8 +17,12 @@ Differences from the reference, all supersets of its contract:
 * ``state_v_first=False`` is handled by stage 2 reading/writing the
   ``[K, V]`` state directly instead of transposing at the boundary
   (kernels.py:499-510); the values are identical;
-* ``use_fused_kernel=True`` is accepted and runs the same two-stage path
-  (the reference's own test requires the two to agree, tests/test_kda_bt16.py:174-200);
+* ``use_fused_kernel=True`` runs the fused kernel (one work-group per
+  sequence and value head, stage 1's records kept in LDS: the reference's
+  single-kernel variant, kernels.py:305-472) whatever the geometry; without
+  it the forward fuses when the (sequence, head) pairs are at least as many
+  as the CUs.  Both give the two-stage results bit for bit (the reference's
+  own test requires the two to agree, tests/test_kda_bt16.py:174-200);
 * ``HV`` may be any multiple of ``H`` (grouped value heads: value head hv
   reads q/k head hv // (HV // H), the indexing of kernels.py:88, which the
   reference's validation does not yet admit, kernels.py:729-730);
@@ -289,8 +293,8 @@ def _make_args(
 
 
 def _flags(use_gate: bool, use_l2norm: bool, use_beta_sigmoid: bool, state_v_first: bool,
-           g_log: bool = False) -> int:
-    f = 0
+           g_log: bool = False, fused: bool = False) -> int:
+    f = _hip.FUSED_KERNEL if fused else 0
     if g_log and not use_gate:
         f |= _hip.G_LOG_DECAY
     if use_gate:
@@ -333,7 +337,6 @@ def _run(
     ``save_state``: run the training forward (``kda_bt16_fwd_save_hip``)
     and return ``(o, ht, saved)``, ``saved`` the uint8 state tensor the
     backward starts from."""
-    del use_fused  # one production path; see module docstring
     _require_gpu(q)
     g = _gate_f32(g)
     q, k, v, g, initial_state, dt_bias = (
@@ -377,7 +380,7 @@ def _run(
             q, k, v, g, beta, scale, lower_bound if use_gate_in_kernel else None,
             A_log, dt_bias, initial_state, o, ht, None, 0,
             _flags(use_gate_in_kernel, use_qk_l2norm_in_kernel, use_beta_sigmoid_in_kernel,
-                   state_v_first, g_log),
+                   state_v_first, g_log, use_fused),
             dbg, cu_seqlens,
         )
         ws_bytes = _hip.workspace_bytes_args(args)
@@ -508,8 +511,11 @@ def _wants_grad(*ts) -> bool:
 def _fwd_maybe_autograd(
     q, k, v, g, beta, scale, initial_state, output_final_state, l2, use_gate, bsig,
     lower_bound, A_log, dt_bias, svf, reuse_workspace=False, cu_seqlens=None, g_log=False,
+    use_fused=False,
 ):
-    """:func:`_run`, through :class:`_KdaBt16Fn` when an input requires grad."""
+    """:func:`_run`, through :class:`_KdaBt16Fn` when an input requires grad
+    (whose training forward keeps its per-chunk state for the backward and so
+    always runs the two stages)."""
     if _wants_grad(q, k, v, g, beta, A_log, dt_bias, initial_state):
         cfg = (scale, output_final_state, l2, use_gate, bsig, lower_bound, svf, g_log,
                reuse_workspace)
@@ -517,7 +523,7 @@ def _fwd_maybe_autograd(
     return _run(
         q, k, v, g, beta, scale, initial_state, output_final_state, l2, use_gate, bsig,
         lower_bound, A_log, dt_bias, svf, return_intermediates=False,
-        reuse_workspace=reuse_workspace, cu_seqlens=cu_seqlens, g_log=g_log,
+        reuse_workspace=reuse_workspace, cu_seqlens=cu_seqlens, g_log=g_log, use_fused=use_fused,
     )
 
 
@@ -623,12 +629,11 @@ def kda_bt16_fwd(
     )
     if scale is None:
         scale = K ** -0.5
-    del use_fused_kernel  # one production path; see module docstring
     return _fwd_maybe_autograd(
         q, k, v, g, beta, scale, initial_state, output_final_state,
         use_qk_l2norm_in_kernel, use_gate_in_kernel, use_beta_sigmoid_in_kernel,
         lower_bound, A_log, dt_bias, state_v_first,
-        reuse_workspace=reuse_workspace, cu_seqlens=cu_seqlens,
+        reuse_workspace=reuse_workspace, cu_seqlens=cu_seqlens, use_fused=use_fused_kernel,
     )
 
 
@@ -816,9 +821,10 @@ def kda_decode_step(
 
 
 def kda_bt16_kernel_fused(*_args, **_kwargs):
-    """The reference's experimental single-kernel variant (kernels.py:305-472)
-    is not built: ``use_fused_kernel=True`` runs the two-stage path."""
+    """The reference exports its single-kernel variant as a raw Triton kernel
+    (kernels.py:305-472) launched with grid syntax; here the fused kernel is
+    reached through ``kda_bt16_fwd(use_fused_kernel=True)``."""
     raise NotImplementedError(
-        "kda_bt16_kernel_fused is not provided on MI355X; "
-        "kda_bt16_fwd(use_fused_kernel=True) runs the two-stage kernels"
+        "kda_bt16_kernel_fused is not a launchable object on MI355X; "
+        "kda_bt16_fwd(use_fused_kernel=True) runs the fused HIP kernel"
     )

@@ -134,6 +134,11 @@ def test_forward_plan_reads_no_device_memory(monkeypatch):
     dbg = dict(dbg_Aqk=fake, dbg_A_inv=fake, dbg_w=fake, dbg_u=fake, dbg_g=fake)
     assert f(ctypes.byref(_args(**ten, **dbg))) == 0
     assert _hip.fwd_plan(_args(**ten)) == 1
+    # the caller's request (use_fused_kernel=True) wins over the environment,
+    # debug outputs over both
+    monkeypatch.setenv("KDA_BT16_FUSED", "0")
+    assert f(ctypes.byref(_args(flags=_hip.FUSED_KERNEL, **ten))) == 1
+    assert f(ctypes.byref(_args(flags=_hip.FUSED_KERNEL, **ten, **dbg))) == 0
 
 
 def test_workspace_checked_before_launch():
