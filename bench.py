@@ -175,6 +175,9 @@ def measured_mfma(kern: dict, b: int = B, t: int = T, h: int = H):
     return out
 
 
+STAGE_REPS = 100  # minimum launches when a stage is timed on its own
+
+
 def time_events(fn, reps: int) -> float:
     """Average ms per call over ``reps`` calls, HIP events on the current stream."""
     start = torch.cuda.Event(enable_timing=True)
@@ -270,7 +273,7 @@ def run_varlen(args, dev, inputs_cpu) -> dict:
                                             A_log=A_log, dt_bias=dt_bias,
                                             lower_bound=LOWER_BOUND, cu_seqlens=cu)
     k1(); k2()
-    reps = max(args.steps, 10)
+    reps = max(args.steps, STAGE_REPS)
     k1_ms, k2_ms = time_events(k1, reps), time_events(k2, reps)
     for _ in range(args.warmup):
         step()
@@ -534,7 +537,11 @@ def run_forward(args, dev, name: str, *, cpu: bool, inputs_cpu=None) -> dict:
                                             output_final_state=True, A_log=A_log,
                                             dt_bias=dt_bias, lower_bound=LOWER_BOUND)
     k1(); k2()
-    reps = max(args.steps, 10)
+    # Each stage over at least 100 launches: a steadier figure than a few,
+    # and ~30 ms of this work has run by the time the forward's own warmup
+    # starts (with 20 launches each, a 20-step run measured the forward ~3 %
+    # slower than a 50- or 200-step run).
+    reps = max(args.steps, STAGE_REPS)
     k1_ms = time_events(k1, reps)
     k2_ms = time_events(k2, reps)
 
