@@ -124,10 +124,20 @@ __device__ __forceinline__ i32x4 buffer_words(const void* base, uint32_t bytes) 
 // lds + 16 l).  Written as inline asm so that the compiler, which cannot
 // tell which LDS bytes such a load writes, does not wait for it before every
 // later LDS access of the wave; the producer waits for it itself (vmcnt)
-// before it reads the staging area.
+// before it reads the staging area.  The load takes its LDS address from
+// M0, which the block saves and restores (the compiler may hold a value
+// there); a wait state separates each M0 write from the next use, as the
+// compiler's own direct loads have.
 __device__ __forceinline__ void dma16(i32x4 rs, uint32_t lds, uint32_t voff) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                 :: "s"(lds), "v"(voff), "s"(rs) : "memory", "m0");
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+        "s_mov_b32 m0, %0\n\t"
+        "s_nop 0"
+        : "=&s"(saved) : "s"(lds), "v"(voff), "s"(rs) : "memory");
 }
 
 // Staging layout: 16 rows of UNITS 16-byte units (16 for a bf16 row, 32
