@@ -171,9 +171,10 @@ int kda_bt16_fwd_plan(const KdaBt16Args* args);
  * with the same results bit for bit; the records stage 1 hands to stage 2
  * (when the forward is not fused) live in a file-scope device array of KDA_BT16_NOALLOC_MAX_WORKSPACE bytes
  * that the library holds on every GPU it runs on until the process ends.
- * args->workspace and args->workspace_bytes are ignored.  Returns
- * KDA_BT16_ESCRATCH (before any HIP call) when kda_bt16_workspace_bytes_args
- * exceeds that size.  Every call on one GPU uses that GPU's one array:
+ * args->workspace and args->workspace_bytes are ignored.  When the forward
+ * runs fused (kda_bt16_fwd_plan) it uses no scratch and takes any size;
+ * otherwise it returns KDA_BT16_ESCRATCH (before any launch) when
+ * kda_bt16_workspace_bytes_args exceeds that size.  Every call on one GPU uses that GPU's one array:
  * calls that overlap on one GPU (two streams, two threads) race and give
  * wrong results; calls in order on one stream are safe.  The array keeps
  * the last call's contents; no part of it needs clearing (stage 1 writes

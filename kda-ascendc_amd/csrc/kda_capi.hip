@@ -351,11 +351,14 @@ int kda_bt16_fwd_noalloc_hip(const KdaBt16Args* args, void* stream) {
     Params p;
     int rc = to_params_core(args, p, true, true);
     if (rc != KDA_BT16_OK) return rc;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    // The fused forward keeps its records in LDS: no scratch, any size.
+    if (kda::fwd_plan(p) == 1) return kda::launch_fused(p, s) == hipSuccess ? KDA_BT16_OK : KDA_BT16_ELAUNCH;
     if (kda_bt16_workspace_bytes_args(args) > KDA_BT16_NOALLOC_MAX_WORKSPACE)
         return KDA_BT16_ESCRATCH;
     rc = scratch_ptr(&p.ws);
     if (rc != KDA_BT16_OK) return rc;
-    if (kda::launch_fwd(p, static_cast<hipStream_t>(stream)) != hipSuccess) return KDA_BT16_ELAUNCH;
+    if (kda::launch_fwd(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
     return KDA_BT16_OK;
 }
 
