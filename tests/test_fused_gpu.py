@@ -116,3 +116,18 @@ def test_heuristic_fuses_when_pairs_fill_the_cus(gpu_device):
     o2, ht2 = _run(c, gpu_device, None, True, True, True, 0)
     o, ht = _run(c, gpu_device, None, True, True, True, None)
     assert torch.equal(o, o2) and torch.equal(ht, ht2)
+
+
+@pytest.mark.parametrize("B,T,H,h0", [(1, 8192, 32, False), (16, 2048, 32, True)],
+                         ids=["configs2_B1_T8192_H32", "configs4_B16_T2048_H32"])
+def test_fused_equals_two_stage_at_baseline_sizes(B, T, H, h0, gpu_device):
+    """BASELINE configs[2] and configs[4] at full size: the fused kernel
+    (forced at configs[2], where the forward picks the two stages; picked by
+    itself at configs[4]) against the two stages, bit for bit."""
+    c = _inputs(B, T, H, H, B, seed=42 + B, gdt="bf16", in_kernel_gate=True)
+    print(f"[fused] full size B={B} T={T} H={H}", flush=True)
+    o2, ht2 = _run(c, gpu_device, None, True, h0, True, 0)
+    o1, ht1 = _run(c, gpu_device, None, True, h0, True, 1)
+    assert torch.isfinite(o2.float()).all() and torch.isfinite(ht2).all()
+    assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
+    assert torch.equal(ht1.view(torch.int32), ht2.view(torch.int32))
