@@ -131,3 +131,55 @@ def test_fused_equals_two_stage_at_baseline_sizes(B, T, H, h0, gpu_device):
     assert torch.isfinite(o2.float()).all() and torch.isfinite(ht2).all()
     assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
     assert torch.equal(ht1.view(torch.int32), ht2.view(torch.int32))
+
+
+@pytest.mark.parametrize("lower_bound", [-8.0, -10.0])
+def test_fused_saturated_gate(lower_bound, gpu_device):
+    """The reference's saturated-gate case (tests/test_kda_bt16.py:128-171:
+    A_log = 0, no dt_bias, g = 20, lower_bound -8 and -10) through the fused
+    kernel: finite, and the two-stage bits."""
+    B, T, H = 2, 200, 2
+    c = _inputs(B, T, H, H, B, seed=11, gdt="bf16", in_kernel_gate=True)
+    c["g"] = torch.full((B, T, H, 128), 20.0).bfloat16()
+    c["A_log"] = torch.zeros(H)
+    outs = []
+    for fused in (0, 1):
+        os.environ[ENV] = str(fused)
+        try:
+            o, ht = kda_bt16_fwd(
+                *(c[x].to(gpu_device) for x in ("q", "k", "v", "g", "beta")), scale=0.1,
+                initial_state=c["h0"].to(gpu_device), output_final_state=True,
+                use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True,
+                use_beta_sigmoid_in_kernel=True, lower_bound=lower_bound,
+                A_log=c["A_log"].to(gpu_device), dt_bias=None)
+            torch.cuda.synchronize()
+        finally:
+            os.environ.pop(ENV, None)
+        assert torch.isfinite(o.float()).all() and torch.isfinite(ht).all()
+        outs.append((o, ht))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+
+
+def test_fused_repeated_calls_are_bit_identical(gpu_device):
+    """Twenty back-to-back fused forwards at B=16 T=512 H=32 on one stream:
+    every call gives the first call's bits (the LDS flags and ring start
+    clean each launch, and no wait of the producer/consumer protocol runs
+    out)."""
+    c = _inputs(16, 512, 32, 32, 16, seed=13, gdt="bf16", in_kernel_gate=True)
+    dev = gpu_device
+    args = [c[x].to(dev) for x in ("q", "k", "v", "g", "beta")]
+    kw = dict(scale=0.1, initial_state=c["h0"].to(dev), output_final_state=True,
+              use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True,
+              use_beta_sigmoid_in_kernel=True, lower_bound=-5.0, A_log=c["A_log"].to(dev),
+              dt_bias=c["dt_bias"].to(dev))
+    os.environ[ENV] = "1"
+    try:
+        runs = [kda_bt16_fwd(*args, **kw) for _ in range(20)]
+        torch.cuda.synchronize()
+    finally:
+        os.environ.pop(ENV, None)
+    o0, h0 = runs[0]
+    assert torch.isfinite(o0.float()).all()
+    for i, (o, ht) in enumerate(runs[1:], 1):
+        assert torch.equal(o.view(torch.int16), o0.view(torch.int16)), f"call {i}: o"
+        assert torch.equal(ht.view(torch.int32), h0.view(torch.int32)), f"call {i}: ht"
