@@ -3,14 +3,15 @@
 //
 // The two-stage forward (kda_k1.hip, then kda_k2.hip / kda_k2w.hip) passes
 // each chunk's 17 KiB record through HBM: written by stage 1, read back by
-// stage 2.  With a work-group per (sequence, head) on every CU that round
-// trip is most of the forward's traffic (B=16 T=2048 H=32: 2.3 GB of
-// records against 1.4 GB of inputs and outputs), and both stages are HBM
-// bound.  Here one work-group per (sequence, value head) keeps the records
-// in LDS:
+// stage 2.  Once the (sequence, head) pairs fill the CUs that round trip is
+// most of the forward's traffic (B=16 T=2048 H=32: 3.7 GB moved per forward
+// for 1.4 GB of inputs and outputs).  Here one work-group per (sequence,
+// value head) keeps the records in LDS:
 //   * NP producer waves each form every NP-th chunk's record with stage 1's
-//     per-chunk code (k1_chunk, kda_k1_chunk.h) straight into a ring of
-//     RING record slots in LDS, each with its own LDS scratch;
+//     per-chunk code (k1_compute, kda_k1_chunk.h) straight into a ring of
+//     RING record slots in LDS, each with its own LDS scratch; each loads
+//     its next chunk's q, k and g rows into an LDS staging area while it
+//     works on the current one;
 //   * four compute waves each run the recurrence for two of the head's
 //     eight 16-column value tiles (wide_step, kda_k2w_step.h), reading the
 //     operands every tile shares from the slot.
@@ -54,10 +55,7 @@ static_assert(F_RING >= F_NP, "every producer can hold a slot");
 // (fp32) bytes for g.
 constexpr int ST_Q = 0, ST_K = 4096, ST_G = 8192, STAGE_BYTES = 16384;
 
-// The work-group's LDS, as separate variables: the compiler then knows that
-// the staging areas, which direct loads write behind its back, share no
-// bytes with the ring, the scratch or the flags, and does not wait for those
-// loads before every other LDS access.
+// The work-group's LDS.
 __shared__ __attribute__((aligned(1024))) uint8_t f_ring[F_RING][REC_BYTES];
 __shared__ __attribute__((aligned(1024))) uint8_t f_stage[F_NP][STAGE_BYTES];
 __shared__ __attribute__((aligned(16))) uint8_t f_scratch[F_NP][K1_SCRATCH];
