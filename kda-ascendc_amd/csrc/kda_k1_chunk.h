@@ -182,8 +182,7 @@ __device__ __forceinline__ void k1_compute(const Params& p, int hv, int c, const
     const Row32& dop = in.dout;
     const Row32& gp = in.g16;
     const f32x4 (&gf)[8] = in.g32;
-    const bool has_bias = p.use_gate && p.dt_bias;
-    f32x4 bias[8];
+    f32x4 bias[8];  // zeros without dt_bias (k1_bias), so s = g + bias either way
 #pragma unroll
     for (int kt = 0; kt < 8; ++kt) bias[kt] = *reinterpret_cast<const f32x4*>(biasp + 16 * kt + colbase);
     const uint32_t beta_bits = in.beta_bits;
@@ -220,15 +219,20 @@ __device__ __forceinline__ void k1_compute(const Params& p, int hv, int c, const
     }
 
     // ---- gate and chunk-local log2 cumsum (kernels.py:115-124) -----------
+    // sigmoid(ea * s) = 1 / (1 + 2^(s * ea * -log2 e)), with ea * -log2 e
+    // formed once; the cumsum is linear, so lower_bound joins the 1/ln 2
+    // after it (one product per element each, not three).
     if (p.use_gate) {
+        const float eal = ea * -1.4426950408889634f;
+        const float lbr = p.lower_bound * RCP_LN2;
 #pragma unroll
         for (int kt = 0; kt < 8; ++kt) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float s = has_bias ? G[4 * kt + i] + bias[kt][i] : G[4 * kt + i];
-                float gate = p.lower_bound * fast_sigmoid(ea * s);
-                gate = valid ? gate : 0.f;
-                G[4 * kt + i] = row_scan16(gate) * RCP_LN2;
+                const float s = G[4 * kt + i] + bias[kt][i];
+                float sig = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(s * eal));
+                sig = valid ? sig : 0.f;
+                G[4 * kt + i] = row_scan16(sig) * lbr;
             }
         }
     } else if (p.g_log) {
@@ -303,7 +307,9 @@ __device__ __forceinline__ void k1_compute(const Params& p, int hv, int c, const
                     if (4 * j4 + i < t) acc = fmaf(-lr[i], a[4 * j4 + i], acc);
                 }
             }
-            a[t] = (t > r) ? acc : (t == r ? 1.f : 0.f);
+            // above the diagonal (t < r) every a[j < t] is zero, so acc is
+            // +0 there
+            a[t] = t == r ? 1.f : acc;
         }
         if (q4 == 0) {
 #pragma unroll
