@@ -226,10 +226,9 @@ __device__ __forceinline__ void produce(const Params& p, int hv, int c, int c_ne
     }
     const int s = c % F_RING;
     wait_ge(&f_done[s], F_NCW * (c / F_RING));
-    uint16_t* sT = reinterpret_cast<uint16_t*>(scr);
-    float* sL = reinterpret_cast<float*>(scr + K1_SCRATCH_T);
-    float* sX = reinterpret_cast<float*>(scr + K1_SCRATCH_T + K1_SCRATCH_L);
-    k1_compute<K1_FWD, FULL, GB16>(p, hv, c, sp, in, f_bias, ea, sT, sL, sX, f_ring[s]);
+    float* sL = reinterpret_cast<float*>(scr);
+    float* sX = reinterpret_cast<float*>(scr + K1_SCRATCH_L);
+    k1_compute<K1_FWD, FULL, GB16>(p, hv, c, sp, in, f_bias, ea, sL, sX, f_ring[s]);
     // the record's LDS writes have completed before the slot is marked full
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     if (lane == 0) __hip_atomic_store(&f_full[s], c + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);

@@ -32,7 +32,6 @@ namespace {
 // and the gram block to p.la.  Those modes run two waves per SIMD: they
 // hold more.
 // LDS of a work-group (one wave): k1_chunk's scratch.
-__shared__ __attribute__((aligned(16))) uint16_t s_T[BT * LROW];
 __shared__ __attribute__((aligned(16))) float s_L[BT * BT];
 __shared__ float s_X[BT * (BT + 1)];
 
@@ -70,7 +69,7 @@ __attribute__((amdgpu_waves_per_eu(K1M != K1_FWD ? 2 : 3))) void k1_kernel(Param
     int hv, c;
     SeqSpan sp;
     if (!block_chunk(p, threadIdx.x, hv, c, sp)) return;
-    k1_chunk<K1M, ALL_FULL, GB16>(p, hv, c, sp, s_T, s_L, s_X, p.ws + (sp.rec0 + c) * REC_BYTES);
+    k1_chunk<K1M, ALL_FULL, GB16>(p, hv, c, sp, s_L, s_X, p.ws + (sp.rec0 + c) * REC_BYTES);
 }
 
 // The dO operand of each backward record that a training forward saved
@@ -81,21 +80,17 @@ __global__ __launch_bounds__(64) void k1_dout_kernel(Params p) {
     int hv, c;
     SeqSpan sp;
     if (!block_chunk(p, lane, hv, c, sp)) return;
-    const int r = lane & 15, q4 = lane >> 4, colbase = 4 * q4;
+    const int r = lane & 15, colbase = 4 * (lane >> 4);
     const int t0 = c * BT;
     const bool valid = r < min(BT, sp.len - t0);
     const int64_t tok = sp.tok0 + t0 + r;
     Row32 dop;
     load_row(p.dout + (tok * p.HV + hv) * DK, valid, colbase, dop);
-#pragma unroll
-    for (int kt = 0; kt < 8; ++kt) lds_put(s_T, r, colbase, kt, dop.v[kt]);
-    __syncthreads();
-    i16x4 doT[8];
-    load_lds_T(s_T, r, q4, doT);
+    const i16x4 eye = eye_operand(lane);
     uint8_t* brec = p.ws_bwd + (sp.rec0 + c) * REC_BYTES;
 #pragma unroll
     for (int vt = 0; vt < 8; ++vt)
-        __builtin_nontemporal_store(__builtin_bit_cast(u32x2, doT[vt]),
+        __builtin_nontemporal_store(__builtin_bit_cast(u32x2, tile_T(dop.v[vt], eye)),
                                     reinterpret_cast<u32x2*>(brec + BREC_DO + vt * 512 + lane * 8));
 }
 

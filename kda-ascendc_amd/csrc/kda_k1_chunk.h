@@ -14,8 +14,6 @@
 namespace kda {
 namespace {
 
-constexpr int LROW = DK + 8;  // bf16 elements per LDS row (padding spreads banks)
-
 // 32 bf16 values of one row in F order, packed: item 4*kt + i is half
 // (i & 1) of word (i >> 1) of v[kt].
 struct Row32 {
@@ -36,37 +34,37 @@ __device__ __forceinline__ void load_row(const uint16_t* __restrict__ src, bool 
     }
 }
 
-// Row r of an LDS tile, F order: 4 values at columns 16*kt + colbase.
-__device__ __forceinline__ void lds_put(uint16_t* lds, int r, int colbase, int kt, u32x2 pk) {
-    *reinterpret_cast<u32x2*>(lds + r * LROW + 16 * kt + colbase) = pk;
-}
-
-// T order read: item 4*kt + i = M[4*q4 + i][16*kt + r], packed for the
-// 16x16x16 bf16 operand of tile kt.
-__device__ __forceinline__ void load_lds_T(const uint16_t* lds, int r, int q4, i16x4 out[8]) {
-#pragma unroll
-    for (int kt = 0; kt < 8; ++kt) {
-        i16x4 v;
-        v.x = (short)lds[(4 * q4 + 0) * LROW + 16 * kt + r];
-        v.y = (short)lds[(4 * q4 + 1) * LROW + 16 * kt + r];
-        v.z = (short)lds[(4 * q4 + 2) * LROW + 16 * kt + r];
-        v.w = (short)lds[(4 * q4 + 3) * LROW + 16 * kt + r];
-        out[kt] = v;
-    }
-}
-
 __device__ __forceinline__ u32x2 pack4(float a, float b, float c, float d) {
     return u32x2{pack2(a, b), pack2(c, d)};
 }
 __device__ __forceinline__ u32x2 pack4(f32x4 v) { return pack4(v.x, v.y, v.z, v.w); }
 
+// The 16x16x16 B operand of the identity: lane (n, q4) holds
+// I[4*q4 + i][n], bf16 1.0 where 4*q4 + i = n.
+__device__ __forceinline__ i16x4 eye_operand(int lane) {
+    const int n = lane & 15, k0 = 4 * (lane >> 4);
+    constexpr short ONE = 0x3F80;
+    return i16x4{short(k0 == n ? ONE : 0), short(k0 + 1 == n ? ONE : 0), short(k0 + 2 == n ? ONE : 0),
+                 short(k0 + 3 == n ? ONE : 0)};
+}
 
-// LDS scratch of one wave's k1_chunk: the transpose tile (bf16), L and the
-// solve's columns (fp32), in bytes.
-constexpr int K1_SCRATCH_T = BT * LROW * 2;
+// Tile kt of a 16x128 bf16 matrix M from F order to T order, through the
+// matrix core: F order, lane (r, q4) holding M[r][16*kt + 4*q4 + i], is the
+// 16x16x16 A layout, so D = M @ I lands as D[4*q4 + i][r], i.e. T order,
+// lane (r, q4) holding M[4*q4 + i][16*kt + r] (the layout of a 16x16x16 B
+// operand, or an A operand of M^T).  Exact: every sum holds one product,
+// x * 1.
+__device__ __forceinline__ i16x4 tile_T(u32x2 f, i16x4 eye) {
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    return as_i16x4(pack4(mfma_bf16_16x16x16(as_i16x4(f), eye, zero)));
+}
+
+
+// LDS scratch of one wave's k1_chunk: L and the solve's columns (fp32), in
+// bytes.
 constexpr int K1_SCRATCH_L = BT * BT * 4;
 constexpr int K1_SCRATCH_X = BT * (BT + 1) * 4;
-constexpr int K1_SCRATCH = K1_SCRATCH_T + K1_SCRATCH_L + K1_SCRATCH_X;
+constexpr int K1_SCRATCH = K1_SCRATCH_L + K1_SCRATCH_X;
 
 // The wave's own LDS writes are complete before its next LDS read: the
 // scratch of k1_chunk belongs to one wave, so no work-group barrier is
@@ -166,7 +164,7 @@ __device__ __forceinline__ float k1_ea(const Params& p, int hv) {
 template <int K1M, bool FULL, bool GB16>
 __device__ __forceinline__ void k1_compute(const Params& p, int hv, int c, const SeqSpan& sp,
                                            const K1In<GB16, K1M == K1_BOTH>& in, const float* biasp,
-                                           float ea, uint16_t* sT, float* sL, float* sX, uint8_t* rec) {
+                                           float ea, float* sL, float* sX, uint8_t* rec) {
     constexpr bool BOTH = K1M != K1_FWD;
     constexpr bool WITH_DO = K1M == K1_BOTH;
     const K1Row w = k1_row<FULL>(p, hv, c, sp);
@@ -329,25 +327,19 @@ __device__ __forceinline__ void k1_compute(const Params& p, int hv, int c, const
     }
     const i16x4 A_op = as_i16x4(ainv_bf);
     const i16x4 A_neg = as_i16x4(ainv_bf ^ 0x80008000u);
+    // the identity operand of the transposes through the matrix core (tile_T)
+    const i16x4 eye = eye_operand(lane);
 
     if constexpr (BOTH) {
         // ---- backward record ---------------------------------------------
         uint8_t* brec = p.ws_bwd + (sp.rec0 + c) * REC_BYTES;
         // Aqk^T as an A operand: lane (r, q4) takes Aqk[4*q4 + i][r], the
-        // transpose of what it holds, through sL (free after the solve).
-        *reinterpret_cast<f32x4*>(sL + r * BT + 4 * q4) = aqk;
-        wave_lds_fence();
-        {
-            f32x4 at;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) at[i] = sL[(4 * q4 + i) * BT + r];
-            __builtin_nontemporal_store(pack4(at),
-                                        reinterpret_cast<u32x2*>(brec + BREC_AQKT + lane * 8));
-        }
+        // transpose of what it holds (bf16 rounding commutes with it).
+        __builtin_nontemporal_store(__builtin_bit_cast(u32x2, tile_T(aqk_bf, eye)),
+                                    reinterpret_cast<u32x2*>(brec + BREC_AQKT + lane * 8));
         // -w in T order straight from the matrix cores: (-A) @ kb tile kt
-        // lands as -w[4*q4 + i][16*kt + r].  bf16(scale * q^ * 2^G) goes
-        // through the LDS tile to T order.
-        u32x2 wT[8], qsF[8];
+        // lands as -w[4*q4 + i][16*kt + r]; bf16(scale * q^ * 2^G) in T
+        // order.
 #pragma unroll
         for (int kt = 0; kt < 8; ++kt) {
             float kb[4], qs[4];
@@ -357,46 +349,18 @@ __device__ __forceinline__ void k1_compute(const Params& p, int hv, int c, const
                 kb[i] = round_bf(elem(kp, 4 * kt + i) * beta) * e;
                 qs[i] = p.scale * (elem(qp, 4 * kt + i) * e);
             }
-            lds_put(sT, r, colbase, kt, pack4(kb[0], kb[1], kb[2], kb[3]));
-            qsF[kt] = pack4(qs[0], qs[1], qs[2], qs[3]);
-        }
-        wave_lds_fence();
-        {
-            i16x4 kbT[8];
-            load_lds_T(sT, r, q4, kbT);
-#pragma unroll
-            for (int kt = 0; kt < 8; ++kt) {
-                const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-                wT[kt] = pack4(mfma_bf16_16x16x16(A_neg, kbT[kt], zero));
-            }
-        }
-        wave_lds_fence();
-#pragma unroll
-        for (int kt = 0; kt < 8; ++kt) lds_put(sT, r, colbase, kt, qsF[kt]);
-        wave_lds_fence();
-        {
-            i16x4 qsT[8];
-            load_lds_T(sT, r, q4, qsT);
-#pragma unroll
-            for (int kt = 0; kt < 8; ++kt) {
-                const u32x2 qv = __builtin_bit_cast(u32x2, qsT[kt]);
-                __builtin_nontemporal_store(
-                    u32x4{qv.x, qv.y, wT[kt].x, wT[kt].y},
-                    reinterpret_cast<u32x4*>(brec + BREC_UPD + kt * 1024 + lane * 16));
-            }
+            const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+            const u32x2 wT = pack4(mfma_bf16_16x16x16(A_neg, tile_T(pack4(kb[0], kb[1], kb[2], kb[3]), eye), zero));
+            const u32x2 qv = __builtin_bit_cast(u32x2, tile_T(pack4(qs[0], qs[1], qs[2], qs[3]), eye));
+            __builtin_nontemporal_store(u32x4{qv.x, qv.y, wT.x, wT.y},
+                                        reinterpret_cast<u32x4*>(brec + BREC_UPD + kt * 1024 + lane * 16));
         }
         // dO as the B operand of each value tile (T order, the layout of u
         // in the forward record): [vt][lane][i] = dO[4*q4 + i][16*vt + r].
         if constexpr (WITH_DO) {
-            wave_lds_fence();
-#pragma unroll
-            for (int kt = 0; kt < 8; ++kt) lds_put(sT, r, colbase, kt, dop.v[kt]);
-            wave_lds_fence();
-            i16x4 doT[8];
-            load_lds_T(sT, r, q4, doT);
 #pragma unroll
             for (int vt = 0; vt < 8; ++vt)
-                __builtin_nontemporal_store(__builtin_bit_cast(u32x2, doT[vt]),
+                __builtin_nontemporal_store(__builtin_bit_cast(u32x2, tile_T(dop.v[vt], eye)),
                                             reinterpret_cast<u32x2*>(brec + BREC_DO + vt * 512 + lane * 8));
         }
         // kg = bf16(k^ * 2^(G_last - G)) in F order (the A operand of
@@ -423,25 +387,20 @@ __device__ __forceinline__ void k1_compute(const Params& p, int hv, int c, const
             __builtin_nontemporal_store(
                 u32x4{kgF[2 * j].x, kgF[2 * j].y, kgF[2 * j + 1].x, kgF[2 * j + 1].y},
                 reinterpret_cast<u32x4*>(brec + BREC_KG + j * 1024 + lane * 16));
-        wave_lds_fence();
     }
 
     // ---- u = A @ bf16(v * beta) (kernels.py:173-174) ----------------------
     // One 16x16x16 tile per 16 value columns; u lands as
-    // u[4*q4 + i][16*vt + r], the order stage 2 subtracts it in.
-#pragma unroll
-    for (int kt = 0; kt < 8; ++kt)
-        lds_put(sT, r, colbase, kt,
-                pack4(elem(vp, 4 * kt) * beta, elem(vp, 4 * kt + 1) * beta,
-                      elem(vp, 4 * kt + 2) * beta, elem(vp, 4 * kt + 3) * beta));
-    wave_lds_fence();
+    // u[4*q4 + i][16*vt + r], the order stage 2 subtracts it in.  The
+    // transposes below go through the matrix core (tile_T).
     {
-        i16x4 vbT[8];
-        load_lds_T(sT, r, q4, vbT);
 #pragma unroll
         for (int vt = 0; vt < 8; ++vt) {
+            const i16x4 vbT = tile_T(pack4(elem(vp, 4 * vt) * beta, elem(vp, 4 * vt + 1) * beta,
+                                           elem(vp, 4 * vt + 2) * beta, elem(vp, 4 * vt + 3) * beta),
+                                     eye);
             const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-            const u32x2 ub = pack4(mfma_bf16_16x16x16(A_op, vbT[vt], zero));
+            const u32x2 ub = pack4(mfma_bf16_16x16x16(A_op, vbT, zero));
             *reinterpret_cast<u32x2*>(rec + REC_U + vt * 512 + lane * 8) = ub;
             if (p.dbg_u) {
 #pragma unroll
@@ -456,13 +415,12 @@ __device__ __forceinline__ void k1_compute(const Params& p, int hv, int c, const
             }
         }
     }
-    wave_lds_fence();
 
     // ---- w = A @ bf16(bf16(k^ * beta) * 2^G) (kernels.py:171-172), and
     // qg = bf16(q^ * 2^G), the gated query stage 2 multiplies the state by
     // (kernels.py:269).  w is computed transposed, w^T = kb^T @ A^T, so that
     // tile kt lands as w[r][16*kt + 4*q4 + i]: F order, stage 2's operand.
-    u32x2 qgp[8];
+    u32x2 qgp[8], kbF[8];
 #pragma unroll
     for (int kt = 0; kt < 8; ++kt) {
         float kb[4], qg[4], e[4];
@@ -472,7 +430,7 @@ __device__ __forceinline__ void k1_compute(const Params& p, int hv, int c, const
             kb[i] = round_bf(elem(kp, 4 * kt + i) * beta) * e[i];
             qg[i] = elem(qp, 4 * kt + i) * e[i];
         }
-        lds_put(sT, r, colbase, kt, pack4(kb[0], kb[1], kb[2], kb[3]));
+        kbF[kt] = pack4(kb[0], kb[1], kb[2], kb[3]);
         qgp[kt] = pack4(qg[0], qg[1], qg[2], qg[3]);
         // the state's decay 2^G_last (kernels.py:282-290): on the chunk's
         // last row, 2^G is it
@@ -487,50 +445,40 @@ __device__ __forceinline__ void k1_compute(const Params& p, int hv, int c, const
             *reinterpret_cast<u32x4*>(rec + REC_QG + j * 1024 + lane * 16) = qgj;
         }
     }
-    wave_lds_fence();
     // The record holds -w (stage 2 forms u - w @ hc^T as one accumulation
     // that starts at u): the product with -A, exact since negation commutes
     // with the bf16 products, the fp32 sums and the rounding.
     u32x2 wpk[8];
-    {
-        i16x4 kbT[8];
-        load_lds_T(sT, r, q4, kbT);
 #pragma unroll
-        for (int kt = 0; kt < 8; ++kt) {
-            const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-            wpk[kt] = pack4(mfma_bf16_16x16x16(kbT[kt], A_neg, zero));
-        }
+    for (int kt = 0; kt < 8; ++kt) {
+        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+        wpk[kt] = pack4(mfma_bf16_16x16x16(tile_T(kbF[kt], eye), A_neg, zero));
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const u32x4 wj = {wpk[2 * j].x, wpk[2 * j].y, wpk[2 * j + 1].x, wpk[2 * j + 1].y};
         *reinterpret_cast<u32x4*>(rec + REC_W + j * 1024 + lane * 16) = wj;
     }
-    wave_lds_fence();
 
     // ---- kg = bf16(k^ * 2^(G_last - G)) (kernels.py:282-290), stored in T
     // order (stage 2's A operand).
     bcast_last([&](auto from_last) {
 #pragma unroll
-        for (int kt = 0; kt < 8; ++kt) {
-            float kg[4];
+        for (int j = 0; j < 4; ++j) {
+            u32x2 kgT[2];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                kg[i] = elem(kp, 4 * kt + i) * fast_exp2(from_last(G[4 * kt + i]) - G[4 * kt + i]);
-            lds_put(sT, r, colbase, kt, pack4(kg[0], kg[1], kg[2], kg[3]));
+            for (int h = 0; h < 2; ++h) {
+                const int kt = 2 * j + h;
+                float kg[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    kg[i] = elem(kp, 4 * kt + i) * fast_exp2(from_last(G[4 * kt + i]) - G[4 * kt + i]);
+                kgT[h] = __builtin_bit_cast(u32x2, tile_T(pack4(kg[0], kg[1], kg[2], kg[3]), eye));
+            }
+            *reinterpret_cast<u32x4*>(rec + REC_KG + j * 1024 + lane * 16) =
+                u32x4{kgT[0].x, kgT[0].y, kgT[1].x, kgT[1].y};
         }
     });
-    wave_lds_fence();
-    {
-        i16x4 kgT[8];
-        load_lds_T(sT, r, q4, kgT);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const u32x2 a = __builtin_bit_cast(u32x2, kgT[2 * j]);
-            const u32x2 bq = __builtin_bit_cast(u32x2, kgT[2 * j + 1]);
-            *reinterpret_cast<u32x4*>(rec + REC_KG + j * 1024 + lane * 16) = u32x4{a.x, a.y, bq.x, bq.y};
-        }
-    }
 
     // ---- optional reference-layout intermediates (kernels.py:125,153,178-184)
     if (p.dbg_w && valid) {
@@ -551,13 +499,13 @@ __device__ __forceinline__ void k1_compute(const Params& p, int hv, int c, const
 // row-validity selects and the rows mid = 8, last = 15 are compile-time.
 // GB16: g is bf16 (else fp32).
 template <int K1M, bool FULL, bool GB16>
-__device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const SeqSpan& sp, uint16_t* sT,
+__device__ __forceinline__ void k1_chunk(const Params& p, int hv, int c, const SeqSpan& sp,
                                          float* sL, float* sX, uint8_t* rec) {
     K1In<GB16, K1M == K1_BOTH> in;
     k1_load<K1M, FULL, GB16>(p, hv, c, sp, in);
     const float* biasp = k1_bias(p, hv);
     const float ea = k1_ea(p, hv);
-    k1_compute<K1M, FULL, GB16>(p, hv, c, sp, in, biasp, ea, sT, sL, sX, rec);
+    k1_compute<K1M, FULL, GB16>(p, hv, c, sp, in, biasp, ea, sL, sX, rec);
 }
 
 }  // namespace
