@@ -59,7 +59,6 @@ __device__ __forceinline__ i16x4 tile_T(u32x2 f, i16x4 eye) {
     return as_i16x4(pack4(mfma_bf16_16x16x16(as_i16x4(f), eye, zero)));
 }
 
-
 // LDS scratch of one wave's k1_chunk: L and the solve's columns (fp32), in
 // bytes.
 constexpr int K1_SCRATCH_L = BT * BT * 4;
