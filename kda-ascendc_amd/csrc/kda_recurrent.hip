@@ -47,10 +47,28 @@ __device__ __forceinline__ float load_scalar(const void* base, int is_bf16, int6
                    : static_cast<const float*>(base)[i];
 }
 
-// Sum over the 32 lanes of a half-wave; every lane receives it.
+// Sum over the 32 lanes of a half-wave; every lane receives it.  Within a
+// 16-lane row by DPP: quad_perm pairs lanes 1 and 2 apart, then
+// row_half_mirror pairs the two quads of each half-row and row_mirror the two
+// half-rows (after each step all lanes of the group hold the same value, so
+// any pairing across groups adds the same two values); across the two rows
+// of the half-wave by one swizzle (lane ^ 16).  Every lane adds the same
+// operands in the same order, so all receive the same bits.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xf, 0xf, true));
+}
 __device__ __forceinline__ float half_sum(float x) {
-#pragma unroll
-    for (int m = 16; m >= 1; m >>= 1) x += __shfl_xor(x, m, 32);
+    constexpr int QP_XOR1 = 0xB1;          // quad_perm [1,0,3,2]
+    constexpr int QP_XOR2 = 0x4E;          // quad_perm [2,3,0,1]
+    constexpr int ROW_HALF_MIRROR = 0x141;
+    constexpr int ROW_MIRROR = 0x140;
+    x += dpp_f<QP_XOR1>(x);
+    x += dpp_f<QP_XOR2>(x);
+    x += dpp_f<ROW_HALF_MIRROR>(x);
+    x += dpp_f<ROW_MIRROR>(x);
+    // ds_swizzle bit mode: and_mask 0x1f, or_mask 0, xor_mask 0x10
+    x += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), 0x401F));
     return x;
 }
 
@@ -140,8 +158,12 @@ __device__ __forceinline__ void store_o(const Params& p, int64_t idx, float x) {
     }
 }
 
-template <bool VFIRST>
-__global__ __launch_bounds__(RT) void recurrent_kernel(Params p) {
+// ONE: a fixed-length batch of single tokens (the decode step): no token
+// loop and no next-token prefetch, which leaves room for four waves per
+// SIMD, so the 4 x 256 work-groups a CU holds stream the states in whole
+// rounds.
+template <bool VFIRST, bool ONE>
+__global__ __launch_bounds__(RT) __attribute__((amdgpu_waves_per_eu(ONE ? 4 : 1))) void recurrent_kernel(Params p) {
     const int HV = p.HV, H = p.H;
     const int bhv = blockIdx.x;  // (batch row or sequence) * HV + hv
     const int hv = bhv - (bhv / HV) * HV;
@@ -180,9 +202,10 @@ __global__ __launch_bounds__(RT) void recurrent_kernel(Params p) {
     const bool vlane = VFIRST ? t < 32 : true;  // V-first: threads that stage v
 
     TokRaw cur, nxt;
-    if (sp.len > 0) load_tok<VFIRST>(p, sp, 0, h, hv, t, cur);
-    for (int tt = 0; tt < sp.len; ++tt) {
-        if (tt + 1 < sp.len) load_tok<VFIRST>(p, sp, tt + 1, h, hv, t, nxt);
+    const int len = ONE ? 1 : sp.len;
+    if (len > 0) load_tok<VFIRST>(p, sp, 0, h, hv, t, cur);
+    for (int tt = 0; tt < len; ++tt) {
+        if (!ONE && tt + 1 < len) load_tok<VFIRST>(p, sp, tt + 1, h, hv, t, nxt);
         const int64_t rv = (sp.tok0 + tt) * HV + hv;
         const bool chunk_start = (tt % BT) == 0;
         float beta = cur.beta;
@@ -313,7 +336,7 @@ __global__ __launch_bounds__(RT) void recurrent_kernel(Params p) {
                 }
             }
         }
-        if (tt + 1 < sp.len) cur = nxt;
+        if (!ONE && tt + 1 < len) cur = nxt;
     }
 
     if (p.ht) {
@@ -327,11 +350,10 @@ __global__ __launch_bounds__(RT) void recurrent_kernel(Params p) {
 
 hipError_t launch_recurrent(const Params& p, hipStream_t stream) {
     const int64_t grid = (int64_t)(p.cu_seqlens ? p.N : p.B) * p.HV;
-    if (p.h0_v_first) {
-        hipLaunchKernelGGL(recurrent_kernel<true>, dim3((unsigned)grid), dim3(RT), 0, stream, p);
-    } else {
-        hipLaunchKernelGGL(recurrent_kernel<false>, dim3((unsigned)grid), dim3(RT), 0, stream, p);
-    }
+    const bool one = !p.cu_seqlens && p.T == 1;
+    auto kern = p.h0_v_first ? (one ? recurrent_kernel<true, true> : recurrent_kernel<true, false>)
+                             : (one ? recurrent_kernel<false, true> : recurrent_kernel<false, false>);
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(RT), 0, stream, p);
     return hipGetLastError();
 }
 
