@@ -100,14 +100,8 @@ __device__ __forceinline__ void lds_get8(const float* src, float (&x)[8]) {
     }
 }
 
-// Sum over the 16 threads of a row (lanes 16*m .. 16*m + 15 of a wave).
-__device__ __forceinline__ float row_sum16(float s) {
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
-    s += __shfl_xor(s, 4);
-    s += __shfl_xor(s, 8);
-    return s;
-}
+// (row_sum16, kda_common.h: the sum over the 16 threads of a row, lanes
+// 16*m .. 16*m + 15 of a wave)
 
 // One value head's row data of this thread (row i, columns c0 .. c0+7):
 // g is the gate's argument g + dt_bias with the in-kernel gate, else g.
@@ -447,7 +441,7 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(GROUP ? 1 : 
                     sm.dkg[row][16 * kt + x] = ak[tt][e];
                 }
                 float s2 = pel[tt];
-                s2 += __shfl_xor(s2, 16);
+                s2 += xor16(s2);
                 s2 += __shfl_xor(s2, 32);
                 if (q4 == 0) sm.del[16 * kt + x] = s2;
             }
@@ -682,8 +676,9 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(GROUP ? 1 : 
                     sal += sm.dqg[r][t];
                 }
                 p.tr_part[rec * PART_STRIDE + t] = sdt;
-#pragma unroll
-                for (int o = 1; o < 64; o <<= 1) sal += __shfl_xor(sal, o);
+                sal = row_sum16(sal);
+                sal += xor16(sal);
+                sal += __shfl_xor(sal, 32);
                 if (lane == 0) sm.red[w] = sal;
             }
             __syncthreads();

@@ -296,6 +296,33 @@ __device__ __forceinline__ float row_bcast(float v) {
                                                                  false));
 }
 
+// Sum over each 16-lane row, every lane receiving it, by DPP: quad_perm
+// pairs lanes 1 and 2 apart, then row_half_mirror pairs the two quads of
+// each half-row and row_mirror the two half-rows.  After each step the
+// lanes of a group hold the same value, so the last two steps add what
+// lane ^ 4 and lane ^ 8 would: the bits of the shuffle tree over 1, 2, 4, 8.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xf, 0xf, true));
+}
+__device__ __forceinline__ float row_sum16(float x) {
+    constexpr int QP_XOR1 = 0xB1;  // quad_perm [1,0,3,2]
+    constexpr int QP_XOR2 = 0x4E;  // quad_perm [2,3,0,1]
+    constexpr int ROW_HALF_MIRROR = 0x141;
+    constexpr int ROW_MIRROR = 0x140;
+    x += dpp_mov<QP_XOR1>(x);
+    x += dpp_mov<QP_XOR2>(x);
+    x += dpp_mov<ROW_HALF_MIRROR>(x);
+    x += dpp_mov<ROW_MIRROR>(x);
+    return x;
+}
+
+// The value of lane ^ 16 (within each 32 lanes), by ds_swizzle in bit mode:
+// and_mask 0x1f, or_mask 0, xor_mask 0x10.
+__device__ __forceinline__ float xor16(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), 0x401F));
+}
+
 __device__ __forceinline__ float shfl(float x, int src_lane) {
     return __builtin_bit_cast(
         float, __builtin_amdgcn_ds_bpermute(src_lane << 2, __builtin_bit_cast(int, x)));

@@ -200,8 +200,8 @@ __device__ __forceinline__ void k1_compute(const Params& p, int hv, int c, const
             sq = fmaf(elem(qp, j), elem(qp, j), sq);
             sk = fmaf(elem(kp, j), elem(kp, j), sk);
         }
-        sq += __shfl_xor(sq, 16);
-        sk += __shfl_xor(sk, 16);
+        sq += xor16(sq);
+        sk += xor16(sk);
         sq += __shfl_xor(sq, 32);
         sk += __shfl_xor(sk, 32);
         const float rq = 1.f / sqrtf(sq + L2_EPS);

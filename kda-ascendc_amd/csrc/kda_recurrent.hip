@@ -47,29 +47,12 @@ __device__ __forceinline__ float load_scalar(const void* base, int is_bf16, int6
                    : static_cast<const float*>(base)[i];
 }
 
-// Sum over the 32 lanes of a half-wave; every lane receives it.  Within a
-// 16-lane row by DPP: quad_perm pairs lanes 1 and 2 apart, then
-// row_half_mirror pairs the two quads of each half-row and row_mirror the two
-// half-rows (after each step all lanes of the group hold the same value, so
-// any pairing across groups adds the same two values); across the two rows
-// of the half-wave by one swizzle (lane ^ 16).  Every lane adds the same
+// Sum over the 32 lanes of a half-wave; every lane receives it: each 16-lane
+// row by DPP, then the two rows by one swizzle.  Every lane adds the same
 // operands in the same order, so all receive the same bits.
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float x) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xf, 0xf, true));
-}
 __device__ __forceinline__ float half_sum(float x) {
-    constexpr int QP_XOR1 = 0xB1;          // quad_perm [1,0,3,2]
-    constexpr int QP_XOR2 = 0x4E;          // quad_perm [2,3,0,1]
-    constexpr int ROW_HALF_MIRROR = 0x141;
-    constexpr int ROW_MIRROR = 0x140;
-    x += dpp_f<QP_XOR1>(x);
-    x += dpp_f<QP_XOR2>(x);
-    x += dpp_f<ROW_HALF_MIRROR>(x);
-    x += dpp_f<ROW_MIRROR>(x);
-    // ds_swizzle bit mode: and_mask 0x1f, or_mask 0, xor_mask 0x10
-    x += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), 0x401F));
-    return x;
+    x = row_sum16(x);
+    return x + xor16(x);
 }
 
 __device__ __forceinline__ float sigmoid_precise(float x) { return 1.0f / (1.0f + expf(-x)); }
