@@ -249,11 +249,10 @@ __global__ __launch_bounds__(RT) __attribute__((amdgpu_waves_per_eu(ONE ? 4 : 1)
                 float k0 = lo16(cur.k.x), k1 = hi16(cur.k.x);
                 if (p.use_l2norm) {
                     float sq = fmaf(q0, q0, q1 * q1), sk = fmaf(k0, k0, k1 * k1);
-#pragma unroll
-                    for (int m = 32; m >= 1; m >>= 1) {
-                        sq += __shfl_xor(sq, m, 64);
-                        sk += __shfl_xor(sk, m, 64);
-                    }
+                    sq = half_sum(sq);
+                    sk = half_sum(sk);
+                    sq += __shfl_xor(sq, 32, 64);
+                    sk += __shfl_xor(sk, 32, 64);
                     const float nq = sqrtf(sq + L2_EPS), nk = sqrtf(sk + L2_EPS);
                     q0 /= nq; q1 /= nq;
                     k0 /= nk; k1 /= nk;
