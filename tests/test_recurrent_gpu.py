@@ -8,7 +8,8 @@ Bars (written in each test):
   only in summation order);
 * bf16 output = the fp32 output rounded to nearest even, bit for bit;
 * T decode steps with the state updated in place = one call over T tokens,
-  bit for bit;
+  bit for bit (the steps run the kernel's one-token variant, the single
+  call its general one);
 * chunked path at B=1 T=8192 H=32 vs this gold: max-abs error of o and ht
   no worse than 1.5x the reference chunked path's own error (the oracle in
   kernel mode) on the same inputs, plus 1e-5.
