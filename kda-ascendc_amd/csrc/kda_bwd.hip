@@ -139,8 +139,10 @@ struct HdhOps {
 // GROUP: grouped value heads (HV > H), the value heads of a q/k head in a
 // loop.  Without it the body runs once, and the compiler keeps nothing live
 // across iterations (hoisted addresses and row values would otherwise hold
-// registers through the whole body).
-template <bool GROUP>
+// registers through the whole body).  FULL: a fixed-length batch with T a
+// multiple of 16, so every row of every chunk is a token (no row-validity
+// selects).
+template <bool GROUP, bool FULL>
 __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(GROUP ? 1 : 2))) void bwd_chunk_kernel(Params p) {
     __shared__ ChunkSmem sm;
     const int t = threadIdx.x;
@@ -176,7 +178,7 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(GROUP ? 1 : 
     const SeqSpan sq = seq_span(p, seq * HV + h * rep);
     const int nvalid = min(BT, sq.len - c * BT);
     const int mid = min(BT / 2, nvalid - 1), last = nvalid - 1;
-    const bool valid = i < nvalid;
+    const bool valid = FULL || i < nvalid;
     const int64_t tok = sq.tok0 + c * BT + i;
 
     // Every load of a value head is issued before the first wait.  Rows
@@ -754,11 +756,10 @@ __global__ __launch_bounds__(RG * DK) void gate_reduce_kernel(Params p) {
 
 hipError_t launch_bwd_chunk(const Params& p, hipStream_t stream) {
     const int64_t grid = p.cu_seqlens ? (int64_t)p.H * p.NS : (int64_t)p.B * p.H * p.NT;
-    if (p.HV > p.H) {
-        hipLaunchKernelGGL(bwd_chunk_kernel<true>, dim3((unsigned)grid), dim3(CT), 0, stream, p);
-    } else {
-        hipLaunchKernelGGL(bwd_chunk_kernel<false>, dim3((unsigned)grid), dim3(CT), 0, stream, p);
-    }
+    const bool full = !p.cu_seqlens && p.T % BT == 0;
+    auto kern = p.HV > p.H ? (full ? bwd_chunk_kernel<true, true> : bwd_chunk_kernel<true, false>)
+                           : (full ? bwd_chunk_kernel<false, true> : bwd_chunk_kernel<false, false>);
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(CT), 0, stream, p);
     return hipGetLastError();
 }
 
