@@ -729,7 +729,9 @@ __global__ __launch_bounds__(RG * DK) void gate_reduce_kernel(Params p) {
     for (int b = 0; b < nb; ++b) {
         const int64_t first = p.cu_seqlens ? (int64_t)hv * p.NS : (int64_t)(b * p.HV + hv) * p.NT;
         const float* base = p.tr_part + first * PART_STRIDE;
-#pragma unroll 4
+        // sixteen records' loads in flight before the adds, which keep
+        // their order (the sums stay bit for bit those of a plain loop)
+#pragma unroll 16
         for (int x = grp; x < nr; x += RG) {
             acc += base[(int64_t)x * PART_STRIDE + t];
             if (t == 0) accA += base[(int64_t)x * PART_STRIDE + DK];
