@@ -147,10 +147,11 @@ size_t kda_bt16_workspace_bytes_args(const KdaBt16Args* args);
 
 /* Full forward on `stream` (a hipStream_t; NULL is the legacy default
  * stream).  Replaces _run's two launches, kernels.py:581-602: stage 1 then
- * stage 2 (kda_bt16_k1_hip, kda_bt16_k2_hip), or, when there are at least as
- * many (sequence, value head) pairs as the device has CUs and no debug
- * output is asked for, one fused kernel that keeps stage 1's per-chunk
- * records in LDS instead of the workspace (same results bit for bit).
+ * stage 2 (kda_bt16_k1_hip, kda_bt16_k2_hip), or, when there are more
+ * (sequence, value head) pairs than half the device's CUs (with cu_seqlens:
+ * at least as many as its CUs) and no debug output is asked for, one fused
+ * kernel that keeps stage 1's per-chunk records in LDS instead of the
+ * workspace (same results bit for bit).
  * KDA_BT16_FUSED_KERNEL in args->flags fuses whatever the count; without
  * it, the environment variable KDA_BT16_FUSED=0 keeps the two stages and =1
  * fuses.  Debug outputs always take the two stages.  The workspace is

@@ -1,5 +1,5 @@
-// The KDA BT=16 forward in one kernel, for shapes with at least as many
-// (sequence, head) pairs as CUs (batched and varlen prefill).
+// The KDA BT=16 forward in one kernel, for shapes with more (sequence, head)
+// pairs than half the CUs (batched and varlen prefill).
 //
 // The two-stage forward (kda_k1.hip, then kda_k2.hip / kda_k2w.hip) passes
 // each chunk's 17 KiB record through HBM: written by stage 1, read back by
@@ -346,8 +346,18 @@ __global__ __launch_bounds__(F_THREADS) void fused_kernel(Params p) {
 // Whether the forward runs as one fused kernel: never when the
 // reference-layout intermediates are asked for (those come from stage 1);
 // always when the caller asks for it (the reference's use_fused_kernel);
-// else KDA_BT16_FUSED=0 keeps the two stages and =1 fuses; else at least as
-// many (sequence, head) pairs as CUs.
+// else KDA_BT16_FUSED=0 keeps the two stages and =1 fuses; else, with fixed
+// length, more (sequence, head) pairs than half the CUs, and with cu_seqlens
+// at least as many pairs as CUs.
+//
+// Below the CU count the fused kernel runs every pair in one round of
+// work-groups, about 1.85 us per chunk whatever their number, while the two
+// stages grow with the pairs (T=4096 forwards, two stages against fused: 128
+// pairs 377 against 476 us, 160 pairs 505 against 480, 224 pairs 658 against
+// 479).  With cu_seqlens the fused kernel's time follows the longest
+// sequence and stage 1's the total; the host never reads cu_seqlens, and a
+// single long sequence among short ones would make the lower threshold up
+// to about twice slower, so there the pairs must fill the CUs.
 bool fused_forward(const Params& p, int ncu) {
     if (p.dbg_w || p.dbg_u || p.dbg_Aqk || p.dbg_A_inv || p.dbg_g) return false;
     if (p.force_fused) return true;
@@ -356,7 +366,7 @@ bool fused_forward(const Params& p, int ncu) {
         if (atoi(e) == 0) return false;
         if (atoi(e) == 1) return true;
     }
-    return nbh >= ncu;
+    return p.cu_seqlens ? nbh >= ncu : 2 * nbh > ncu;
 }
 
 hipError_t launch_fused(const Params& p, hipStream_t stream) {

@@ -188,8 +188,12 @@ __global__ __launch_bounds__((WideGeom<TPW, TW>::THREADS)) void k2w_kernel(Param
 }  // namespace
 
 // Value tiles per work-group of the wide stage 2, or 0 for kda_k2.hip's one
-// tile per work-group: several tiles once (sequences x heads x 8 tiles)
-// exceed the CUs, as many as still leave about one work-group per CU.
+// tile per work-group: the fewest tiles (1, 2, 4, 8) that keep the
+// (sequences x heads x 8 / tiles) work-groups within one per CU.  A second
+// round of work-groups costs more than wider ones: B=2 T=8192 H=32 (64
+// pairs) runs stage 2 in 196 us with 2 tiles, 233 with 4 and 321 with 1;
+// B=4 T=4096 H=32 (128 pairs) in 156 us with 4 tiles, 193 with 2 and 198
+// with 8.
 int k2_wide_tiles(const Params& p, int ncu) {
     const int64_t nbh = (int64_t)(p.cu_seqlens ? p.N : p.B) * p.HV;
     if (const char* e = getenv("KDA_BT16_K2_TILES")) {
@@ -198,8 +202,9 @@ int k2_wide_tiles(const Params& p, int ncu) {
         if (t == 2 || t == 4 || t == 8) return t;
     }
     if (nbh * 8 <= ncu) return 0;
-    if (nbh * 2 >= ncu) return 8;
-    return 4;
+    if (nbh * 4 <= ncu) return 2;
+    if (nbh * 2 <= ncu) return 4;
+    return 8;
 }
 
 namespace {

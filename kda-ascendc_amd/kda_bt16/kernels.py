@@ -20,9 +20,10 @@ Differences from the reference, all supersets of its contract:
 * ``use_fused_kernel=True`` runs the fused kernel (one work-group per
   sequence and value head, stage 1's records kept in LDS: the reference's
   single-kernel variant, kernels.py:305-472) whatever the geometry; without
-  it the forward fuses when the (sequence, head) pairs are at least as many
-  as the CUs.  Both give the two-stage results bit for bit (the reference's
-  own test requires the two to agree, tests/test_kda_bt16.py:174-200);
+  it the forward fuses when the (sequence, head) pairs are more than half
+  the CUs (with ``cu_seqlens``: at least as many as the CUs).  Both give
+  the two-stage results bit for bit (the reference's own test requires the
+  two to agree, tests/test_kda_bt16.py:174-200);
 * ``HV`` may be any multiple of ``H`` (grouped value heads: value head hv
   reads q/k head hv // (HV // H), the indexing of kernels.py:88, which the
   reference's validation does not yet admit, kernels.py:729-730);

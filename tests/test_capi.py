@@ -141,6 +141,28 @@ def test_forward_plan_reads_no_device_memory(monkeypatch):
     assert f(ctypes.byref(_args(flags=_hip.FUSED_KERNEL, **ten, **dbg))) == 0
 
 
+def test_forward_plan_thresholds(monkeypatch):
+    """Without the flag or the environment, fixed length fuses once the
+    (sequence, value head) pairs are more than half the CUs, cu_seqlens once
+    they are at least as many as the CUs.  Without a GPU the library counts
+    256 CUs, the MI355X's count."""
+    monkeypatch.delenv("KDA_BT16_FUSED", raising=False)
+    f = _hip.lib().kda_bt16_fwd_plan
+    fake = 1 << 40
+    ten = dict(q=fake, k=fake, v=fake, g=fake, beta=fake, o=fake)
+
+    def plan(**kw):
+        return f(ctypes.byref(_args(**ten, **kw)))
+
+    assert plan(B=1, H=128, HV=128) == 0
+    assert plan(B=1, H=129, HV=129) == 1
+    assert plan(B=2, H=32, HV=64) == 0  # 128 pairs through grouped value heads
+    assert plan(B=5, H=32, HV=32) == 1
+    cu = dict(cu_seqlens=fake, cu_seqlens_dtype=_hip.DTYPE_I32, T=4096)
+    assert plan(N=7, H=32, HV=32, **cu) == 0  # 224 pairs
+    assert plan(N=8, H=32, HV=32, **cu) == 1  # 256 pairs
+
+
 def test_workspace_checked_before_launch():
     fake = 1 << 40  # never dereferenced: the size check fails first
     a = _args(q=fake, k=fake, v=fake, g=fake, beta=fake, o=fake, workspace=fake, workspace_bytes=100)

@@ -5,12 +5,12 @@ the fused kernel runs stage 1's per-chunk code and the wide stage 2's step
 record lives differs.
 
 ``KDA_BT16_FUSED`` forces the choice over the launch heuristic (0: two
-stages; 1: fused), which fuses when the (sequence, head) pairs are at least
-as many as the CUs.  The cases cover what the record ring has edges at:
-fewer chunks than ring slots, counts that are and are not multiples of the
-ring and of the producer count, partial last chunks, empty sequences in a
-varlen batch, grouped value heads, both state layouts, fp32 and bf16 gates,
-and the precomputed-gate mode.
+stages; 1: fused), which fuses when the (sequence, head) pairs are more than
+half the CUs (with cu_seqlens: at least as many as the CUs).  The cases
+cover what the record ring has edges at: fewer chunks than ring slots,
+counts that are and are not multiples of the ring and of the producer count,
+partial last chunks, empty sequences in a varlen batch, grouped value heads,
+both state layouts, fp32 and bf16 gates, and the precomputed-gate mode.
 """
 
 from __future__ import annotations

@@ -221,7 +221,9 @@ def test_varlen_multi_sequence_work_groups(with_h0, with_ht, vfirst, k2_tiles, g
     """Several sequences per stage-2 work-group (KDA_BT16_K2_TILES=1 forces
     the one-tile kernel, which then groups sequences) and the default, which
     takes several value tiles per work-group here; each sequence equals its
-    own call."""
+    own call.  KDA_BT16_FUSED=0 keeps the two stages: with 320 (sequence,
+    head) pairs the forward would otherwise run the fused kernel."""
+    monkeypatch.setenv("KDA_BT16_FUSED", "0")
     if k2_tiles is None:
         monkeypatch.delenv("KDA_BT16_K2_TILES", raising=False)
     else:
