@@ -28,6 +28,9 @@ headline metric):
   --workload decode   one decode step (T = 1, state updated in place) for
                       B = 128 sequences of 32 heads: the token recurrence,
                       bound by reading and writing the fp32 states.
+  --workload dispatch the forward at shapes around its dispatch boundaries
+                      (40-224 (sequence, head) pairs), every choice forced
+                      and the library's own; a table, not a metric line.
 """
 
 from __future__ import annotations
@@ -495,6 +498,67 @@ def run_decode(args, dev) -> dict:
     }
 
 
+# (B, T, H) shapes around the forward's dispatch boundaries: stage-2 value
+# tiles per work-group (1, 2, 4, 8) and fused against two stages.
+DISPATCH_SHAPES = [(1, 4096, 40), (1, 4096, 48), (1, 4096, 64), (1, 4096, 80), (1, 4096, 128),
+                   (1, 4096, 160), (1, 4096, 192), (1, 4096, 224), (1, 2048, 160), (1, 2048, 224)]
+
+
+def run_dispatch(args, dev) -> dict:
+    """The forward at each DISPATCH_SHAPES shape with every choice forced
+    (KDA_BT16_FUSED=0 and KDA_BT16_K2_TILES=1|2|4|8 for the two stages,
+    use_fused_kernel=True for the fused kernel) and with the library's own
+    choice, HIP events over ``steps`` calls after ``warmup`` (µs per call),
+    the faster of two rounds.  Every choice gives the same bits; this only
+    measures which is fastest."""
+    rows = []
+    for B, T, Hs in DISPATCH_SHAPES:
+        gen = torch.Generator(device=dev).manual_seed(3)
+        q, k, v, g = (torch.randn(B, T, Hs, D, device=dev, generator=gen).bfloat16()
+                      for _ in range(4))
+        beta = torch.randn(B, T, Hs, device=dev, generator=gen).bfloat16()
+        A_log = torch.log(torch.rand(Hs, device=dev, generator=gen) * 15.0 + 1.0)
+        dt_bias = torch.randn(Hs * D, device=dev, generator=gen) * 0.1
+        kw = dict(scale=SCALE, output_final_state=True, use_qk_l2norm_in_kernel=True,
+                  use_gate_in_kernel=True, use_beta_sigmoid_in_kernel=True,
+                  lower_bound=LOWER_BOUND, A_log=A_log, dt_bias=dt_bias)
+
+        def timed(**over):
+            fn = lambda: kda_bt16_fwd(q, k, v, g, beta, **kw, **over)  # noqa: E731
+            for _ in range(args.warmup):
+                fn()
+            return round(time_events(fn, args.steps) * 1e3, 1)
+
+        row = {"B": B, "T": T, "H": Hs, "pairs": B * Hs}
+        saved = {n: os.environ.get(n) for n in ("KDA_BT16_FUSED", "KDA_BT16_K2_TILES")}
+        # two rounds over the choices, the faster of each choice's two timings:
+        # a two-stage timing taken right after the fused kernel reads a few
+        # percent slow, so the fused kernel comes last in each round
+        choices = [(f"two_stage_{t}_tiles_us", {"KDA_BT16_FUSED": "0", "KDA_BT16_K2_TILES": str(t)}, {})
+                   for t in (1, 2, 4, 8)]
+        choices += [("library_choice_us", {}, {}), ("fused_us", {}, {"use_fused_kernel": True})]
+        try:
+            for _ in range(2):
+                for key, env, over in choices:
+                    for n in saved:
+                        os.environ.pop(n, None)
+                    os.environ.update(env)
+                    t_us = timed(**over)
+                    row[key] = min(row.get(key, t_us), t_us)
+        finally:
+            for n, val in saved.items():
+                if val is None:
+                    os.environ.pop(n, None)
+                else:
+                    os.environ[n] = val
+        rows.append(row)
+        print(f"# {row}", file=sys.stderr, flush=True)
+        del q, k, v, g, beta
+    return {"workload": "forward dispatch: stage-2 value tiles and fused against two stages, "
+                        "K=V=128 bf16, all in-kernel flags",
+            "steps": args.steps, "warmup": args.warmup, "unit": "us per forward", "rows": rows}
+
+
 def precision_vs_recurrence(fwd_out, ins, kw) -> dict:
     """Max-abs error of o and ht against the token recurrence in fp32 on the
     GPU (kda_recurrent_fwd with an fp32 o: no rounding between tokens, the
@@ -661,7 +725,8 @@ def main() -> None:
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 256 MiB device copy (3 launches), the reference "
                          "kernel for scaling rocprof FETCH_SIZE / WRITE_SIZE to bytes")
-    ap.add_argument("--workload", choices=("headline", "config", "varlen", "decode", "train"),
+    ap.add_argument("--workload",
+                    choices=("headline", "config", "varlen", "decode", "train", "dispatch"),
                     default="headline")
     ap.add_argument("--config", choices=sorted(CONFIGS), default="c2",
                     help="BASELINE config of --workload config")
@@ -686,6 +751,9 @@ def main() -> None:
         del src, dst
     if args.workload == "decode":
         print(json.dumps(run_decode(args, dev)), flush=True)
+        return
+    if args.workload == "dispatch":
+        print(json.dumps(run_dispatch(args, dev)), flush=True)
         return
     inputs_cpu = make_inputs()
     if args.workload == "varlen":
