@@ -51,7 +51,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "kda-ascendc_amd"))
 
 from kda_bt16 import (  # noqa: E402
-    kda_bt16_fwd, kda_bt16_stage_launchers, kda_decode_step, kda_recurrent_fwd)
+    forward_choice, kda_bt16_fwd, kda_bt16_stage_launchers, kda_decode_step, kda_recurrent_fwd)
 
 METRIC = "KDA fwd tokens/sec and ms at B=1 T=8192 H=32 bf16; % HBM/MFMA roofline"
 B, T, H, D = 1, 8192, 32, 128
@@ -506,11 +506,12 @@ DISPATCH_SHAPES = [(1, 4096, 40), (1, 4096, 48), (1, 4096, 64), (1, 4096, 80), (
 
 def run_dispatch(args, dev) -> dict:
     """The forward at each DISPATCH_SHAPES shape with every choice forced
-    (KDA_BT16_FUSED=0 and KDA_BT16_K2_TILES=1|2|4|8 for the two stages,
-    use_fused_kernel=True for the fused kernel) and with the library's own
-    choice, HIP events over ``steps`` calls after ``warmup`` (µs per call),
-    the faster of two rounds.  Every choice gives the same bits; this only
-    measures which is fastest."""
+    through ``forward_choice`` (the C ABI's ``KDA_BT16_TWO_STAGE`` flag and
+    ``k2_tiles`` field: 1, 2, 4 or 8 value tiles per stage-2 work-group;
+    ``KDA_BT16_FUSED_KERNEL`` for the fused kernel) and with the library's
+    own choice, HIP events over ``steps`` calls after ``warmup`` (µs per
+    call), the faster of two rounds.  Every choice gives the same bits; this
+    only measures which is fastest."""
     rows = []
     for B, T, Hs in DISPATCH_SHAPES:
         gen = torch.Generator(device=dev).manual_seed(3)
@@ -523,40 +524,85 @@ def run_dispatch(args, dev) -> dict:
                   use_gate_in_kernel=True, use_beta_sigmoid_in_kernel=True,
                   lower_bound=LOWER_BOUND, A_log=A_log, dt_bias=dt_bias)
 
-        def timed(**over):
-            fn = lambda: kda_bt16_fwd(q, k, v, g, beta, **kw, **over)  # noqa: E731
-            for _ in range(args.warmup):
-                fn()
-            return round(time_events(fn, args.steps) * 1e3, 1)
+        def timed(**choice):
+            fn = lambda: kda_bt16_fwd(q, k, v, g, beta, **kw)  # noqa: E731
+            with forward_choice(**choice):
+                for _ in range(args.warmup):
+                    fn()
+                return round(time_events(fn, args.steps) * 1e3, 1)
 
         row = {"B": B, "T": T, "H": Hs, "pairs": B * Hs}
-        saved = {n: os.environ.get(n) for n in ("KDA_BT16_FUSED", "KDA_BT16_K2_TILES")}
         # two rounds over the choices, the faster of each choice's two timings:
         # a two-stage timing taken right after the fused kernel reads a few
         # percent slow, so the fused kernel comes last in each round
-        choices = [(f"two_stage_{t}_tiles_us", {"KDA_BT16_FUSED": "0", "KDA_BT16_K2_TILES": str(t)}, {})
-                   for t in (1, 2, 4, 8)]
-        choices += [("library_choice_us", {}, {}), ("fused_us", {}, {"use_fused_kernel": True})]
-        try:
-            for _ in range(2):
-                for key, env, over in choices:
-                    for n in saved:
-                        os.environ.pop(n, None)
-                    os.environ.update(env)
-                    t_us = timed(**over)
-                    row[key] = min(row.get(key, t_us), t_us)
-        finally:
-            for n, val in saved.items():
-                if val is None:
-                    os.environ.pop(n, None)
-                else:
-                    os.environ[n] = val
+        choices = [(f"two_stage_{t}_tiles_us", dict(fused=False, k2_tiles=t)) for t in (1, 2, 4, 8)]
+        choices += [("library_choice_us", {}), ("fused_us", dict(fused=True))]
+        for _ in range(2):
+            for key, choice in choices:
+                t_us = timed(**choice)
+                row[key] = min(row.get(key, t_us), t_us)
         rows.append(row)
         print(f"# {row}", file=sys.stderr, flush=True)
         del q, k, v, g, beta
     return {"workload": "forward dispatch: stage-2 value tiles and fused against two stages, "
                         "K=V=128 bf16, all in-kernel flags",
-            "steps": args.steps, "warmup": args.warmup, "unit": "us per forward", "rows": rows}
+            "steps": args.steps, "warmup": args.warmup, "unit": "us per forward", "rows": rows,
+            "varlen_rows": run_dispatch_varlen(args, dev)}
+
+
+# Packed sequences (cu_seqlens, 32 heads) at or above the CU count of
+# (sequence, head) pairs: one long sequence among short ones, and equal
+# lengths.
+DISPATCH_VARLEN = [("one_long", [16384] + [1024] * 7), ("equal", [2944] * 8),
+                   ("one_long_16", [8192] + [512] * 15)]
+
+
+def run_dispatch_varlen(args, dev) -> list:
+    """The varlen forward at each DISPATCH_VARLEN batch: the two stages and
+    the fused kernel forced, and the library's own choice without and with
+    the ``max_seqlen`` hint (which the fused-or-not choice weighs against
+    the longest sequence).  HIP events, µs per call, the faster of two
+    rounds."""
+    rows = []
+    Hs = 32
+    for name, lens in DISPATCH_VARLEN:
+        cu_list = [0]
+        for n in lens:
+            cu_list.append(cu_list[-1] + n)
+        T = cu_list[-1]
+        gen = torch.Generator(device=dev).manual_seed(5)
+        q, k, v, g = (torch.randn(1, T, Hs, D, device=dev, generator=gen).bfloat16()
+                      for _ in range(4))
+        beta = torch.randn(1, T, Hs, device=dev, generator=gen).bfloat16()
+        A_log = torch.log(torch.rand(Hs, device=dev, generator=gen) * 15.0 + 1.0)
+        dt_bias = torch.randn(Hs * D, device=dev, generator=gen) * 0.1
+        cu = torch.tensor(cu_list, dtype=torch.int32, device=dev)
+        kw = dict(scale=SCALE, output_final_state=True, use_qk_l2norm_in_kernel=True,
+                  use_gate_in_kernel=True, use_beta_sigmoid_in_kernel=True,
+                  lower_bound=LOWER_BOUND, A_log=A_log, dt_bias=dt_bias, cu_seqlens=cu)
+
+        def timed(choice, **over):
+            fn = lambda: kda_bt16_fwd(q, k, v, g, beta, **kw, **over)  # noqa: E731
+            with forward_choice(**choice):
+                for _ in range(args.warmup):
+                    fn()
+                return round(time_events(fn, args.steps) * 1e3, 1)
+
+        row = {"name": name, "lengths": lens, "T": T, "H": Hs, "pairs": len(lens) * Hs}
+        choices = [("two_stage_us", dict(fused=False), {}),
+                   ("library_choice_us", {}, {}),
+                   ("library_choice_max_seqlen_us", {}, {"max_seqlen": max(lens)}),
+                   ("fused_us", dict(fused=True), {})]
+        for _ in range(2):
+            for key, choice, over in choices:
+                t_us = timed(choice, **over)
+                row[key] = min(row.get(key, t_us), t_us)
+        best = min(row["two_stage_us"], row["fused_us"])
+        row["hinted_choice_within_3pct_of_best"] = row["library_choice_max_seqlen_us"] <= 1.03 * best
+        rows.append(row)
+        print(f"# {row}", file=sys.stderr, flush=True)
+        del q, k, v, g, beta
+    return rows
 
 
 def precision_vs_recurrence(fwd_out, ins, kw) -> dict:

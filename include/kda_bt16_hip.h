@@ -53,7 +53,7 @@
 extern "C" {
 #endif
 
-#define KDA_BT16_ABI_VERSION 3
+#define KDA_BT16_ABI_VERSION 4
 
 /* Flags: the reference's tl.constexpr switches (kernels.py:78-82, 208-212).
  * USE_INITIAL_STATE / STORE_FINAL_STATE / HAS_BIAS / STORE_A_INV follow from
@@ -75,6 +75,9 @@ extern "C" {
  * its single-kernel variant kernels.py:305-472).  Debug outputs still take
  * the two stages; the other entries ignore it. */
 #define KDA_BT16_FUSED_KERNEL      (1u << 6)
+/* The forward entries: run stage 1 then stage 2 whatever the (sequence,
+ * value head) count.  Not with KDA_BT16_FUSED_KERNEL (KDA_BT16_EINVAL). */
+#define KDA_BT16_TWO_STAGE         (1u << 7)
 
 /* Element types of g and beta, and of cu_seqlens. */
 #define KDA_BT16_DTYPE_F32  0
@@ -87,7 +90,10 @@ extern "C" {
 #define KDA_BT16_EINVAL            -1 /* null pointer, non-positive size, bad dtype tag,
                                          misaligned tensor (16 B; beta its element size;
                                          Aqk/A_inv 8 B; cu_seqlens its element size),
-                                         cu_seqlens with B != 1 or N <= 0 */
+                                         cu_seqlens with B != 1 or N <= 0, both
+                                         KDA_BT16_FUSED_KERNEL and KDA_BT16_TWO_STAGE,
+                                         k2_tiles not 0/1/2/4/8, k2_wave_tiles not 0/1/2,
+                                         max_seqlen < 0 */
 #define KDA_BT16_EUNSUPPORTED      -2 /* K != 128, V != 128 (kernels.py:727-728) or HV not
                                          a multiple of H; work beyond the 32-bit grids or
                                          per-sequence record sizes (T > 1973776), and
@@ -122,7 +128,8 @@ typedef struct KdaBt16Args {
     const float* h0;      /* optional initial state */
     void* o;              /* required */
     float* ht;            /* optional final state */
-    void* workspace;      /* kda_bt16_workspace_bytes() bytes, 256-byte aligned */
+    void* workspace;      /* kda_bt16_workspace_bytes() bytes, 256-byte aligned; not read
+                             (may be NULL) when the forward runs fused */
     size_t workspace_bytes;
     void* dbg_Aqk;        /* optional debug outputs, all or none */
     void* dbg_A_inv;
@@ -132,6 +139,14 @@ typedef struct KdaBt16Args {
     const void* cu_seqlens;   /* optional: packed sequences (varlen) */
     int32_t cu_seqlens_dtype; /* KDA_BT16_DTYPE_I32 or KDA_BT16_DTYPE_I64 */
     int32_t N;                /* number of sequences with cu_seqlens */
+    /* The forward's kernel choices (ABI 4).  Each 0 leaves the choice to
+     * the library; every choice gives the same results bit for bit. */
+    int32_t k2_tiles;         /* stage-2 value tiles per work-group: 1, 2, 4 or 8 */
+    int32_t k2_wave_tiles;    /* with 2-8 tiles per work-group, tiles per compute wave: 1 or 2 */
+    int32_t max_seqlen;       /* with cu_seqlens: the longest sequence's length, when the
+                                 caller knows it (a hint for the choice between the fused
+                                 kernel and the two stages; a wrong value changes only the
+                                 choice, never the results) */
 } KdaBt16Args;
 
 /* Bytes of scratch the two stages exchange for a fixed-length geometry (one
@@ -147,15 +162,22 @@ size_t kda_bt16_workspace_bytes_args(const KdaBt16Args* args);
 
 /* Full forward on `stream` (a hipStream_t; NULL is the legacy default
  * stream).  Replaces _run's two launches, kernels.py:581-602: stage 1 then
- * stage 2 (kda_bt16_k1_hip, kda_bt16_k2_hip), or, when there are more
- * (sequence, value head) pairs than half the device's CUs (with cu_seqlens:
- * at least as many as its CUs) and no debug output is asked for, one fused
- * kernel that keeps stage 1's per-chunk records in LDS instead of the
- * workspace (same results bit for bit).
- * KDA_BT16_FUSED_KERNEL in args->flags fuses whatever the count; without
- * it, the environment variable KDA_BT16_FUSED=0 keeps the two stages and =1
- * fuses.  Debug outputs always take the two stages.  The workspace is
- * required either way. */
+ * stage 2 (kda_bt16_k1_hip, kda_bt16_k2_hip), or one fused kernel that
+ * keeps stage 1's per-chunk records in LDS instead of the workspace (same
+ * results bit for bit).  The choice (kda_bt16_fwd_plan) depends on the
+ * arguments and the device's CU count only:
+ *   - debug outputs: the two stages;
+ *   - KDA_BT16_FUSED_KERNEL: fused; KDA_BT16_TWO_STAGE: the two stages;
+ *   - fixed length: fused when the (batch row, value head) pairs are more
+ *     than half the CUs;
+ *   - cu_seqlens without max_seqlen: fused when the pairs are at least as
+ *     many as the CUs;
+ *   - cu_seqlens with max_seqlen: fused when its estimated time (set by the
+ *     longest sequence's chunks, or by the chunks per CU) is at most the two
+ *     stages' (set by all chunks for stage 1 and the longest chain for
+ *     stage 2), so one long sequence among short ones keeps the two stages.
+ * The workspace is required when the call runs the two stages and ignored
+ * (may be NULL) when it runs fused. */
 int kda_bt16_fwd_hip(const KdaBt16Args* args, void* stream);
 
 /* Which kernels kda_bt16_fwd_hip (and kda_bt16_fwd_noalloc_hip) run for
@@ -165,21 +187,37 @@ int kda_bt16_fwd_hip(const KdaBt16Args* args, void* stream);
  * whose _run always launches its two stages (kernels.py:581-602). */
 int kda_bt16_fwd_plan(const KdaBt16Args* args);
 
+/* Work-groups of the fused kernel that gave up a wait on the current
+ * device since the library was loaded or the count last reset.  No
+ * counterpart in the reference.  The fused kernel's waves meet through LDS
+ * flags, and every wait is bounded (2^22 polls) so that a stalled
+ * work-group cannot hang the GPU; one that runs out writes NaN over its
+ * (sequence, value head)'s o rows and final state and adds 1 to this
+ * count.  Synchronous: it waits for the device's work to finish.  With
+ * `reset` non-zero the count is set back to 0 after it is read.  Not for
+ * use during graph capture. */
+int kda_bt16_fused_aborts(uint32_t* count, int32_t reset);
+
 /* Full forward that allocates nothing and takes no workspace.  No
  * counterpart in the reference: it is for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  The same kernels as kda_bt16_fwd_hip,
- * with the same results bit for bit; the records stage 1 hands to stage 2
- * (when the forward is not fused) live in a file-scope device array of KDA_BT16_NOALLOC_MAX_WORKSPACE bytes
- * that the library holds on every GPU it runs on until the process ends.
- * args->workspace and args->workspace_bytes are ignored.  When the forward
- * runs fused (kda_bt16_fwd_plan) it uses no scratch and takes any size;
- * otherwise it returns KDA_BT16_ESCRATCH (before any launch) when
- * kda_bt16_workspace_bytes_args exceeds that size.  Every call on one GPU uses that GPU's one array:
- * calls that overlap on one GPU (two streams, two threads) race and give
- * wrong results; calls in order on one stream are safe.  The array keeps
- * the last call's contents; no part of it needs clearing (stage 1 writes
- * every record stage 2 reads). */
+ * with the same results bit for bit.
+ *   - When the forward runs fused (kda_bt16_fwd_plan) it uses no scratch
+ *     and takes any size.
+ *   - Otherwise the records stage 1 hands to stage 2 live in a file-scope
+ *     device array of KDA_BT16_NOALLOC_MAX_WORKSPACE bytes; a geometry that
+ *     needs more (kda_bt16_workspace_bytes_args) returns KDA_BT16_ESCRATCH
+ *     before any launch.  The first such call on a device looks up the
+ *     array's device address (the runtime places the array on that device
+ *     then, and the library holds it until the process ends): make that
+ *     first call before capturing calls into a graph.
+ *   - Every call on one GPU uses that GPU's one array: calls that overlap
+ *     on one GPU (two streams, two threads) race and give wrong results;
+ *     calls in order on one stream are safe.  The array keeps the last
+ *     call's contents; no part of it needs clearing (stage 1 writes every
+ *     record stage 2 reads).
+ * args->workspace and args->workspace_bytes are ignored. */
 int kda_bt16_fwd_noalloc_hip(const KdaBt16Args* args, void* stream);
 
 /* Stage 1 only: per-chunk gates, grams, (I+L)^-1 solve and W/U into the

@@ -65,16 +65,6 @@ struct ChunkSmem {
     float red[CT / 64];
 };
 
-__device__ __forceinline__ void load8(const uint16_t* src, bool valid, float (&out)[8]) {
-    u32x4 w = {0u, 0u, 0u, 0u};
-    if (valid) w = *reinterpret_cast<const u32x4*>(src);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        out[2 * j] = __builtin_bit_cast(float, w[j] << 16);
-        out[2 * j + 1] = __builtin_bit_cast(float, w[j] & 0xffff0000u);
-    }
-}
-
 __device__ __forceinline__ void store8(uint16_t* dst, const float (&x)[8]) {
     *reinterpret_cast<u32x4*>(dst) =
         u32x4{pack2(x[0], x[1]), pack2(x[2], x[3]), pack2(x[4], x[5]), pack2(x[6], x[7])};

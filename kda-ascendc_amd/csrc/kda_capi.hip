@@ -76,6 +76,14 @@ int check_common(const KdaBt16Args* a, Params& p) {
     p.use_beta_sigmoid = (a->flags & KDA_BT16_USE_BETA_SIGMOID) != 0;
     p.g_log = (a->flags & KDA_BT16_G_LOG_DECAY) != 0;
     p.force_fused = (a->flags & KDA_BT16_FUSED_KERNEL) != 0;
+    p.two_stage = (a->flags & KDA_BT16_TWO_STAGE) != 0;
+    if (p.force_fused && p.two_stage) return KDA_BT16_EINVAL;
+    if (a->k2_tiles != 0 && a->k2_tiles != 1 && a->k2_tiles != 2 && a->k2_tiles != 4 && a->k2_tiles != 8)
+        return KDA_BT16_EINVAL;
+    if (a->k2_wave_tiles < 0 || a->k2_wave_tiles > 2 || a->max_seqlen < 0) return KDA_BT16_EINVAL;
+    p.k2_tiles = a->k2_tiles;
+    p.k2_wave_tiles = a->k2_wave_tiles;
+    p.max_seqlen = a->cu_seqlens ? a->max_seqlen : 0;
     p.h0_v_first = p.ht_v_first = (a->flags & KDA_BT16_STATE_V_FIRST) != 0;
     p.cu_seqlens = a->cu_seqlens;
     p.cu_i64 = a->cu_seqlens_dtype == KDA_BT16_DTYPE_I64;
@@ -121,15 +129,20 @@ int to_params_core(const KdaBt16Args* a, Params& p, bool need_inputs, bool need_
     return KDA_BT16_OK;
 }
 
-// The chunked entries with the caller's workspace.
-int to_params(const KdaBt16Args* a, Params& p, bool need_inputs, bool need_outputs) {
-    int rc = to_params_core(a, p, need_inputs, need_outputs);
-    if (rc != KDA_BT16_OK) return rc;
+// The caller's workspace (for the records stage 1 hands to stage 2).
+int take_workspace(const KdaBt16Args* a, Params& p) {
     const size_t need = kda_bt16_workspace_bytes_args(a);
     if (!a->workspace || a->workspace_bytes < need) return KDA_BT16_EWORKSPACE;
     if ((reinterpret_cast<uintptr_t>(a->workspace) & 255u) != 0) return KDA_BT16_EWORKSPACE;
     p.ws = static_cast<uint8_t*>(a->workspace);
     return KDA_BT16_OK;
+}
+
+// The chunked entries with the caller's workspace.
+int to_params(const KdaBt16Args* a, Params& p, bool need_inputs, bool need_outputs) {
+    int rc = to_params_core(a, p, need_inputs, need_outputs);
+    if (rc != KDA_BT16_OK) return rc;
+    return take_workspace(a, p);
 }
 
 // Scratch of kda_bt16_fwd_noalloc_hip: the records stage 1 hands to stage
@@ -334,9 +347,14 @@ int kda_bt16_k2_hip(const KdaBt16Args* args, void* stream) {
 
 int kda_bt16_fwd_hip(const KdaBt16Args* args, void* stream) {
     Params p;
-    int rc = to_params(args, p, true, true);
+    int rc = to_params_core(args, p, true, true);
     if (rc != KDA_BT16_OK) return rc;
-    if (kda::launch_fwd(p, static_cast<hipStream_t>(stream)) != hipSuccess) return KDA_BT16_ELAUNCH;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    // The fused forward keeps its records in LDS: no workspace.
+    if (kda::fwd_plan(p) == 1) return kda::launch_fused(p, s) == hipSuccess ? KDA_BT16_OK : KDA_BT16_ELAUNCH;
+    rc = take_workspace(args, p);
+    if (rc != KDA_BT16_OK) return rc;
+    if (kda::launch_two_stage(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
     return KDA_BT16_OK;
 }
 
@@ -345,6 +363,11 @@ int kda_bt16_fwd_plan(const KdaBt16Args* args) {
     const int rc = to_params_core(args, p, true, true);
     if (rc != KDA_BT16_OK) return rc;
     return kda::fwd_plan(p);
+}
+
+int kda_bt16_fused_aborts(uint32_t* count, int32_t reset) {
+    if (count == nullptr) return KDA_BT16_EINVAL;
+    return kda::fused_abort_count(count, reset != 0) == hipSuccess ? KDA_BT16_OK : KDA_BT16_ELAUNCH;
 }
 
 int kda_bt16_fwd_noalloc_hip(const KdaBt16Args* args, void* stream) {
@@ -358,7 +381,7 @@ int kda_bt16_fwd_noalloc_hip(const KdaBt16Args* args, void* stream) {
         return KDA_BT16_ESCRATCH;
     rc = scratch_ptr(&p.ws);
     if (rc != KDA_BT16_OK) return rc;
-    if (kda::launch_fwd(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
+    if (kda::launch_two_stage(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
     return KDA_BT16_OK;
 }
 
@@ -464,7 +487,8 @@ const char* kda_bt16_strerror(int code) {
         case KDA_BT16_OK: return "ok";
         case KDA_BT16_EINVAL:
             return "invalid argument (null pointer, non-positive size, bad dtype tag, "
-                   "misaligned tensor, or cu_seqlens with B != 1 or N <= 0)";
+                   "misaligned tensor, cu_seqlens with B != 1 or N <= 0, both FUSED_KERNEL and "
+                   "TWO_STAGE, or a kernel choice out of range)";
         case KDA_BT16_EUNSUPPORTED:
             return "unsupported geometry (needs K=V=128, HV a multiple of H, T <= 1973776 and "
                    "32-bit grids) or flag";

@@ -133,7 +133,13 @@ struct Params {
     int g_log;  // without use_gate: g is the per-token natural-log decay
     int h0_v_first, ht_v_first;  // layouts of h0 / ht: [V, K] if set, else [K, V]
     int o_fp32;                  // token recurrence only: o in fp32
-    int force_fused;             // forward: the fused kernel whatever the geometry
+    // The forward's kernel choices (KdaBt16Args, ABI 4): force_fused /
+    // two_stage from the flags; k2_tiles (1, 2, 4, 8) and k2_wave_tiles (1,
+    // 2) for stage 2, 0 for the library's choice; max_seqlen, with
+    // cu_seqlens, the caller's hint of the longest sequence (0: unknown).
+    int force_fused, two_stage;
+    int k2_tiles, k2_wave_tiles;
+    int max_seqlen;
     // Varlen: N sequences packed along T (B == 1), sequence n holding tokens
     // [cu_seqlens[n], cu_seqlens[n+1]); states are [N, HV, ...].  NS is the
     // number of record slots per value head.  Null cu_seqlens: fixed length.
@@ -404,13 +410,16 @@ hipError_t launch_k2(const Params& p, hipStream_t stream);
 int k2_wide_tiles(const Params& p, int ncu);
 hipError_t launch_k2_wide(const Params& p, int tpw, hipStream_t stream);
 // The forward as one kernel (kda_fused.hip): whether it is taken for a
-// geometry on `ncu` CUs, and its launch.
+// geometry on `ncu` CUs, its launch, and the count of its work-groups that
+// gave up a bounded wait on the current device (read synchronously, then
+// optionally reset).
 bool fused_forward(const Params& p, int ncu);
 hipError_t launch_fused(const Params& p, hipStream_t stream);
-// The forward: fused, or stage 1 then stage 2 (kda_k2.hip); fwd_plan says
+hipError_t fused_abort_count(uint32_t* count, bool reset);
+// The forward is fused or stage 1 then stage 2 (kda_k2.hip); fwd_plan says
 // which on the current device (1 fused, 0 two stages).
-hipError_t launch_fwd(const Params& p, hipStream_t stream);
 int fwd_plan(const Params& p);
+hipError_t launch_two_stage(const Params& p, hipStream_t stream);
 hipError_t launch_recurrent(const Params& p, hipStream_t stream);
 // Backward (kda_bt16_bwd.hip, and the training variants of the stages).
 hipError_t launch_k1_both_records(const Params& p, hipStream_t stream);

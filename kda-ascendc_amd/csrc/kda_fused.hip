@@ -28,11 +28,10 @@
 // Chunk c's producer only waits for reads of chunk c - RING, which needs
 // only chunks below c, all produced by then (each producer takes its chunks
 // in order), so the waits always end.  Each wait is also bounded (SPIN_LIMIT
-// polls): a bound that runs out marks the work-group aborted, after which no
-// wave waits again and the work-group drains with wrong values instead of
-// hanging the GPU.
-#include <cstdlib>
-
+// polls) so that a stalled work-group cannot hang the GPU: a bound that runs
+// out marks the work-group aborted, after which no wave waits again; the
+// work-group drains, writes NaN over its o rows and final state, and adds 1
+// to a device-wide count that the host reads (fused_abort_count).
 #include "kda_common.h"
 #include "kda_k1_chunk.h"
 #include "kda_k2_shared.h"
@@ -64,6 +63,10 @@ __shared__ int f_full[F_RING];
 __shared__ int f_done[F_RING];
 __shared__ int f_aborted;
 
+// Work-groups that gave up a wait on this device since the library was
+// loaded or the count was reset (fused_abort_count).
+__device__ uint32_t g_aborts;
+
 __device__ __forceinline__ int lds_load(const int* a) {
     return __builtin_amdgcn_readfirstlane(__hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
 }
@@ -77,8 +80,30 @@ __device__ __forceinline__ void wait_ge(const int* a, int target) {
         }
         __builtin_amdgcn_s_sleep(1);
     }
-    __hip_atomic_store(&f_aborted, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    // the first wave of the work-group to give up counts it
+    if ((threadIdx.x & 63) == 0 &&
+        __hip_atomic_exchange(&f_aborted, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) == 0)
+        __hip_atomic_fetch_add(&g_aborts, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     asm volatile("" ::: "memory");
+}
+
+// A work-group that gave up a wait has read slots whose chunks it cannot
+// vouch for: this compute wave's o columns (its two value tiles) over the
+// whole sequence and its final-state rows become NaN.
+__device__ __noinline__ void mark_lost(const Params& p, const SeqSpan& sp, int hv, int ut, int lane,
+                                       f32x4 (&SA)[8], f32x4 (&SB)[8]) {
+    const float nan = __builtin_nanf("");
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) {
+        SA[kt] = f32x4{nan, nan, nan, nan};
+        SB[kt] = SA[kt];
+    }
+    // the wave's o stores of the chunks have completed before these replace them
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const u32x4 nan8 = {0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};
+    uint16_t* base = p.o + (sp.tok0 * p.HV + hv) * DK + 16 * ut + 8 * (lane & 3);
+    for (int r = lane >> 2; r < sp.len; r += 16)
+        *reinterpret_cast<u32x4*>(base + (int64_t)r * p.HV * DK) = nan8;
 }
 
 // The compute waves' side of the LDS flags (wide_step's hooks).
@@ -336,6 +361,7 @@ __global__ __launch_bounds__(F_THREADS) void fused_kernel(Params p) {
     cx.obase[1] = cx.obase[0] + 16;
     cx.orow_stride = (int64_t)p.HV * DK;
     for (int c = 0; c < cx.NT; c += F_RING) fused_round<0, F_RING>(cx, c, SA, SB, ut);
+    if (lds_load(&f_aborted)) mark_lost(p, sp, hv, ut, lane, SA, SB);
     store_state(p, sbase, va, q4, SA);
     store_state(p, sbase, va + 16, q4, SB);
     __builtin_amdgcn_endpgm();
@@ -343,32 +369,54 @@ __global__ __launch_bounds__(F_THREADS) void fused_kernel(Params p) {
 
 }  // namespace
 
+// Estimated times (us) of a varlen forward on `ncu` CUs, from per-chunk
+// costs measured on MI355X (K = V = 128, every in-kernel flag):
+//   fused: each work-group takes ~1.85 us per chunk of its sequence, in
+//     parallel with the others, so the longest sequence sets the time, or
+//     the chunks per CU once the work-groups run in rounds;
+//   two stages: stage 1 ~7.5 ns per record slot and value head, stage 2
+//     ~0.65 us per step of its longest chain (or of the chunks per CU).
+// Measured at 192 (sequence, head) pairs (HV = 32): lengths 19456 + 5 x
+// 1024, fused 2188 us and two stages 1146 (estimates 2250 and 1160);
+// 6 x 4096, 480 against 590 (474 and 536).
+double fused_estimate_us(const Params& p, int ncu) {
+    const double chunks = (double)((std::min(p.max_seqlen, p.T) + BT - 1) / BT);
+    const double per_cu = (double)p.HV * p.NS / ncu;
+    return 1.85 * std::max(chunks, per_cu);
+}
+
+double two_stage_estimate_us(const Params& p, int ncu) {
+    const double chunks = (double)((std::min(p.max_seqlen, p.T) + BT - 1) / BT);
+    const double slots = (double)p.HV * p.NS;
+    return 0.0075 * slots + 0.65 * std::max(chunks, slots / ncu);
+}
+
 // Whether the forward runs as one fused kernel: never when the
 // reference-layout intermediates are asked for (those come from stage 1);
-// always when the caller asks for it (the reference's use_fused_kernel);
-// else KDA_BT16_FUSED=0 keeps the two stages and =1 fuses; else, with fixed
-// length, more (sequence, head) pairs than half the CUs, and with cu_seqlens
-// at least as many pairs as CUs.
+// as the caller asks (force_fused, the reference's use_fused_kernel, or
+// two_stage); else, with fixed length, when the (sequence, head) pairs are
+// more than half the CUs; with cu_seqlens and the caller's max_seqlen, when
+// the fused estimate is at most the two stages'; with cu_seqlens alone,
+// when the pairs fill the CUs.
 //
 // Below the CU count the fused kernel runs every pair in one round of
 // work-groups, about 1.85 us per chunk whatever their number, while the two
 // stages grow with the pairs (T=4096 forwards, two stages against fused: 128
 // pairs 377 against 476 us, 160 pairs 505 against 480, 224 pairs 658 against
 // 479).  With cu_seqlens the fused kernel's time follows the longest
-// sequence and stage 1's the total; the host never reads cu_seqlens, and a
-// single long sequence among short ones makes the lower threshold up to
-// about twice slower (192 pairs, lengths 19456 + 5 x 1024: fused 2188 us,
-// two stages 1146; equal lengths: 480 against 590), so there the pairs must
-// fill the CUs.
+// sequence and stage 1's the total: a single long sequence among short ones
+// makes the fused kernel up to about twice slower (192 pairs, lengths
+// 19456 + 5 x 1024: fused 2188 us, two stages 1146; equal lengths: 480
+// against 590).  Without the length of the longest sequence, the pairs
+// must fill the CUs.
 bool fused_forward(const Params& p, int ncu) {
     if (p.dbg_w || p.dbg_u || p.dbg_Aqk || p.dbg_A_inv || p.dbg_g) return false;
     if (p.force_fused) return true;
+    if (p.two_stage) return false;
     const int64_t nbh = (int64_t)(p.cu_seqlens ? p.N : p.B) * p.HV;
-    if (const char* e = getenv("KDA_BT16_FUSED")) {
-        if (atoi(e) == 0) return false;
-        if (atoi(e) == 1) return true;
-    }
-    return p.cu_seqlens ? nbh >= ncu : 2 * nbh > ncu;
+    if (!p.cu_seqlens) return 2 * nbh > ncu;
+    if (p.max_seqlen > 0) return fused_estimate_us(p, ncu) <= two_stage_estimate_us(p, ncu);
+    return nbh >= ncu;
 }
 
 hipError_t launch_fused(const Params& p, hipStream_t stream) {
@@ -376,6 +424,15 @@ hipError_t launch_fused(const Params& p, hipStream_t stream) {
     auto kern = p.g_bf16 ? fused_kernel<true> : fused_kernel<false>;
     hipLaunchKernelGGL(kern, dim3((unsigned)nbh), dim3(F_THREADS), 0, stream, p);
     return hipGetLastError();
+}
+
+hipError_t fused_abort_count(uint32_t* count, bool reset) {
+    hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return e;
+    e = hipMemcpyFromSymbol(count, HIP_SYMBOL(g_aborts), sizeof(uint32_t), 0, hipMemcpyDeviceToHost);
+    if (e != hipSuccess || !reset) return e;
+    const uint32_t zero = 0;
+    return hipMemcpyToSymbol(HIP_SYMBOL(g_aborts), &zero, sizeof(uint32_t), 0, hipMemcpyHostToDevice);
 }
 
 }  // namespace kda

@@ -1014,8 +1014,7 @@ hipError_t launch_k2(const Params& p, hipStream_t stream) {
 
 int fwd_plan(const Params& p) { return fused_forward(p, cu_count()) ? 1 : 0; }
 
-hipError_t launch_fwd(const Params& p, hipStream_t stream) {
-    if (fused_forward(p, cu_count())) return launch_fused(p, stream);
+hipError_t launch_two_stage(const Params& p, hipStream_t stream) {
     const hipError_t e = launch_k1(p, stream);
     return e != hipSuccess ? e : launch_k2(p, stream);
 }

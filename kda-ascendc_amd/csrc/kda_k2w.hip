@@ -25,8 +25,6 @@
 //     hc, which needs only the state): with two tiles a wave reads them once
 //     for both, with one tile twice the waves issue the work.
 // The waves meet at one barrier per chunk.
-#include <cstdlib>
-
 #include "kda_common.h"
 #include "kda_k2_shared.h"
 #include "kda_k2w_step.h"
@@ -188,19 +186,15 @@ __global__ __launch_bounds__((WideGeom<TPW, TW>::THREADS)) void k2w_kernel(Param
 }  // namespace
 
 // Value tiles per work-group of the wide stage 2, or 0 for kda_k2.hip's one
-// tile per work-group: the fewest tiles (1, 2, 4, 8) that keep the
-// (sequences x heads x 8 / tiles) work-groups within one per CU.  A second
-// round of work-groups costs more than wider ones: B=2 T=8192 H=32 (64
-// pairs) runs stage 2 in 196 us with 2 tiles, 233 with 4 and 321 with 1;
-// B=4 T=4096 H=32 (128 pairs) in 156 us with 4 tiles, 193 with 2 and 198
-// with 8.
+// tile per work-group: the caller's p.k2_tiles when set, else the fewest
+// tiles (1, 2, 4, 8) that keep the (sequences x heads x 8 / tiles)
+// work-groups within one per CU.  A second round of work-groups costs more
+// than wider ones: B=2 T=8192 H=32 (64 pairs) runs stage 2 in 196 us with 2
+// tiles, 233 with 4 and 321 with 1; B=4 T=4096 H=32 (128 pairs) in 156 us
+// with 4 tiles, 193 with 2 and 198 with 8.
 int k2_wide_tiles(const Params& p, int ncu) {
     const int64_t nbh = (int64_t)(p.cu_seqlens ? p.N : p.B) * p.HV;
-    if (const char* e = getenv("KDA_BT16_K2_TILES")) {
-        const int t = atoi(e);
-        if (t == 1) return 0;
-        if (t == 2 || t == 4 || t == 8) return t;
-    }
+    if (p.k2_tiles != 0) return p.k2_tiles == 1 ? 0 : p.k2_tiles;
     if (nbh * 8 <= ncu) return 0;
     if (nbh * 4 <= ncu) return 2;
     if (nbh * 2 <= ncu) return 4;
@@ -222,9 +216,8 @@ hipError_t launch_k2_wide(const Params& p, int tpw, hipStream_t stream) {
     // One tile per compute wave issues the work of 2 or 4 tiles from twice
     // the waves (B=1 T=8192 H=96, 4 tiles: stage 2 284 against 354 us);
     // with 8 tiles, 9 waves gained nothing over 5 (B=16 T=2048 H=32: 317 us
-    // both), so two tiles per wave there.
-    int tw = tpw == 8 ? 2 : 1;
-    if (const char* e = getenv("KDA_BT16_K2_WAVE_TILES")) tw = atoi(e) == 1 ? 1 : 2;
+    // both), so two tiles per wave there.  p.k2_wave_tiles overrides.
+    const int tw = p.k2_wave_tiles != 0 ? p.k2_wave_tiles : (tpw == 8 ? 2 : 1);
     switch (tpw * 4 + tw) {
         case 2 * 4 + 1: launch_w<2, 1>(p, padded, stream); break;
         case 4 * 4 + 1: launch_w<4, 1>(p, padded, stream); break;

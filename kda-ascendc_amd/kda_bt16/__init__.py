@@ -17,6 +17,8 @@ and a per-function backend dispatch that registers these kernels
 from . import dispatch
 from .fla import chunk_kda, fused_recurrent_kda
 from .kernels import (
+    forward_choice,
+    fused_abort_count,
     kda_bt16_bwd,
     kda_bt16_debug,
     kda_bt16_fwd,
@@ -36,6 +38,8 @@ __all__ = [
     "kda_recurrent_fwd",
     "kda_decode_step",
     "set_backward_recompute",
+    "forward_choice",
+    "fused_abort_count",
     "chunk_kda",
     "fused_recurrent_kda",
     "dispatch",

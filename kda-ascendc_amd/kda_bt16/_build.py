@@ -10,6 +10,7 @@ from __future__ import annotations
 import os
 import shutil
 import subprocess
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
@@ -50,16 +51,38 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (looked in $HIPCC, /opt/rocm/bin, PATH)")
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every HIP source into ``libkda_bt16_hip.so``; return its path."""
-    srcs = [str(CSRC / s) for s in SOURCES]
-    tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", *srcs, "-o", str(tmp)]
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
+    # hipcc's host pass does not know the packed-fp32 feature flag: harmless
+    out = "\n".join(ln for ln in (res.stdout + res.stderr).splitlines()
+                    if ln.strip() and "packed-fp32-ops' is not a recognized feature" not in ln)
+    if verbose and out:
+        print(out, flush=True)
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every HIP source (one hipcc process per source, in parallel)
+    and link ``libkda_bt16_hip.so``; return its path.  Objects go to a
+    scratch folder beside the sources (``_build/``)."""
+    cc = hipcc()
+    objdir = PKG_DIR.parent / "_build"
+    objdir.mkdir(exist_ok=True)
+    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    jobs = []
+    for s in SOURCES:
+        obj = objdir / (Path(s).stem + ".o")
+        jobs.append(([cc, *compile_flags, f"-I{INCLUDE}", "-c", str(CSRC / s), "-o", str(obj)], obj))
+    workers = max(1, min(len(jobs), os.cpu_count() or 1, 16))
+    with ThreadPoolExecutor(max_workers=workers) as ex:
+        for f in [ex.submit(_run, cmd, verbose) for cmd, _ in jobs]:
+            f.result()
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *(str(o) for _, o in jobs), "-o", str(tmp)],
+         verbose)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

@@ -12,7 +12,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libkda_bt16_hip.so"
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 USE_GATE = 1 << 0
 USE_QK_L2NORM = 1 << 1
@@ -21,6 +21,7 @@ STATE_V_FIRST = 1 << 3
 O_FP32 = 1 << 4  # token recurrence only
 G_LOG_DECAY = 1 << 5  # without USE_GATE: g is the per-token natural-log decay
 FUSED_KERNEL = 1 << 6  # forward entries: the fused kernel whatever the geometry
+TWO_STAGE = 1 << 7  # forward entries: stage 1 then stage 2 whatever the geometry
 
 # Bytes of the static scratch of kda_bt16_fwd_noalloc_hip, and the code it
 # returns for a geometry whose records do not fit.
@@ -47,6 +48,7 @@ EXPORTED_SYMBOLS = (
     "kda_bt16_fwd_save_hip",
     "kda_bt16_bwd_saved_workspace_bytes",
     "kda_bt16_bwd_saved_hip",
+    "kda_bt16_fused_aborts",
     "kda_bt16_strerror",
     "kda_bt16_abi_version",
 )
@@ -88,6 +90,9 @@ class KdaBt16Args(ctypes.Structure):
         ("cu_seqlens", ctypes.c_void_p),
         ("cu_seqlens_dtype", ctypes.c_int32),
         ("N", ctypes.c_int32),
+        ("k2_tiles", ctypes.c_int32),
+        ("k2_wave_tiles", ctypes.c_int32),
+        ("max_seqlen", ctypes.c_int32),
     ]
 
 
@@ -161,6 +166,8 @@ def lib() -> ctypes.CDLL:
                                              ctypes.c_size_t, ctypes.c_void_p]
         h.kda_bt16_fwd_plan.restype = ctypes.c_int
         h.kda_bt16_fwd_plan.argtypes = [ctypes.POINTER(KdaBt16Args)]
+        h.kda_bt16_fused_aborts.restype = ctypes.c_int
+        h.kda_bt16_fused_aborts.argtypes = [ctypes.POINTER(ctypes.c_uint32), ctypes.c_int32]
         h.kda_bt16_strerror.restype = ctypes.c_char_p
         h.kda_bt16_strerror.argtypes = [ctypes.c_int]
         h.kda_bt16_abi_version.restype = ctypes.c_int
@@ -189,6 +196,17 @@ def fwd_plan(args: KdaBt16Args) -> int:
     if rc < 0:
         raise RuntimeError(f"kda_bt16_fwd_plan: {lib().kda_bt16_strerror(rc).decode()}")
     return rc
+
+
+def fused_aborts(reset: bool = False) -> int:
+    """``kda_bt16_fused_aborts``: fused-kernel work-groups on the current
+    device that gave up a bounded wait (their o rows and final state are
+    NaN) since load or the last reset.  Waits for the device's work."""
+    n = ctypes.c_uint32(0)
+    rc = int(lib().kda_bt16_fused_aborts(ctypes.byref(n), 1 if reset else 0))
+    if rc != 0:
+        raise KdaHipError("kda_bt16_fused_aborts", rc, lib().kda_bt16_strerror(rc).decode())
+    return int(n.value)
 
 
 def bwd_workspace_bytes(args: KdaBt16Args) -> int:

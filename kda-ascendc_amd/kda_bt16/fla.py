@@ -29,7 +29,7 @@ from __future__ import annotations
 
 import torch
 
-from .kernels import _fwd_maybe_autograd, _validate_kda_inputs, kda_recurrent_fwd
+from .kernels import _check_max_seqlen, _fwd_maybe_autograd, _validate_kda_inputs, kda_recurrent_fwd
 
 _LB_RANGE = (-11.0, 0.0)
 
@@ -130,6 +130,7 @@ def chunk_kda(
     chunk_size: int = 64,
     return_intermediate_states: bool = False,
     cp_context=None,
+    max_seqlen: int | None = None,
     **kwargs,
 ):
     """FLA ``chunk_kda`` on the MI355X chunked kernels.
@@ -138,6 +139,8 @@ def chunk_kda(
     final state (``None`` unless ``output_final_state``), K-first
     ``[N, HV, K, V]`` unless ``state_v_first``.  Raises
     ``NotImplementedError`` outside :func:`verify_chunk_kda`'s bucket.
+    ``max_seqlen`` (with ``cu_seqlens``) is the longest sequence's length,
+    a hint for the kernel choice (:func:`kda_bt16.kda_bt16_fwd`).
     """
     del chunk_size, kwargs  # 16-token chunks; other FLA options do not change the forward
     reason = verify_chunk_kda(
@@ -151,13 +154,14 @@ def chunk_kda(
         q, k, v, g, beta, initial_state, use_gate_in_kernel, True, lower_bound,
         A_log, dt_bias, state_v_first, cu_seqlens,
     )
+    _check_max_seqlen(max_seqlen)
     if scale is None:
         scale = K ** -0.5
     return _fwd_maybe_autograd(
         q, k, v, g, beta, scale, initial_state, output_final_state,
         use_qk_l2norm_in_kernel, use_gate_in_kernel, use_beta_sigmoid_in_kernel,
         lower_bound, A_log, dt_bias, state_v_first,
-        cu_seqlens=cu_seqlens, g_log=not use_gate_in_kernel,
+        cu_seqlens=cu_seqlens, g_log=not use_gate_in_kernel, max_seqlen=max_seqlen,
     )
 
 

@@ -39,8 +39,9 @@ Differences from the reference, all supersets of its contract:
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
-import os
+import threading
 
 import torch
 
@@ -56,14 +57,56 @@ _WORKSPACE_CACHE: dict[tuple, dict[str, torch.Tensor]] = {}
 # 16-token chunk and value head) and the backward starts from it; False:
 # the forward keeps only its inputs and the backward recomputes the state.
 # The two give the same gradients, bit for bit.
-_SAVE_STATE = [os.environ.get("KDA_BT16_BWD_RECOMPUTE", "0") != "1"]
+_SAVE_STATE = [True]
 
 
 def set_backward_recompute(recompute: bool) -> None:
     """Choose the training memory policy: ``True`` recomputes the chunk
     states in the backward (memory of the inputs only), ``False`` (the
-    default, or ``KDA_BT16_BWD_RECOMPUTE=0``) keeps them from the forward."""
+    default) keeps them from the forward."""
     _SAVE_STATE[0] = not recompute
+
+
+# Kernel choices forced by :func:`forward_choice` on this thread.
+_CHOICE = threading.local()
+
+
+@contextlib.contextmanager
+def forward_choice(*, fused: bool | None = None, k2_tiles: int = 0, k2_wave_tiles: int = 0):
+    """Force the forward's kernel choices for the calls this thread makes
+    inside the block (no counterpart in the reference, whose ``_run``
+    always launches its two stages, kernels.py:581-602):
+
+    * ``fused``: True runs the fused kernel, False stage 1 then stage 2,
+      None (default) leaves it to the library; an explicit
+      ``use_fused_kernel=True`` still wins;
+    * ``k2_tiles``: stage-2 value tiles per work-group (1, 2, 4 or 8);
+    * ``k2_wave_tiles``: with 2-8 tiles, value tiles per compute wave (1, 2);
+
+    0 leaves the choice to the library.  They reach the C ABI as the
+    ``KDA_BT16_FUSED_KERNEL`` / ``KDA_BT16_TWO_STAGE`` flags and the
+    ``k2_tiles`` / ``k2_wave_tiles`` fields.  Every choice gives the same
+    results bit for bit: this is for measurement and tests."""
+    if k2_tiles not in (0, 1, 2, 4, 8):
+        raise ValueError(f"k2_tiles must be 0, 1, 2, 4 or 8, got {k2_tiles}")
+    if k2_wave_tiles not in (0, 1, 2):
+        raise ValueError(f"k2_wave_tiles must be 0, 1 or 2, got {k2_wave_tiles}")
+    prev = getattr(_CHOICE, "value", None)
+    _CHOICE.value = (fused, k2_tiles, k2_wave_tiles)
+    try:
+        yield
+    finally:
+        _CHOICE.value = prev
+
+
+def fused_abort_count(reset: bool = False, device: torch.device | int | None = None) -> int:
+    """Fused-kernel work-groups on ``device`` (default: the current one)
+    that gave up a bounded wait since the library was loaded or the count
+    last reset (``kda_bt16_fused_aborts``).  Such a work-group writes NaN
+    over its (sequence, value head)'s o rows and final state instead of
+    hanging the GPU.  Waits for the device's work to finish."""
+    with torch.cuda.device(torch.cuda.current_device() if device is None else device):
+        return _hip.fused_aborts(reset)
 
 _RCP_LN2 = 1.4426950216
 _EPS = 1e-6
@@ -260,7 +303,7 @@ def _dtype_tag(t: torch.Tensor) -> int:
 
 def _make_args(
     q, k, v, g, beta, scale, lower_bound, A_log, dt_bias, h0, o, ht, ws, ws_bytes,
-    flags, dbg=None, cu_seqlens=None,
+    flags, dbg=None, cu_seqlens=None, max_seqlen=None,
 ) -> _hip.KdaBt16Args:
     B, T, H, K = q.shape
     HV, V = v.shape[2], v.shape[-1]
@@ -290,6 +333,14 @@ def _make_args(
         a.cu_seqlens = cu_seqlens.data_ptr()
         a.cu_seqlens_dtype = _hip.DTYPE_I64 if cu_seqlens.dtype == torch.int64 else _hip.DTYPE_I32
         a.N = cu_seqlens.numel() - 1
+        a.max_seqlen = int(max_seqlen or 0)
+    choice = getattr(_CHOICE, "value", None)
+    if choice is not None:
+        fused, a.k2_tiles, a.k2_wave_tiles = choice
+        if fused is False and not flags & _hip.FUSED_KERNEL:
+            a.flags |= _hip.TWO_STAGE
+        elif fused is True:
+            a.flags |= _hip.FUSED_KERNEL
     return a
 
 
@@ -331,9 +382,11 @@ def _run(
     cu_seqlens: torch.Tensor | None = None,
     g_log: bool = False,
     save_state: bool = False,
+    max_seqlen: int | None = None,
 ):
     """Host driver, the counterpart of kernels.py:475-606: allocate outputs,
-    lease the workspace, launch stage 1 and stage 2 through the C ABI.
+    lease the workspace when the forward runs its two stages (the fused
+    kernel keeps the records in LDS), launch through the C ABI.
 
     ``save_state``: run the training forward (``kda_bt16_fwd_save_hip``)
     and return ``(o, ht, saved)``, ``saved`` the uint8 state tensor the
@@ -382,11 +435,12 @@ def _run(
             A_log, dt_bias, initial_state, o, ht, None, 0,
             _flags(use_gate_in_kernel, use_qk_l2norm_in_kernel, use_beta_sigmoid_in_kernel,
                    state_v_first, g_log, use_fused),
-            dbg, cu_seqlens,
+            dbg, cu_seqlens, max_seqlen,
         )
-        ws_bytes = _hip.workspace_bytes_args(args)
-        ws = workspace.lease(dev, stream, ws_bytes)
-        args.workspace, args.workspace_bytes = ws.data_ptr(), ws_bytes
+        if save_state or _hip.fwd_plan(args) == 0:
+            ws_bytes = _hip.workspace_bytes_args(args)
+            ws = workspace.lease(dev, stream, ws_bytes)
+            args.workspace, args.workspace_bytes = ws.data_ptr(), ws_bytes
         if save_state:
             nbytes = _hip.saved_bytes(args)
             saved = torch.empty(nbytes, dtype=torch.uint8, device=dev)
@@ -509,10 +563,15 @@ def _wants_grad(*ts) -> bool:
     return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts)
 
 
+def _check_max_seqlen(max_seqlen) -> None:
+    if max_seqlen is not None and (not isinstance(max_seqlen, int) or max_seqlen < 0):
+        raise ValueError(f"max_seqlen must be a non-negative int or None, got {max_seqlen!r}")
+
+
 def _fwd_maybe_autograd(
     q, k, v, g, beta, scale, initial_state, output_final_state, l2, use_gate, bsig,
     lower_bound, A_log, dt_bias, svf, reuse_workspace=False, cu_seqlens=None, g_log=False,
-    use_fused=False,
+    use_fused=False, max_seqlen=None,
 ):
     """:func:`_run`, through :class:`_KdaBt16Fn` when an input requires grad
     (whose training forward keeps its per-chunk state for the backward and so
@@ -525,6 +584,7 @@ def _fwd_maybe_autograd(
         q, k, v, g, beta, scale, initial_state, output_final_state, l2, use_gate, bsig,
         lower_bound, A_log, dt_bias, svf, return_intermediates=False,
         reuse_workspace=reuse_workspace, cu_seqlens=cu_seqlens, g_log=g_log, use_fused=use_fused,
+        max_seqlen=max_seqlen,
     )
 
 
@@ -602,6 +662,7 @@ def kda_bt16_fwd(
     reuse_workspace: bool = False,
     *,
     cu_seqlens: torch.Tensor | None = None,
+    max_seqlen: int | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor | None]:
     """KDA forward (reference: kernels.py:752-810).
 
@@ -617,6 +678,11 @@ def kda_bt16_fwd(
             ``[B, HV, K, V]``; ``N`` rows instead of ``B`` with ``cu_seqlens``.
         cu_seqlens: optional int32/int64 ``[N + 1]`` offsets of N sequences
             packed along T (B must be 1).
+        max_seqlen: with ``cu_seqlens``, the longest sequence's length if
+            the caller knows it (FLA's varlen convention).  A hint for the
+            choice between the fused kernel and the two stages, which it
+            makes from estimated times: one long sequence among short ones
+            keeps the two stages.  The results are the same either way.
 
     Returns:
         ``o`` of shape ``[B, T, HV, V]`` (bf16) and, if
@@ -628,6 +694,7 @@ def kda_bt16_fwd(
         use_gate_in_kernel, safe_gate, lower_bound,
         A_log, dt_bias, state_v_first, cu_seqlens,
     )
+    _check_max_seqlen(max_seqlen)
     if scale is None:
         scale = K ** -0.5
     return _fwd_maybe_autograd(
@@ -635,6 +702,7 @@ def kda_bt16_fwd(
         use_qk_l2norm_in_kernel, use_gate_in_kernel, use_beta_sigmoid_in_kernel,
         lower_bound, A_log, dt_bias, state_v_first,
         reuse_workspace=reuse_workspace, cu_seqlens=cu_seqlens, use_fused=use_fused_kernel,
+        max_seqlen=max_seqlen,
     )
 
 

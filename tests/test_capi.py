@@ -8,10 +8,19 @@ import re
 from pathlib import Path
 
 import pytest
+import torch
 
 from kda_bt16 import _hip
 
 HEADER = Path(__file__).resolve().parents[1] / "include" / "kda_bt16_hip.h"
+
+# Tests that hand a launching entry point stand-in device pointers (1 << 40)
+# rely on its argument checks failing before any launch.  Without a GPU no
+# launch can happen whatever the checks do; on a GPU box they are skipped,
+# so that a regressed check can never launch a kernel on such an address.
+fake_pointers = pytest.mark.skipif(
+    torch.cuda.is_available(),
+    reason="stand-in device pointers are passed to launching entry points only where no GPU is present")
 
 
 def _declared_functions() -> list[str]:
@@ -65,6 +74,7 @@ def test_workspace_bytes():
     assert _hip.workspace_bytes_args(_args(cu_seqlens=fake, N=0)) == 0
 
 
+@fake_pointers
 def test_varlen_argument_checks():
     fake = 1 << 40  # never dereferenced: argument checks fail first
     vl = dict(cu_seqlens=fake, cu_seqlens_dtype=_hip.DTYPE_I64, N=3)
@@ -84,7 +94,7 @@ def test_varlen_argument_checks():
 
 def test_strerror_codes():
     lib = _hip.lib()
-    for code in (0, -1, -2, -3, -4, -5, -6):
+    for code in (0, -1, -2, -3, -4, -5, -6, -7):
         assert lib.kda_bt16_strerror(code)
     assert lib.kda_bt16_strerror(-99) == b"unknown error"
 
@@ -101,6 +111,7 @@ def _args(**kw):
 
 
 @pytest.mark.parametrize("fn", ["kda_bt16_fwd_hip", "kda_bt16_k1_hip", "kda_bt16_k2_hip"])
+@fake_pointers
 def test_argument_checks_return_codes_without_launching(fn):
     f = getattr(_hip.lib(), fn)
     assert f(None, None) == -1
@@ -117,36 +128,55 @@ def test_argument_checks_return_codes_without_launching(fn):
         _hip.call(fn, _args(), 0)
 
 
-def test_forward_plan_reads_no_device_memory(monkeypatch):
-    """kda_bt16_fwd_plan: argument checks, the KDA_BT16_FUSED override, and
-    the two stages whenever debug outputs are asked for (they come from
-    stage 1).  Pointers are never dereferenced."""
+def test_forward_plan_reads_no_device_memory():
+    """kda_bt16_fwd_plan: argument checks, the caller's choice through the
+    flags, and the two stages whenever debug outputs are asked for (they
+    come from stage 1).  Pointers are never dereferenced and nothing is
+    launched."""
     f = _hip.lib().kda_bt16_fwd_plan
     fake = 1 << 40
     ten = dict(q=fake, k=fake, v=fake, g=fake, beta=fake, o=fake)
     assert f(None) == -1
     assert f(ctypes.byref(_args(K=64, **ten))) == -2
     assert f(ctypes.byref(_args())) == -1  # missing tensors
-    monkeypatch.setenv("KDA_BT16_FUSED", "0")
-    assert f(ctypes.byref(_args(B=16, H=32, HV=32, **ten))) == 0
-    monkeypatch.setenv("KDA_BT16_FUSED", "1")
-    assert f(ctypes.byref(_args(**ten))) == 1
-    dbg = dict(dbg_Aqk=fake, dbg_A_inv=fake, dbg_w=fake, dbg_u=fake, dbg_g=fake)
-    assert f(ctypes.byref(_args(**ten, **dbg))) == 0
-    assert _hip.fwd_plan(_args(**ten)) == 1
-    # the caller's request (use_fused_kernel=True) wins over the environment,
-    # debug outputs over both
-    monkeypatch.setenv("KDA_BT16_FUSED", "0")
+    assert f(ctypes.byref(_args(B=16, H=32, HV=32, **ten))) == 1
+    assert f(ctypes.byref(_args(B=16, H=32, HV=32, flags=_hip.TWO_STAGE, **ten))) == 0
+    assert f(ctypes.byref(_args(**ten))) == 0
     assert f(ctypes.byref(_args(flags=_hip.FUSED_KERNEL, **ten))) == 1
+    dbg = dict(dbg_Aqk=fake, dbg_A_inv=fake, dbg_w=fake, dbg_u=fake, dbg_g=fake)
+    # debug outputs win over the caller's request
     assert f(ctypes.byref(_args(flags=_hip.FUSED_KERNEL, **ten, **dbg))) == 0
+    assert _hip.fwd_plan(_args(flags=_hip.FUSED_KERNEL, **ten)) == 1
+    # both requests at once, and kernel choices out of range, are refused
+    assert f(ctypes.byref(_args(flags=_hip.FUSED_KERNEL | _hip.TWO_STAGE, **ten))) == -1
+    for bad in (dict(k2_tiles=3), dict(k2_tiles=16), dict(k2_tiles=-1), dict(k2_wave_tiles=3),
+                dict(k2_wave_tiles=-1), dict(max_seqlen=-1)):
+        assert f(ctypes.byref(_args(**ten, **bad))) == -1, bad
+    for ok in (dict(k2_tiles=1), dict(k2_tiles=8, k2_wave_tiles=1), dict(max_seqlen=16)):
+        assert f(ctypes.byref(_args(**ten, **ok))) == 0, ok
 
 
-def test_forward_plan_thresholds(monkeypatch):
-    """Without the flag or the environment, fixed length fuses once the
-    (sequence, value head) pairs are more than half the CUs, cu_seqlens once
-    they are at least as many as the CUs.  Without a GPU the library counts
-    256 CUs, the MI355X's count."""
-    monkeypatch.delenv("KDA_BT16_FUSED", raising=False)
+@pytest.mark.parametrize("env", [{"KDA_BT16_FUSED": "1"}, {"KDA_BT16_FUSED": "0"},
+                                 {"KDA_BT16_K2_TILES": "2", "KDA_BT16_K2_WAVE_TILES": "2"}])
+def test_forward_plan_ignores_the_environment(monkeypatch, env):
+    """The choice depends on the arguments only: variables that once
+    overrode it change nothing."""
+    f = _hip.lib().kda_bt16_fwd_plan
+    fake = 1 << 40
+    ten = dict(q=fake, k=fake, v=fake, g=fake, beta=fake, o=fake)
+    shapes = [dict(), dict(B=16, H=32, HV=32), dict(B=1, H=129, HV=129),
+              dict(N=8, H=32, HV=32, T=4096, cu_seqlens=fake, cu_seqlens_dtype=_hip.DTYPE_I32)]
+    before = [f(ctypes.byref(_args(**ten, **sh))) for sh in shapes]
+    for name, val in env.items():
+        monkeypatch.setenv(name, val)
+    assert [f(ctypes.byref(_args(**ten, **sh))) for sh in shapes] == before
+
+
+def test_forward_plan_thresholds():
+    """Without the caller's choice, fixed length fuses once the (sequence,
+    value head) pairs are more than half the CUs, cu_seqlens once they are
+    at least as many as the CUs.  Without a GPU the library counts 256 CUs,
+    the MI355X's count."""
     f = _hip.lib().kda_bt16_fwd_plan
     fake = 1 << 40
     ten = dict(q=fake, k=fake, v=fake, g=fake, beta=fake, o=fake)
@@ -161,8 +191,36 @@ def test_forward_plan_thresholds(monkeypatch):
     cu = dict(cu_seqlens=fake, cu_seqlens_dtype=_hip.DTYPE_I32, T=4096)
     assert plan(N=7, H=32, HV=32, **cu) == 0  # 224 pairs
     assert plan(N=8, H=32, HV=32, **cu) == 1  # 256 pairs
+    # max_seqlen is only read with cu_seqlens
+    assert plan(B=5, H=32, HV=32, max_seqlen=16) == 1
 
 
+def test_forward_plan_with_max_seqlen():
+    """With cu_seqlens and the longest sequence's length, the choice follows
+    the estimated times: the fused kernel's is set by the longest sequence
+    (~1.85 us a chunk) or the chunks per CU, the two stages' by all chunks
+    (stage 1) plus the longest chain (stage 2, ~0.65 us a step).  Measured
+    at 192 pairs (HV = 32): lengths 19456 + 5 x 1024, fused 2188 us against
+    1146; 6 x 4096, 480 against 590."""
+    f = _hip.lib().kda_bt16_fwd_plan
+    fake = 1 << 40
+    ten = dict(q=fake, k=fake, v=fake, g=fake, beta=fake, o=fake)
+
+    def plan(N, T, longest, HV=32):
+        cu = dict(cu_seqlens=fake, cu_seqlens_dtype=_hip.DTYPE_I32)
+        return f(ctypes.byref(_args(N=N, T=T, H=HV, HV=HV, max_seqlen=longest, **cu, **ten)))
+
+    assert plan(6, 24576, 19456) == 0  # skewed: two stages
+    assert plan(6, 24576, 4096) == 1   # equal lengths: fused, below the pair-count threshold too
+    assert plan(8, 16384 + 7 * 1024, 16384) == 0  # 256 pairs, one long sequence
+    assert plan(8, 8 * 2944, 2944) == 1  # 256 pairs, equal
+    assert plan(16, 8192, 1527) == 1  # bench's 16 packed sequences (512 pairs)
+    assert plan(16, 16 * 2048, 2048) == 1  # c4's shape packed
+    # a hint longer than T is read as T
+    assert plan(6, 24576, 1 << 30) == plan(6, 24576, 24576)
+
+
+@fake_pointers
 def test_workspace_checked_before_launch():
     fake = 1 << 40  # never dereferenced: the size check fails first
     a = _args(q=fake, k=fake, v=fake, g=fake, beta=fake, o=fake, workspace=fake, workspace_bytes=100)
@@ -172,6 +230,7 @@ def test_workspace_checked_before_launch():
     assert _hip.lib().kda_bt16_fwd_hip(ctypes.byref(a), None) == -3
 
 
+@fake_pointers
 def test_recurrent_entry_argument_checks():
     f = _hip.lib().kda_recurrent_fwd_hip
     assert f(None, None) == -1
@@ -191,6 +250,7 @@ def test_recurrent_entry_argument_checks():
     assert f(ctypes.byref(_args(**{**full, "o": fake + 2}, flags=_hip.O_FP32)), None) == -1
 
 
+@fake_pointers
 def test_o_fp32_is_refused_on_chunked_entries():
     fake = 1 << 40
     a = _args(q=fake, k=fake, v=fake, g=fake, beta=fake, o=fake, flags=_hip.O_FP32)
@@ -223,6 +283,7 @@ def _bwd(fwd, **kw):
     return b
 
 
+@fake_pointers
 def test_bwd_argument_checks_return_codes_without_launching():
     f = _hip.lib().kda_bt16_bwd_hip
     fake = 1 << 40  # never dereferenced: the checks fail first

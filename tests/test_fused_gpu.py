@@ -4,8 +4,9 @@ the fused kernel runs stage 1's per-chunk code and the wide stage 2's step
 (kernels.py:53-302) on records kept in LDS instead of HBM, so only where the
 record lives differs.
 
-``KDA_BT16_FUSED`` forces the choice over the launch heuristic (0: two
-stages; 1: fused), which fuses when the (sequence, head) pairs are more than
+``forward_choice(fused=...)`` (the ``KDA_BT16_TWO_STAGE`` /
+``KDA_BT16_FUSED_KERNEL`` flags of the C ABI) forces the choice over the
+launch heuristic, which fuses when the (sequence, head) pairs are more than
 half the CUs (with cu_seqlens: at least as many as the CUs).  The cases
 cover what the record ring has edges at: fewer chunks than ring slots,
 counts that are and are not multiples of the ring and of the producer count,
@@ -15,16 +16,15 @@ both state layouts, fp32 and bf16 gates, and the precomputed-gate mode.
 
 from __future__ import annotations
 
-import os
-
 import pytest
 import torch
 
-from kda_bt16 import kda_bt16_fwd
+from kda_bt16 import forward_choice, kda_bt16_fwd, workspace
 
 pytestmark = pytest.mark.gpu
 
-ENV = "KDA_BT16_FUSED"
+# 0: the two stages, 1: the fused kernel, None: the library's choice
+_CHOICE = {0: False, 1: True, None: None}
 
 # name, B, T, H, HV, cu_seqlens, state_v_first, h0, g dtype, in-kernel gate
 CASES = [
@@ -65,12 +65,7 @@ def _inputs(B, T, H, HV, S, seed, gdt, in_kernel_gate):
 
 
 def _run(c, dev, cu, svf, h0, gate, fused):
-    old = os.environ.get(ENV)
-    if fused is None:
-        os.environ.pop(ENV, None)
-    else:
-        os.environ[ENV] = str(fused)
-    try:
+    with forward_choice(fused=_CHOICE[fused]):
         init = None
         if h0:
             init = c["h0"] if svf else c["h0"].transpose(-1, -2).contiguous()
@@ -84,11 +79,6 @@ def _run(c, dev, cu, svf, h0, gate, fused):
             cu_seqlens=None if cu is None else torch.tensor(cu, dtype=torch.int32, device=dev))
         torch.cuda.synchronize()
         return o, ht
-    finally:
-        if old is None:
-            os.environ.pop(ENV, None)
-        else:
-            os.environ[ENV] = old
 
 
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
@@ -144,8 +134,7 @@ def test_fused_saturated_gate(lower_bound, gpu_device):
     c["A_log"] = torch.zeros(H)
     outs = []
     for fused in (0, 1):
-        os.environ[ENV] = str(fused)
-        try:
+        with forward_choice(fused=_CHOICE[fused]):
             o, ht = kda_bt16_fwd(
                 *(c[x].to(gpu_device) for x in ("q", "k", "v", "g", "beta")), scale=0.1,
                 initial_state=c["h0"].to(gpu_device), output_final_state=True,
@@ -153,8 +142,6 @@ def test_fused_saturated_gate(lower_bound, gpu_device):
                 use_beta_sigmoid_in_kernel=True, lower_bound=lower_bound,
                 A_log=c["A_log"].to(gpu_device), dt_bias=None)
             torch.cuda.synchronize()
-        finally:
-            os.environ.pop(ENV, None)
         assert torch.isfinite(o.float()).all() and torch.isfinite(ht).all()
         outs.append((o, ht))
     assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
@@ -172,14 +159,56 @@ def test_fused_repeated_calls_are_bit_identical(gpu_device):
               use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True,
               use_beta_sigmoid_in_kernel=True, lower_bound=-5.0, A_log=c["A_log"].to(dev),
               dt_bias=c["dt_bias"].to(dev))
-    os.environ[ENV] = "1"
-    try:
+    with forward_choice(fused=True):
         runs = [kda_bt16_fwd(*args, **kw) for _ in range(20)]
         torch.cuda.synchronize()
-    finally:
-        os.environ.pop(ENV, None)
     o0, h0 = runs[0]
     assert torch.isfinite(o0.float()).all()
     for i, (o, ht) in enumerate(runs[1:], 1):
         assert torch.equal(o.view(torch.int16), o0.view(torch.int16)), f"call {i}: o"
         assert torch.equal(ht.view(torch.int32), h0.view(torch.int32)), f"call {i}: ht"
+
+
+def test_fused_forward_leases_no_workspace(gpu_device):
+    """A fused forward keeps its records in LDS: it leases nothing from the
+    workspace pool (B=16 T=512 H=32 would otherwise pin 272 MiB), while a
+    two-stage forward of the same inputs does."""
+    c = _inputs(16, 512, 32, 32, 16, seed=17, gdt="bf16", in_kernel_gate=True)
+    workspace.clear()
+    o1, ht1 = _run(c, gpu_device, None, True, True, True, None)
+    assert workspace.pooled_bytes() == 0
+    o2, ht2 = _run(c, gpu_device, None, True, True, True, 0)
+    assert workspace.pooled_bytes() >= 16 * 32 * 32 * 17408
+    workspace.clear()
+    assert torch.equal(o1, o2) and torch.equal(ht1, ht2)
+
+
+def test_varlen_max_seqlen_hint_keeps_the_results(gpu_device):
+    """With cu_seqlens, max_seqlen only steers the choice of kernels: one
+    long sequence among short ones (256 pairs) takes the two stages with the
+    hint and the fused kernel without it, and both give the same bits."""
+    lens = [2048] + [128] * 7
+    cu_list = [0]
+    for n in lens:
+        cu_list.append(cu_list[-1] + n)
+    T, HV = cu_list[-1], 32
+    dev = gpu_device
+    if len(lens) * HV < torch.cuda.get_device_properties(dev).multi_processor_count:
+        pytest.skip("the case needs at least as many (sequence, head) pairs as CUs")
+    c = _inputs(1, T, HV, HV, len(lens), seed=19, gdt="bf16", in_kernel_gate=True)
+    cu = torch.tensor(cu_list, dtype=torch.int32, device=dev)
+    kw = dict(scale=0.1, initial_state=c["h0"].to(dev), output_final_state=True,
+              use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True,
+              use_beta_sigmoid_in_kernel=True, lower_bound=-5.0, A_log=c["A_log"].to(dev),
+              dt_bias=c["dt_bias"].to(dev), cu_seqlens=cu)
+    args = [c[x].to(dev) for x in ("q", "k", "v", "g", "beta")]
+    workspace.clear()
+    o1, ht1 = kda_bt16_fwd(*args, **kw)  # 256 pairs: fused
+    torch.cuda.synchronize()
+    assert workspace.pooled_bytes() == 0
+    o2, ht2 = kda_bt16_fwd(*args, max_seqlen=max(lens), **kw)  # skewed: two stages
+    torch.cuda.synchronize()
+    assert workspace.pooled_bytes() > 0
+    workspace.clear()
+    assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
+    assert torch.equal(ht1.view(torch.int32), ht2.view(torch.int32))

@@ -3,26 +3,21 @@ against stage 2 with one tile per work-group (csrc/kda_k2.hip), bit for
 bit: the two run the same arithmetic in the same order (kernels.py:225-302),
 only the division of the work differs.
 
-``KDA_BT16_K2_TILES`` forces the tiles per work-group (1: kda_k2.hip; 2, 4,
-8: kda_k2w.hip) over the launch heuristic, which picks several tiles only
-when (sequences x heads x 8) exceeds the CU count, and
-``KDA_BT16_K2_WAVE_TILES`` the tiles per compute wave of kda_k2w.hip (1 or
-2).
+``forward_choice(k2_tiles=...)`` (the ``k2_tiles`` field of the C ABI's
+arguments) forces the tiles per work-group (1: kda_k2.hip; 2, 4, 8:
+kda_k2w.hip) over the launch heuristic, which picks several tiles only when
+(sequences x heads x 8) exceeds the CU count, and ``k2_wave_tiles`` the
+tiles per compute wave of kda_k2w.hip (1 or 2).
 """
 
 from __future__ import annotations
 
-import os
-
 import pytest
 import torch
 
-from kda_bt16 import kda_bt16_fwd
+from kda_bt16 import forward_choice, kda_bt16_fwd
 
 pytestmark = pytest.mark.gpu
-
-ENV = "KDA_BT16_K2_TILES"
-ENV_WAVE = "KDA_BT16_K2_WAVE_TILES"
 
 # name, B, T, H, HV, cu_seqlens, state_v_first, h0
 CASES = [
@@ -52,13 +47,7 @@ def _inputs(B, T, H, HV, S, seed):
 
 
 def _run(c, dev, cu, svf, h0, tiles, wave_tiles=None):
-    old = {e: os.environ.get(e) for e in (ENV, ENV_WAVE)}
-    os.environ[ENV] = str(tiles)
-    if wave_tiles is None:
-        os.environ.pop(ENV_WAVE, None)
-    else:
-        os.environ[ENV_WAVE] = str(wave_tiles)
-    try:
+    with forward_choice(k2_tiles=tiles, k2_wave_tiles=wave_tiles or 0):
         init = None
         if h0:
             init = c["h0"] if svf else c["h0"].transpose(-1, -2).contiguous()
@@ -71,12 +60,6 @@ def _run(c, dev, cu, svf, h0, tiles, wave_tiles=None):
             cu_seqlens=None if cu is None else torch.tensor(cu, dtype=torch.int32, device=dev))
         torch.cuda.synchronize()
         return o, ht
-    finally:
-        for e, v in old.items():
-            if v is None:
-                os.environ.pop(e, None)
-            else:
-                os.environ[e] = v
 
 
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
@@ -100,16 +83,11 @@ def test_heuristic_takes_the_wide_kernel_for_many_heads(gpu_device):
     default and gives the one-tile result."""
     c = _inputs(1, 64, 96, 96, 1, seed=9)
     o1, ht1 = _run(c, gpu_device, None, True, True, 1)
-    old = os.environ.pop(ENV, None)
-    try:
-        o, ht = kda_bt16_fwd(
-            *(c[x].to(gpu_device) for x in ("q", "k", "v", "g", "beta")), scale=0.1,
-            initial_state=c["h0"].to(gpu_device), output_final_state=True,
-            use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True,
-            use_beta_sigmoid_in_kernel=True, lower_bound=-5.0, A_log=c["A_log"].to(gpu_device),
-            dt_bias=c["dt_bias"].to(gpu_device))
-        torch.cuda.synchronize()
-    finally:
-        if old is not None:
-            os.environ[ENV] = old
+    o, ht = kda_bt16_fwd(
+        *(c[x].to(gpu_device) for x in ("q", "k", "v", "g", "beta")), scale=0.1,
+        initial_state=c["h0"].to(gpu_device), output_final_state=True,
+        use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True,
+        use_beta_sigmoid_in_kernel=True, lower_bound=-5.0, A_log=c["A_log"].to(gpu_device),
+        dt_bias=c["dt_bias"].to(gpu_device))
+    torch.cuda.synchronize()
     assert torch.equal(o, o1) and torch.equal(ht, ht1)

@@ -17,7 +17,8 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from kda_bt16 import _hip, chunk_kda, dispatch, fused_recurrent_kda, kda_bt16_fwd, kda_recurrent_fwd
+from kda_bt16 import (_hip, chunk_kda, dispatch, forward_choice, fused_recurrent_kda, kda_bt16_fwd,
+                      kda_recurrent_fwd)
 from kda_oracle import RCP_LN2, chunked_reference, per_sequence, recurrent_gold
 from kda_testlib import assert_close_rel, maxdiff
 
@@ -216,18 +217,17 @@ MS_LENS = [0, 33, 16, 0, 0, 129, 1, 47, 0, 200, 15, 17, 0, 64, 3, 90, 31, 0, 48,
                          [(True, True, True), (False, True, True), (True, False, True),
                           (True, True, False)])
 @pytest.mark.parametrize("k2_tiles", ["1", None], ids=["one_tile_ms", "default"])
-def test_varlen_multi_sequence_work_groups(with_h0, with_ht, vfirst, k2_tiles, gpu_device,
-                                           monkeypatch):
-    """Several sequences per stage-2 work-group (KDA_BT16_K2_TILES=1 forces
-    the one-tile kernel, which then groups sequences) and the default, which
+def test_varlen_multi_sequence_work_groups(with_h0, with_ht, vfirst, k2_tiles, gpu_device):
+    """Several sequences per stage-2 work-group (k2_tiles=1 forces the
+    one-tile kernel, which then groups sequences) and the default, which
     takes several value tiles per work-group here; each sequence equals its
-    own call.  KDA_BT16_FUSED=0 keeps the two stages: with 320 (sequence,
-    head) pairs the forward would otherwise run the fused kernel."""
-    monkeypatch.setenv("KDA_BT16_FUSED", "0")
-    if k2_tiles is None:
-        monkeypatch.delenv("KDA_BT16_K2_TILES", raising=False)
-    else:
-        monkeypatch.setenv("KDA_BT16_K2_TILES", k2_tiles)
+    own call.  fused=False keeps the two stages: with 320 (sequence, head)
+    pairs the forward would otherwise run the fused kernel."""
+    with forward_choice(fused=False, k2_tiles=int(k2_tiles or 0)):
+        _multi_sequence_case(with_h0, with_ht, vfirst, gpu_device)
+
+
+def _multi_sequence_case(with_h0, with_ht, vfirst, gpu_device):
     cu_list = [0]
     for n in MS_LENS:
         cu_list.append(cu_list[-1] + n)
@@ -261,14 +261,15 @@ def test_varlen_multi_sequence_work_groups(with_h0, with_ht, vfirst, k2_tiles, g
 
 
 @pytest.mark.parametrize("k2_tiles", ["1", None], ids=["one_tile_ms", "default"])
-def test_fixed_length_batch_multi_sequence_work_groups(k2_tiles, gpu_device, monkeypatch):
+def test_fixed_length_batch_multi_sequence_work_groups(k2_tiles, gpu_device):
     """B = 8 rows of 300 tokens, HV = 8: 512 triples, so stage 2 takes two
-    or more rows per work-group (KDA_BT16_K2_TILES=1), or several value
-    tiles per work-group (the default); each row equals its own call."""
-    if k2_tiles is None:
-        monkeypatch.delenv("KDA_BT16_K2_TILES", raising=False)
-    else:
-        monkeypatch.setenv("KDA_BT16_K2_TILES", k2_tiles)
+    or more rows per work-group (k2_tiles=1), or several value tiles per
+    work-group (the default); each row equals its own call."""
+    with forward_choice(k2_tiles=int(k2_tiles or 0)):
+        _fixed_length_rows_case(gpu_device)
+
+
+def _fixed_length_rows_case(gpu_device):
     B, T, HV = 8, 300, 8
     c = _inputs(T, 2, HV, seed=73, B=B)
     d = _dev(c, gpu_device)

@@ -29,13 +29,18 @@ def _args(**kw):
     return a
 
 
+@pytest.mark.skipif(torch.cuda.is_available(),
+                    reason="stand-in device pointers are passed to a launching entry point only "
+                           "where no GPU is present")
 def test_noalloc_refuses_oversized_geometry_without_launching():
-    fake = 1 << 40  # never dereferenced: the size check fails before any HIP call
+    fake = 1 << 40  # never dereferenced: the size check fails before any launch
     full = dict(q=fake, k=fake, v=fake, g=fake, beta=fake, o=fake)
     f = _hip.lib().kda_bt16_fwd_noalloc_hip
-    # B=1 T=8192 HV=32 needs 272 MiB of records
-    a = _args(B=1, T=8192, H=32, HV=32, **full)
+    # B=1 T=8192 HV=32 needs 272 MiB of records, on the two-stage path (a
+    # fused geometry would launch: checked first, and the call skipped)
+    a = _args(B=1, T=8192, H=32, HV=32, flags=_hip.TWO_STAGE, **full)
     assert _hip.workspace_bytes_args(a) > _hip.NOALLOC_MAX_WORKSPACE
+    assert _hip.fwd_plan(a) == 0
     assert f(ctypes.byref(a), None) == _hip.ESCRATCH
     assert b"static" in _hip.lib().kda_bt16_strerror(_hip.ESCRATCH)
     # the ordinary argument checks come first
@@ -112,3 +117,51 @@ def test_noalloc_equals_fwd_on_consecutive_calls(gpu_device):
         assert torch.isfinite(o_ref.float()).all(), name
         assert torch.equal(o.view(torch.int16), o_ref.view(torch.int16)), f"{name}: o differs"
         assert torch.equal(ht.view(torch.int32), ht_ref.view(torch.int32)), f"{name}: ht differs"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,T,H", [(2, 1024, 4), (16, 256, 32)], ids=["two_stage", "fused"])
+def test_noalloc_graph_replays_equal_fwd(B, T, H, gpu_device):
+    """kda_bt16_fwd_noalloc_hip captured into a HIP graph (torch.cuda.CUDAGraph)
+    after one eager call on the device (which looks up the scratch's
+    address), replayed on new inputs copied into the captured buffers, with
+    eager work and a synchronisation between replays: every replay equals
+    kda_bt16_fwd on the same inputs, bit for bit."""
+    dev = gpu_device
+    print(f"[noalloc graph] B={B} T={T} H={H}", flush=True)
+    cases = [_case(B, T, H, H, seed=20 + i, h0=True, svf=True) for i in range(3)]
+    for c in cases:
+        for x in ("q", "k", "v", "g", "beta", "A_log", "dt_bias", "h0"):
+            c[x] = c[x].to(dev)
+    kw = dict(scale=0.1, output_final_state=True, use_qk_l2norm_in_kernel=True,
+              use_gate_in_kernel=True, use_beta_sigmoid_in_kernel=True, lower_bound=-5.0)
+    eager = []
+    for c in cases:
+        o, ht = kda_bt16_fwd(c["q"], c["k"], c["v"], c["g"], c["beta"], initial_state=c["h0"],
+                             A_log=c["A_log"], dt_bias=c["dt_bias"], **kw)
+        eager.append((o.clone(), ht.clone()))
+    names = ("q", "k", "v", "g", "beta", "A_log", "dt_bias", "h0")
+    st = {x: cases[0][x].clone() for x in names}
+    o = torch.empty(B, T, H, 128, dtype=torch.bfloat16, device=dev)
+    ht = torch.empty(B, H, 128, 128, dtype=torch.float32, device=dev)
+    args = _make_args(st["q"], st["k"], st["v"], st["g"], st["beta"], 0.1, -5.0, st["A_log"],
+                      st["dt_bias"], st["h0"], o, ht, None, 0, _flags(True, True, True, True))
+    fused = _hip.fwd_plan(args) == 1
+    assert fused == (B * H * 2 > torch.cuda.get_device_properties(dev).multi_processor_count)
+    # the eager call first: on the two-stage path it looks up the scratch
+    _hip.call("kda_bt16_fwd_noalloc_hip", args, torch.cuda.current_stream(dev).cuda_stream)
+    torch.cuda.synchronize(dev)
+    assert torch.equal(o, eager[0][0]) and torch.equal(ht, eager[0][1])
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _hip.call("kda_bt16_fwd_noalloc_hip", args, torch.cuda.current_stream(dev).cuda_stream)
+    for i, c in enumerate(cases):
+        for x in names:
+            st[x].copy_(c[x])
+        o.fill_(float("nan"))
+        ht.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize(dev)
+        _ = float(torch.randn(4096, device=dev).square().sum())  # eager work between replays
+        assert torch.equal(o.view(torch.int16), eager[i][0].view(torch.int16)), f"replay {i}: o"
+        assert torch.equal(ht.view(torch.int32), eager[i][1].view(torch.int32)), f"replay {i}: ht"
