@@ -90,7 +90,7 @@ __device__ __forceinline__ void wait_ge(const int* a, int target) {
 // A work-group that gave up a wait has read slots whose chunks it cannot
 // vouch for: this compute wave's o columns (its two value tiles) over the
 // whole sequence and its final-state rows become NaN.
-__device__ __noinline__ void mark_lost(const Params& p, const SeqSpan& sp, int hv, int ut, int lane,
+__device__ __forceinline__ void mark_lost(const Params& p, const SeqSpan& sp, int hv, int ut, int lane,
                                        f32x4 (&SA)[8], f32x4 (&SB)[8]) {
     const float nan = __builtin_nanf("");
 #pragma unroll

@@ -59,11 +59,30 @@ class Violation:
 
 def tools_available() -> bool:
     return all(os.path.exists(os.path.join(LLVM_BIN, t))
-               for t in ("llvm-objcopy", "clang-offload-bundler", "llvm-objdump"))
+               for t in ("llvm-objcopy", "clang-offload-bundler", "llvm-objdump", "llvm-readelf"))
 
 
 def disassemble(lib_path: str) -> list[str]:
     """The gfx950 disassembly of every code object bundled in `lib_path`."""
+    return _each_code_object(lib_path, [os.path.join(LLVM_BIN, "llvm-objdump"), "-d", "--mcpu=gfx950"])
+
+
+def kernel_resources(lib_path: str) -> dict[str, dict[str, int]]:
+    """Per kernel of `lib_path`'s gfx950 code objects, from their metadata
+    notes: `scratch` (private segment bytes per lane, what register spills
+    and calls need), `vgprs` and `sgprs`."""
+    out = {}
+    pat = re.compile(r"\.name:\s+(\S+).*?\.private_segment_fixed_size:\s+(\d+).*?"
+                     r"\.sgpr_count:\s+(\d+).*?\.vgpr_count:\s+(\d+)", re.S)
+    for text in _each_code_object(lib_path, [os.path.join(LLVM_BIN, "llvm-readelf"), "--notes"]):
+        for m in pat.finditer(text):
+            out[m.group(1)] = {"scratch": int(m.group(2)), "sgprs": int(m.group(3)),
+                               "vgprs": int(m.group(4))}
+    return out
+
+
+def _each_code_object(lib_path: str, tool: list[str]) -> list[str]:
+    """`tool` run on every gfx950 code object bundled in `lib_path`."""
     texts = []
     with tempfile.TemporaryDirectory() as tmp:
         fat = os.path.join(tmp, "fatbin")
@@ -81,8 +100,7 @@ def disassemble(lib_path: str) -> list[str]:
                                capture_output=True)
             if r.returncode != 0 or not os.path.getsize(co):
                 continue
-            d = subprocess.run([os.path.join(LLVM_BIN, "llvm-objdump"), "-d", "--mcpu=gfx950", co],
-                               check=True, capture_output=True, text=True)
+            d = subprocess.run([*tool, co], check=True, capture_output=True, text=True)
             texts.append(d.stdout)
     return texts
 

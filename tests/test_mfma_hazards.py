@@ -67,3 +67,16 @@ def test_library_has_no_mixed_shape_accumulation():
     n, bad = isa_check.check_library(str(lib))
     assert n > 1000, f"only {n} MFMAs found: the disassembly did not cover the kernels"
     assert not bad, "\n".join(str(v) for v in bad[:10])
+
+
+def test_no_kernel_uses_scratch():
+    """Every kernel of the built library keeps its state in registers and
+    LDS: no private (scratch) segment, which register spills and
+    non-inlined calls would need.  A non-inlined helper in the fused kernel
+    once gave it 688 bytes of scratch per lane and made it ~3x slower with
+    the same results; this catches such a change on the CPU."""
+    res = isa_check.kernel_resources(str(_build.LIB_PATH))
+    assert len(res) >= 30, sorted(res)
+    assert any("fused_kernel" in n for n in res) and any("k2_kernel" in n for n in res)
+    spill = {n: r["scratch"] for n, r in res.items() if r["scratch"]}
+    assert not spill, spill
