@@ -743,6 +743,11 @@ def run_forward(args, dev, name: str, *, cpu: bool, inputs_cpu=None) -> dict:
             "heads": h,
             "parallelism": "none (1 GPU)",
         },
+        # everything that runs on the GPU before the timed region: the
+        # precision check (one forward and the fp32 recurrence), each stage
+        # timed on its own (1 + reps launches each), then the warmup forwards
+        "pre_timed_launches": {"forwards": 1 + args.warmup, "fp32_recurrence": 1,
+                               "stage1": 1 + reps, "stage2": 1 + reps},
         "latency_ms": {"p20": round(lat[len(lat) // 5], 4),
                        "median": round(statistics.median(lat), 4),
                        "p80": round(lat[(4 * len(lat)) // 5], 4)},

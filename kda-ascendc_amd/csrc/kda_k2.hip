@@ -36,7 +36,8 @@ namespace kda {
 namespace {
 
 // Record ring: RING slots, each the 13 KiB every value tile needs plus the
-// 1 KiB pair of u slices that holds this tile's (14 loads of 1 KiB).
+// 1 KiB pair of u slices that holds this tile's; only this tile's 512-byte
+// slice is loaded into it (13 loads of 1 KiB and one of 512 bytes).
 // Chunk j lives in slot j % RING.  The state wave reads it during chunk
 // j - 1 and the output wave, two chunks behind, during chunk j + 2; the
 // copy wave refills the slot with chunk j + RING during chunk
@@ -86,19 +87,23 @@ __device__ __forceinline__ void wait_chunk_ladder(int n_after) {
 template <int NL = LOADS_PER_CHUNK>
 __device__ __forceinline__ void wait_chunk(int n_after) { wait_chunk_ladder<LEAD - 2, NL>(n_after); }
 
-// One chunk's copy: 13 shared KiB, then the u pair.  Buffer loads with the
-// chunk offset in an SGPR and a fixed per-lane VGPR offset.
+// One chunk's copy: 13 shared KiB, then this tile's 512-byte u slice (half
+// a load: lanes 0-31) at its place in the slot's u pair, u_lds.  Buffer
+// loads with the chunk offset in an SGPR and a fixed per-lane VGPR offset.
 // NL == LOADS_NO_QG: without qg (its slot bytes are left as they were).
 template <int NL = LOADS_PER_CHUNK>
 __device__ __forceinline__ void issue_chunk(__amdgpu_buffer_rsrc_t rs, uint32_t chunk_off,
-                                            lds_u8* slot, uint32_t u_off, uint32_t voff16) {
+                                            lds_u8* slot, uint32_t u_off, uint32_t u_lds,
+                                            uint32_t voff16) {
 #pragma unroll
-    for (int i = 0; i < LOADS_PER_CHUNK; ++i) {
+    for (int i = 0; i < SHARED_LOADS; ++i) {
         if (NL == LOADS_NO_QG && i >= REC_QG / 1024 && i < REC_KG / 1024) continue;
-        const uint32_t src = i < SHARED_LOADS ? chunk_off + i * 1024 : chunk_off + u_off;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_u8*)(slot + i * 1024), 16, voff16, src,
-                                                 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_u8*)(slot + i * 1024), 16, voff16,
+                                                 chunk_off + i * 1024, 0, 0);
     }
+    if (voff16 < 512)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_u8*)(slot + u_lds), 16, voff16,
+                                                 chunk_off + u_off, 0, 0);
 }
 
 // The state wave's operands of one chunk.
@@ -151,7 +156,8 @@ __device__ __forceinline__ void chunk_barrier_nodrain() {
 struct Ctx {
     __amdgpu_buffer_rsrc_t rs;  // copy: this sequence-head's records, NT * REC_BYTES bytes
     uint32_t voff16;            // copy: lane * 16
-    uint32_t u_off;             // copy: REC_U + 1024 * (vt / 2)
+    uint32_t u_off;             // copy: REC_U + 512 * vt, this tile's u slice in the record
+    uint32_t u_lds;             // copy: REC_SHARED + 512 * (vt % 2), its place in a ring slot
     uint16_t* obase;            // output: o[first token, hv, 16*vt + 4*((lane%16)/4)]
     int64_t orow_stride;        // output: elements between consecutive tokens of o
     uint16_t* trh;              // training: h of the first record, this tile, column 4*((lane%16)/4)
@@ -370,7 +376,7 @@ template <int S, int NL>
 __device__ __forceinline__ void copy_step(const Ctx& cx, int c) {
     if (c + LEAD < cx.NT)
         issue_chunk<NL>(cx.rs, step_rec(cx, c + LEAD),
-                        ring_lds() + ((S + LEAD) % RING) * SLOT, cx.u_off, cx.voff16);
+                        ring_lds() + ((S + LEAD) % RING) * SLOT, cx.u_off, cx.u_lds, cx.voff16);
     // chunk c + 2 is read by the state wave after this barrier
     if (c + 2 < cx.NT) wait_chunk<NL>(min(LEAD - 2, cx.NT - 3 - c));
     copy_barrier();
@@ -422,11 +428,13 @@ __device__ __forceinline__ void copy_wave(const Params& p, Ctx& cx, const SeqSpa
     uint8_t* recs = (cx.rev ? p.ws_bwd : p.ws) + sp.rec0 * REC_BYTES;
     cx.rs = __builtin_amdgcn_make_buffer_rsrc(recs, (short)0, NT * REC_BYTES, BUF_DWORD3);
     cx.voff16 = cx.lane * 16;
-    cx.u_off = REC_U + 1024 * (cx.vt >> 1);
+    cx.u_off = REC_U + 512 * cx.vt;
+    cx.u_lds = REC_SHARED + 512 * (cx.vt & 1);
 #pragma unroll
     for (int d = 0; d < LEAD; ++d)
         if (d < NT)
-            issue_chunk<NL>(cx.rs, step_rec(cx, d), ring_lds() + d * SLOT, cx.u_off, cx.voff16);
+            issue_chunk<NL>(cx.rs, step_rec(cx, d), ring_lds() + d * SLOT, cx.u_off, cx.u_lds,
+                            cx.voff16);
     // chunks 0 and 1 (those that exist) before the first barrier
     wait_chunk<NL>(NT >= 2 ? min(LEAD, NT) - 2 : 0);
     copy_barrier();
@@ -822,7 +830,7 @@ __device__ __forceinline__ void issue_ms(const Params& p, const Ctx& cx, const S
                                          lds_u8* slot) {
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         p.ws + w.sp.rec0 * REC_BYTES, (short)0, w.sp.nt * REC_BYTES, BUF_DWORD3);
-    issue_chunk(rs, (uint32_t)w.c * REC_BYTES, slot, cx.u_off, cx.voff16);
+    issue_chunk(rs, (uint32_t)w.c * REC_BYTES, slot, cx.u_off, cx.u_lds, cx.voff16);
 }
 
 template <int S>
@@ -844,7 +852,8 @@ __device__ __forceinline__ void copy_wave_ms(const Params& p, Ctx& cx, const MsC
     SeqWalk w;
     walk_init(p, m.hv, m.n0, m.n1, w);
     cx.voff16 = cx.lane * 16;
-    cx.u_off = REC_U + 1024 * (cx.vt >> 1);
+    cx.u_off = REC_U + 512 * cx.vt;
+    cx.u_lds = REC_SHARED + 512 * (cx.vt & 1);
 #pragma unroll
     for (int d = 0; d < LEAD; ++d) {
         if (d < m.J) {

@@ -22,7 +22,8 @@ Passes (``PASSES``): ``trace`` (``--kernel-trace --stats``), ``fetch``
 (``FETCH_SIZE``), ``write`` (``WRITE_SIZE``), ``mfma`` (matrix-op counts and
 busy cycles), ``texture`` (the per-CU vector-memory path), ``lds`` (LDS
 instructions, bank conflicts and waits), ``l2write`` (L1-to-L2 and L2-to-HBM
-write requests).  Each pass is its own process under ``timeout -s KILL``,
+write requests), ``waves`` (where the waves' cycles go: waiting, issuing,
+by instruction kind).  Each pass is its own process under ``timeout -s KILL``,
 with at most the counters one rocprofv3 run can collect.
 
 HBM bytes: rocprofv3's ``FETCH_SIZE`` / ``WRITE_SIZE`` (KiB per dispatch)
@@ -64,6 +65,9 @@ PASSES = {
             "GRBM_GUI_ACTIVE"],
     "l2write": ["--pmc", "TCP_TCC_WRITE_REQ_sum", "TCC_EA0_WRREQ_sum", "TCC_EA0_WRREQ_64B_sum",
                 "GRBM_GUI_ACTIVE"],
+    "waves": ["--pmc", "SQ_WAVE_CYCLES", "SQ_BUSY_CYCLES", "SQ_WAIT_ANY", "SQ_WAIT_INST_ANY",
+              "SQ_ACTIVE_INST_ANY", "SQ_ACTIVE_INST_VALU", "SQ_ACTIVE_INST_LDS", "SQ_ACTIVE_INST_MISC",
+              "GRBM_GUI_ACTIVE"],
 }
 DEFAULT_PASSES = ("trace", "fetch", "write", "mfma")
 PASS_LIMIT_S = 180
@@ -375,7 +379,8 @@ def summarize(args) -> int:
         m = counter_summary(d / "mfma", manifest, "mfma")
         (prof / f"{prefix}_mfma.json").write_text(json.dumps(m, indent=1) + "\n")
         written.append(f"{prefix}_mfma.json")
-    extra = {p: counter_summary(d / p, manifest, p) for p in ("texture", "lds", "l2write") if p in passes}
+    extra = {p: counter_summary(d / p, manifest, p) for p in ("texture", "lds", "l2write", "waves")
+             if p in passes}
     if extra:
         (prof / f"{prefix}_counters.json").write_text(json.dumps(extra, indent=1) + "\n")
         (prof / f"{prefix}_counters.md").write_text(counters_md(extra, manifest))
