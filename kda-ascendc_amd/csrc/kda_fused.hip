@@ -62,6 +62,7 @@ __shared__ __attribute__((aligned(16))) float f_bias[DK];  // the head's dt_bias
 __shared__ int f_full[F_RING];
 __shared__ int f_done[F_RING];
 __shared__ int f_aborted;
+__shared__ int f_counted;  // the work-group's give-up has been counted
 
 // Work-groups that gave up a wait on this device since the library was
 // loaded or the count was reset (fused_abort_count).
@@ -80,10 +81,7 @@ __device__ __forceinline__ void wait_ge(const int* a, int target) {
         }
         __builtin_amdgcn_s_sleep(1);
     }
-    // the first wave of the work-group to give up counts it
-    if ((threadIdx.x & 63) == 0 &&
-        __hip_atomic_exchange(&f_aborted, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) == 0)
-        __hip_atomic_fetch_add(&g_aborts, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&f_aborted, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     asm volatile("" ::: "memory");
 }
 
@@ -333,7 +331,10 @@ __global__ __launch_bounds__(F_THREADS) void fused_kernel(Params p) {
         f_full[threadIdx.x] = 0;
         f_done[threadIdx.x] = 0;
     }
-    if (threadIdx.x == 0) f_aborted = 0;
+    if (threadIdx.x == 0) {
+        f_aborted = 0;
+        f_counted = 0;
+    }
     if (threadIdx.x < DK) f_bias[threadIdx.x] = p.use_gate && p.dt_bias ? p.dt_bias[hv * DK + threadIdx.x] : 0.f;
     __syncthreads();
 
@@ -361,7 +362,16 @@ __global__ __launch_bounds__(F_THREADS) void fused_kernel(Params p) {
     cx.obase[1] = cx.obase[0] + 16;
     cx.orow_stride = (int64_t)p.HV * DK;
     for (int c = 0; c < cx.NT; c += F_RING) fused_round<0, F_RING>(cx, c, SA, SB, ut);
-    if (lds_load(&f_aborted)) mark_lost(p, sp, hv, ut, lane, SA, SB);
+    // Every give-up is seen here by at least one compute wave: a producer
+    // marks the work-group before it publishes the chunk it gave up on, and
+    // this wave consumed every chunk; a compute wave sees its own.  The first
+    // compute wave to see it counts the work-group, outside every wait loop.
+    if (lds_load(&f_aborted)) {
+        if (lane == 0 &&
+            __hip_atomic_exchange(&f_counted, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) == 0)
+            __hip_atomic_fetch_add(&g_aborts, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        mark_lost(p, sp, hv, ut, lane, SA, SB);
+    }
     store_state(p, sbase, va, q4, SA);
     store_state(p, sbase, va + 16, q4, SB);
     __builtin_amdgcn_endpgm();
