@@ -55,6 +55,32 @@ def test_headline_bytes_are_the_roofline_rule():
     assert k1 + k2 == B * T * H * 1282 + B * H * STATE_BYTES + 516 * H
 
 
+def test_roofline_is_the_dominant_kernels():
+    """achieved = the forward's algorithmic bytes / the longest kernel's
+    mean launch time; traffic = that kernel's bytes per launch; the whole
+    forward's figures beside them (c2-like numbers, stage 2 the longer)."""
+    kern = {"k1": {"ms": 0.118}, "k2": {"ms": 0.150}}
+    traffic = {"k1": 558_000_000, "k2": 362_000_000}
+    r = bench._dominant_roofline(kern, traffic, 340_000_000, 31_000_000_000, 0.26, False)
+    assert r["kernel"].startswith("stage 2")
+    assert r["achieved"] == pytest.approx(340e6 / 0.150 / 1e6, rel=1e-4)
+    assert r["frac"] == pytest.approx(r["achieved"] / bench.HBM_PEAK_GBS, rel=1e-3)
+    assert r["traffic"] == 362_000_000 and r["kernel_ms_events"] == 0.15
+    f = r["forward"]
+    assert f["achieved"] == pytest.approx(340e6 / 0.26 / 1e6, rel=1e-4)
+    assert f["traffic"] == 920_000_000
+    # stage 1 the longer (c3-like); no profile: traffic unknown
+    kern = {"k1": {"ms": 0.345}, "k2": {"ms": 0.267}}
+    r = bench._dominant_roofline(kern, None, 1_020_000_000, 93e9, 0.61, False)
+    assert r["kernel"].startswith("stage 1") and r["traffic"] is None
+    assert r["forward"]["traffic"] is None
+    # fused: one launch, the forward itself
+    r = bench._dominant_roofline({"fused": {"ms": 0.5}}, {"fused": 1_430_000_000}, 1_411_000_000,
+                                 124e9, 0.5, True)
+    assert r["kernel"].startswith("fused_kernel") and r["traffic"] == 1_430_000_000
+    assert r["achieved"] == r["forward"]["achieved"]
+
+
 def _run(*args):
     return subprocess.run([sys.executable, str(ROOT / "bench.py"), *args], capture_output=True,
                           text=True, timeout=300, cwd=ROOT)
