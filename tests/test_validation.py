@@ -201,3 +201,64 @@ def test_recurrent_host_errors():
     with pytest.raises(ValueError, match="ROCm GPU"):
         kda_decode_step(q[:, :1], k[:, :1], v[:, :1], g[:, :1], beta[:, :1],
                         torch.zeros(B, H, D, D))
+
+
+def test_max_seqlen_is_checked_before_the_device():
+    """The varlen hint: a non-negative int or None (chunk_kda's max_seqlen)."""
+    q, k, v, g, beta = _inputs()
+    for bad in (-1, 3.5, "16"):
+        with pytest.raises(ValueError, match="max_seqlen must be a non-negative int or None"):
+            kda_bt16_fwd(q, k, v, g, beta, max_seqlen=bad)
+    with pytest.raises(ValueError, match="ROCm GPU"):
+        kda_bt16_fwd(q, k, v, g, beta, max_seqlen=16)
+
+
+def test_forward_choice_rejects_unknown_widths():
+    from kda_bt16 import forward_choice
+
+    for kw, msg in ((dict(k2_tiles=3), "k2_tiles must be 0, 1, 2, 4 or 8"),
+                    (dict(k2_tiles=16), "k2_tiles must be 0, 1, 2, 4 or 8"),
+                    (dict(k2_wave_tiles=4), "k2_wave_tiles must be 0, 1 or 2")):
+        with pytest.raises(ValueError, match=msg):
+            with forward_choice(**kw):
+                pass
+
+
+def test_forward_choice_reaches_the_abi_arguments():
+    """forward_choice sets the ABI 4 flags and fields of the arguments the
+    forward passes on (built here from CPU tensors; nothing is launched),
+    nests, restores the enclosing choice, and is per thread."""
+    import threading
+
+    from kda_bt16 import _hip, forward_choice
+    from kda_bt16.kernels import _make_args
+
+    q, k, v, g, beta = _inputs()
+
+    def args(flags=0):
+        return _make_args(q, k, v, g, beta, 0.088, -5.0, None, None, None, None, None, None, 0,
+                          flags)
+
+    a = args()
+    assert not a.flags & (_hip.FUSED_KERNEL | _hip.TWO_STAGE) and a.k2_tiles == a.k2_wave_tiles == 0
+    with forward_choice(fused=False, k2_tiles=4, k2_wave_tiles=1):
+        a = args()
+        assert a.flags & _hip.TWO_STAGE and not a.flags & _hip.FUSED_KERNEL
+        assert (a.k2_tiles, a.k2_wave_tiles) == (4, 1)
+        # use_fused_kernel=True (the flag) wins over fused=False
+        a = args(_hip.FUSED_KERNEL)
+        assert a.flags & _hip.FUSED_KERNEL and not a.flags & _hip.TWO_STAGE
+        with forward_choice(fused=True):
+            a = args()
+            assert a.flags & _hip.FUSED_KERNEL and not a.flags & _hip.TWO_STAGE
+            assert (a.k2_tiles, a.k2_wave_tiles) == (0, 0)
+        a = args()
+        assert a.flags & _hip.TWO_STAGE and a.k2_tiles == 4
+        seen = []
+        t = threading.Thread(target=lambda: seen.append(args()))
+        t.start()
+        t.join()
+        assert not seen[0].flags & (_hip.FUSED_KERNEL | _hip.TWO_STAGE)
+        assert seen[0].k2_tiles == 0
+    a = args()
+    assert not a.flags & (_hip.FUSED_KERNEL | _hip.TWO_STAGE) and a.k2_tiles == 0
