@@ -191,9 +191,10 @@ int kda_bt16_fwd_plan(const KdaBt16Args* args);
  * device since the library was loaded or the count last reset.  No
  * counterpart in the reference.  The fused kernel's waves meet through LDS
  * flags, and every wait is bounded (2^22 polls) so that a stalled
- * work-group cannot hang the GPU; one that runs out writes NaN over its
- * (sequence, value head)'s o rows and final state and adds 1 to this
- * count.  Synchronous: it waits for the device's work to finish.  With
+ * work-group cannot hang the GPU; one that runs out writes NaN over the o
+ * columns and final-state rows of its compute waves that had not finished
+ * (a wave that finished first consumed only completed chunks) and adds 1
+ * to this count.  Synchronous: it waits for the device's work to finish.  With
  * `reset` non-zero the count is set back to 0 after it is read.  Not for
  * use during graph capture. */
 int kda_bt16_fused_aborts(uint32_t* count, int32_t reset);

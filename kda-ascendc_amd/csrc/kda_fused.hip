@@ -30,8 +30,9 @@
 // in order), so the waits always end.  Each wait is also bounded (SPIN_LIMIT
 // polls) so that a stalled work-group cannot hang the GPU: a bound that runs
 // out marks the work-group aborted, after which no wave waits again; the
-// work-group drains, writes NaN over its o rows and final state, and adds 1
-// to a device-wide count that the host reads (fused_abort_count).
+// work-group drains, its compute waves that had not finished write NaN over
+// their o columns and final-state rows, and it adds 1 to a device-wide
+// count that the host reads (fused_abort_count).
 #include "kda_common.h"
 #include "kda_k1_chunk.h"
 #include "kda_k2_shared.h"

@@ -200,8 +200,9 @@ def fwd_plan(args: KdaBt16Args) -> int:
 
 def fused_aborts(reset: bool = False) -> int:
     """``kda_bt16_fused_aborts``: fused-kernel work-groups on the current
-    device that gave up a bounded wait (their o rows and final state are
-    NaN) since load or the last reset.  Waits for the device's work."""
+    device that gave up a bounded wait (the o columns and final-state rows
+    of their compute waves still running are NaN) since load or the last
+    reset.  Waits for the device's work."""
     n = ctypes.c_uint32(0)
     rc = int(lib().kda_bt16_fused_aborts(ctypes.byref(n), 1 if reset else 0))
     if rc != 0:

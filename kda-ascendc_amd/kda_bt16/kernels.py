@@ -103,8 +103,9 @@ def fused_abort_count(reset: bool = False, device: torch.device | int | None = N
     """Fused-kernel work-groups on ``device`` (default: the current one)
     that gave up a bounded wait since the library was loaded or the count
     last reset (``kda_bt16_fused_aborts``).  Such a work-group writes NaN
-    over its (sequence, value head)'s o rows and final state instead of
-    hanging the GPU.  Waits for the device's work to finish."""
+    over the o columns and final-state rows of its compute waves that had
+    not finished, instead of hanging the GPU.  Waits for the device's work
+    to finish."""
     with torch.cuda.device(torch.cuda.current_device() if device is None else device):
         return _hip.fused_aborts(reset)
 
