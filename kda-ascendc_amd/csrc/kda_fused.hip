@@ -56,7 +56,7 @@ static_assert(F_RING >= F_NP, "every producer can hold a slot");
 constexpr int ST_Q = 0, ST_K = 4096, ST_G = 8192, STAGE_BYTES = 16384;
 
 // The work-group's LDS.
-__shared__ __attribute__((aligned(1024))) uint8_t f_ring[F_RING][REC_BYTES];
+__shared__ __attribute__((aligned(1024))) uint8_t f_ring[F_RING][FREC_BYTES];
 __shared__ __attribute__((aligned(1024))) uint8_t f_stage[F_NP][STAGE_BYTES];
 __shared__ __attribute__((aligned(16))) uint8_t f_scratch[F_NP][K1_SCRATCH];
 __shared__ __attribute__((aligned(16))) float f_bias[DK];  // the head's dt_bias (zeros without it)
@@ -105,10 +105,27 @@ __device__ __forceinline__ void mark_lost(const Params& p, const SeqSpan& sp, in
         *reinterpret_cast<u32x4*>(base + (int64_t)r * p.HV * DK) = nan8;
 }
 
-// The compute waves' side of the LDS flags (wide_step's hooks).
+// The compute waves' side of the LDS flags (wide_step's hooks), and their
+// share of stage 1: u of their two tiles, formed from the raw v tiles,
+// bf16(A_inv) and beta the producers leave in u's place (FREC_*), with the
+// instructions stage 1 uses (form_u).  The producers pace the work-group;
+// this moves ~6 % of their issue work to the compute waves, which wait for
+// them most of the time.
 template <int S>
 struct FlagHooks {
+    u32x2 v[2], a;  // raw v of the two tiles, bf16(A_inv) as the A operand
+    float beta;     // beta of this lane's row
     __device__ __forceinline__ void ready(int c) { wait_ge(&f_full[S], c + 1); }
+    __device__ __forceinline__ void read_u(const uint8_t* slot, int lane, int ut) {
+        v[0] = *reinterpret_cast<const u32x2*>(slot + REC_U + ut * 512 + lane * 8);
+        v[1] = *reinterpret_cast<const u32x2*>(slot + REC_U + (ut + 1) * 512 + lane * 8);
+        a = *reinterpret_cast<const u32x2*>(slot + FREC_A + lane * 8);
+        beta = *reinterpret_cast<const float*>(slot + FREC_BETA + 4 * (lane & 15));
+    }
+    __device__ __forceinline__ f32x4 u_start(int t) const {
+        const int lane = threadIdx.x & 63;
+        return unpack_u(form_u(v[t], beta, as_i16x4(a), eye_operand(lane)));
+    }
     __device__ __forceinline__ void consumed() {
         // the slot reads have completed before they are counted
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -252,7 +269,7 @@ __device__ __forceinline__ void produce(const Params& p, int hv, int c, int c_ne
     wait_ge(&f_done[s], F_NCW * (c / F_RING));
     float* sL = reinterpret_cast<float*>(scr);
     float* sX = reinterpret_cast<float*>(scr + K1_SCRATCH_L);
-    k1_compute<K1_FWD, FULL, GB16>(p, hv, c, sp, in, f_bias, ea, sL, sX, f_ring[s]);
+    k1_compute<K1_FWD, FULL, GB16, true>(p, hv, c, sp, in, f_bias, ea, sL, sX, f_ring[s]);
     // the record's LDS writes have completed before the slot is marked full
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     if (lane == 0) __hip_atomic_store(&f_full[s], c + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);

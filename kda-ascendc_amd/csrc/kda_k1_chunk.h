@@ -59,6 +59,21 @@ __device__ __forceinline__ i16x4 tile_T(u32x2 f, i16x4 eye) {
     return as_i16x4(pack4(mfma_bf16_16x16x16(as_i16x4(f), eye, zero)));
 }
 
+// Tile vt of u = bf16(A @ bf16(v * beta)) (kernels.py:173-174) from the raw
+// v tile in F order (lane (r, q4) holding v[r][16*vt + 4*q4 + i]), the
+// lane's row's beta and bf16(A_inv) as the 16x16x16 A operand; it lands as
+// u[4*q4 + i][16*vt + r], the order stage 2 subtracts it in.  Stage 1 and
+// the fused forward's compute waves both form u with it.
+__device__ __forceinline__ u32x2 form_u(u32x2 v, float beta, i16x4 A_op, i16x4 eye) {
+    const float v0 = __builtin_bit_cast(float, v.x << 16);
+    const float v1 = __builtin_bit_cast(float, v.x & 0xffff0000u);
+    const float v2 = __builtin_bit_cast(float, v.y << 16);
+    const float v3 = __builtin_bit_cast(float, v.y & 0xffff0000u);
+    const i16x4 vbT = tile_T(pack4(v0 * beta, v1 * beta, v2 * beta, v3 * beta), eye);
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    return pack4(mfma_bf16_16x16x16(A_op, vbT, zero));
+}
+
 // LDS scratch of one wave's k1_chunk: L and the solve's columns (fp32), in
 // bytes.
 constexpr int K1_SCRATCH_L = BT * BT * 4;
@@ -77,6 +92,18 @@ __device__ __forceinline__ void wave_lds_fence() { asm volatile("s_waitcnt lgkmc
 // record, the gram block, and the backward record without dO, which the
 // backward adds (k1_dout_kernel) once dO exists.
 enum K1Mode { K1_FWD = 0, K1_BOTH = 1, K1_SAVE = 2 };
+
+// The fused forward's ring slot (kda_fused.hip): the forward record with
+// u left to the compute waves, whose producers have the scarcer issue
+// slots.  In u's place the slot holds the chunk's raw v tiles in the
+// order u would take ([vt][lane][4] bf16, F order: lane (r, q4) holds
+// v[r][16*vt + 4*q4 + i]); then bf16(A_inv) as the 16x16x16 A operand
+// ([lane][4]) and beta per row as stage 1 applied it (fp32 [16]).  The
+// compute waves form u = bf16(A @ bf16(v * beta)) with the instructions
+// stage 1 uses (form_u), so u is the same bits.
+constexpr int FREC_A = REC_BYTES;
+constexpr int FREC_BETA = REC_BYTES + 512;
+constexpr int FREC_BYTES = REC_BYTES + 1024;
 
 // The inputs of one chunk: k1_load issues their loads, k1_compute uses
 // them, so that a caller can load the next chunk while it works on this one
@@ -160,7 +187,7 @@ __device__ __forceinline__ float k1_ea(const Params& p, int hv) {
 
 // The work on one chunk's inputs: biasp the head's dt_bias (k1_bias, or a
 // copy of it), ea = k1_ea.
-template <int K1M, bool FULL, bool GB16>
+template <int K1M, bool FULL, bool GB16, bool U_IN_SLOT = false>
 __device__ __forceinline__ void k1_compute(const Params& p, int hv, int c, const SeqSpan& sp,
                                            const K1In<GB16, K1M == K1_BOTH>& in, const float* biasp,
                                            float ea, float* sL, float* sX, uint8_t* rec) {
@@ -391,15 +418,18 @@ __device__ __forceinline__ void k1_compute(const Params& p, int hv, int c, const
     // ---- u = A @ bf16(v * beta) (kernels.py:173-174) ----------------------
     // One 16x16x16 tile per 16 value columns; u lands as
     // u[4*q4 + i][16*vt + r], the order stage 2 subtracts it in.  The
-    // transposes below go through the matrix core (tile_T).
-    {
+    // transposes below go through the matrix core (tile_T).  In the fused
+    // forward's slot the operands go in u's place instead (FREC_*).
+    if constexpr (U_IN_SLOT) {
+#pragma unroll
+        for (int vt = 0; vt < 8; ++vt)
+            *reinterpret_cast<u32x2*>(rec + REC_U + vt * 512 + lane * 8) = vp.v[vt];
+        *reinterpret_cast<u32x2*>(rec + FREC_A + lane * 8) = ainv_bf;
+        if (q4 == 0) *reinterpret_cast<float*>(rec + FREC_BETA + 4 * r) = beta;
+    } else {
 #pragma unroll
         for (int vt = 0; vt < 8; ++vt) {
-            const i16x4 vbT = tile_T(pack4(elem(vp, 4 * vt) * beta, elem(vp, 4 * vt + 1) * beta,
-                                           elem(vp, 4 * vt + 2) * beta, elem(vp, 4 * vt + 3) * beta),
-                                     eye);
-            const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-            const u32x2 ub = pack4(mfma_bf16_16x16x16(A_op, vbT, zero));
+            const u32x2 ub = form_u(vp.v[vt], beta, A_op, eye);
             *reinterpret_cast<u32x2*>(rec + REC_U + vt * 512 + lane * 8) = ub;
             if (p.dbg_u) {
 #pragma unroll

@@ -17,7 +17,6 @@ struct WideOps {
     u32x4 kg[4];  // kg, 16x16x16 A operands of the update (two k-tiles each)
     u32x2 aqk;    // Aqk, 16x16x16 A operand
     f32x2 dc;     // 2^G_last for the decay broadcast
-    u32x2 u[2];   // u of the two tiles, fp32 accumulator start (bf16 pairs)
 };
 
 __device__ __forceinline__ void read_wide_ops(const uint8_t* slot, int lane, int ut, WideOps& op) {
@@ -29,8 +28,6 @@ __device__ __forceinline__ void read_wide_ops(const uint8_t* slot, int lane, int
     }
     op.aqk = *reinterpret_cast<const u32x2*>(slot + REC_AQK + lane * 8);
     op.dc = *reinterpret_cast<const f32x2*>(slot + decay_offset(lane));
-    op.u[0] = *reinterpret_cast<const u32x2*>(slot + REC_SHARED + ut * 512 + lane * 8);
-    op.u[1] = *reinterpret_cast<const u32x2*>(slot + REC_SHARED + (ut + 1) * 512 + lane * 8);
 }
 
 __device__ __forceinline__ f32x4 unpack_u(u32x2 u) {
@@ -66,12 +63,21 @@ struct WideCtx {
 
 // How the waves of a work-group meet around one chunk of a compute wave:
 // `ready(c)` before the wave reads chunk c's operands from their ring slot,
-// `consumed()` once those reads are issued, `end()` after the chunk.
-// kda_k2w.hip: one barrier per chunk (BarrierHooks); kda_fused.hip: LDS
-// flags between the waves that form the records and those that read them.
+// `consumed()` once those reads are issued, `end()` after the chunk; and
+// where u comes from: `read_u` with the slot reads, `u_start(t)` for tile
+// t's accumulator start after them.  kda_k2w.hip: one barrier per chunk,
+// u as stage 1 stored it (BarrierHooks); kda_fused.hip: LDS flags between
+// the waves that form the records and those that read them, u formed here
+// from the operands the producers leave in its place.
 struct BarrierHooks {
+    u32x2 u[2];  // u of the two tiles (bf16 pairs)
     __device__ __forceinline__ void ready(int) {}
+    __device__ __forceinline__ void read_u(const uint8_t* slot, int lane, int ut) {
+        u[0] = *reinterpret_cast<const u32x2*>(slot + REC_SHARED + ut * 512 + lane * 8);
+        u[1] = *reinterpret_cast<const u32x2*>(slot + REC_SHARED + (ut + 1) * 512 + lane * 8);
+    }
     __device__ __forceinline__ void consumed() {}
+    __device__ __forceinline__ f32x4 u_start(int t) const { return unpack_u(u[t]); }
     __device__ __forceinline__ void end() { chunk_barrier(); }
 };
 
@@ -85,6 +91,7 @@ __device__ __forceinline__ void wide_step(const WideCtx& cx, int c, f32x4 (&SA)[
     hk.ready(c);
     WideOps cur;
     read_wide_ops(slot, cx.lane, ut, cur);
+    hk.read_u(slot, cx.lane, ut);
     u32x4 ha[4], hb[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -93,8 +100,8 @@ __device__ __forceinline__ void wide_step(const WideCtx& cx, int c, f32x4 (&SA)[
     }
     hk.consumed();
     // v_new = u - w @ hc^T: one accumulation chain per tile, from u
-    f32x4 va = unpack_u(cur.u[0]);
-    f32x4 vb = unpack_u(cur.u[1]);
+    f32x4 va = hk.u_start(0);
+    f32x4 vb = hk.u_start(1);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         va = mfma_bf16_16x16x32(as_bf16x8(cur.w[j]), as_bf16x8(ha[j]), va);
