@@ -142,7 +142,9 @@ typedef struct KdaBt16Args {
     /* The forward's kernel choices (ABI 4).  Each 0 leaves the choice to
      * the library; every choice gives the same results bit for bit. */
     int32_t k2_tiles;         /* stage-2 value tiles per work-group: 1, 2, 4 or 8 */
-    int32_t k2_wave_tiles;    /* with 2-8 tiles per work-group, tiles per compute wave: 1 or 2 */
+    int32_t k2_wave_tiles;    /* with 2-8 tiles per work-group, 1 or 2 forces compute waves
+                                 of that many whole tiles (0: a state wave per tile at 2
+                                 tiles, two-tile compute waves at 8, one-tile at 4) */
     int32_t max_seqlen;       /* with cu_seqlens: the longest sequence's length, when the
                                  caller knows it (a hint for the choice between the fused
                                  kernel and the two stages; a wrong value changes only the

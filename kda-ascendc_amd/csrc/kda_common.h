@@ -135,7 +135,8 @@ struct Params {
     int o_fp32;                  // token recurrence only: o in fp32
     // The forward's kernel choices (KdaBt16Args, ABI 4): force_fused /
     // two_stage from the flags; k2_tiles (1, 2, 4, 8) and k2_wave_tiles (1,
-    // 2) for stage 2, 0 for the library's choice; max_seqlen, with
+    // 2: kda_k2w.hip's compute waves of that many tiles) for stage 2, 0 for
+    // the library's choice; max_seqlen, with
     // cu_seqlens, the caller's hint of the longest sequence (0: unknown).
     int force_fused, two_stage;
     int k2_tiles, k2_wave_tiles;

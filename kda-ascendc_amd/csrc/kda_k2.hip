@@ -114,16 +114,25 @@ struct StateOps {
     // 2*x + 1 (x = lane % 16); the 16 lanes of a row hold their row's 32.
     f32x2 dc;
     u32x2 u;
+    u32x4 qg[4];  // split work-groups: the chunk's qg, for qg @ hc^T
 };
 
 // The prologue's read of chunk 0's operands (inside the loop the next
 // chunk's operands are read piecewise, spread through the step).
+// TPW > 1: a split work-group (below), whose slot holds the TPW u slices in
+// tile order (ut: this wave's), and whose state wave also reads qg.
+template <int TPW = 1>
 __device__ __forceinline__ void read_state_ops_a(const uint8_t* slot, int lane, int vt,
-                                                 StateOps& op) {
+                                                 StateOps& op, int ut = 0) {
+    if constexpr (TPW > 1) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            op.qg[j] = *reinterpret_cast<const u32x4*>(slot + REC_QG + j * 1024 + lane * 16);
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j)
         op.w[j] = *reinterpret_cast<const u32x4*>(slot + REC_W + j * 1024 + lane * 16);
-    op.u = *reinterpret_cast<const u32x2*>(slot + REC_SHARED + (vt & 1) * 512 + lane * 8);
+    op.u = *reinterpret_cast<const u32x2*>(slot + REC_SHARED + (TPW > 1 ? ut : vt & 1) * 512 + lane * 8);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
         op.kg[j] = *reinterpret_cast<const u32x4*>(slot + REC_KG + j * 1024 + lane * 16);
@@ -141,6 +150,31 @@ __shared__ __attribute__((aligned(1024))) uint8_t hc_buf[HANDOFF][HC_BYTES];
 __shared__ __attribute__((aligned(16))) uint8_t vn_buf[HANDOFF][VN_BYTES];
 
 __device__ __forceinline__ lds_u8* ring_lds() { return (lds_u8*)ring; }
+
+// Work-groups of TPW = 2 value tiles of one (sequence, head) (k2s_kernel
+// below): one state wave per tile, one output wave for both, one copy wave.
+// A ring slot holds the shared 13 KiB and the two u slices; the hand-off
+// per tile and chunk is v_new and qg @ hc^T (fp32, 1 KiB), which the state
+// wave forms itself, so the output wave reads neither hc nor qg.  (At four
+// tiles the same structure ran slower than kda_k2w.hip's: B=1 T=8192 H=96
+// forward 632 against 613 us.)
+constexpr int QH_BYTES = 1024;
+template <int TPW>
+struct SplitLds {
+    static constexpr int SLOT = REC_SHARED + TPW * 512;
+    static constexpr int NL = SHARED_LOADS + TPW / 2;  // 1 KiB loads per chunk
+    static_assert(TPW == 2, "two value tiles");
+    static_assert((LEAD - 1) * NL <= 63, "vmcnt is a 6-bit count");
+    static __device__ __forceinline__ uint8_t* ring();
+    static __device__ __forceinline__ uint8_t* vn(int h, int ut);
+    static __device__ __forceinline__ uint8_t* qh(int h, int ut);
+};
+__shared__ __attribute__((aligned(1024))) uint8_t ring_s2[RING * SplitLds<2>::SLOT];
+__shared__ __attribute__((aligned(16))) uint8_t vn_s2[HANDOFF][2][VN_BYTES];
+__shared__ __attribute__((aligned(16))) uint8_t qh_s2[HANDOFF][2][QH_BYTES];
+template <> __device__ __forceinline__ uint8_t* SplitLds<2>::ring() { return ring_s2; }
+template <> __device__ __forceinline__ uint8_t* SplitLds<2>::vn(int h, int ut) { return vn_s2[h][ut]; }
+template <> __device__ __forceinline__ uint8_t* SplitLds<2>::qh(int h, int ut) { return qh_s2[h][ut]; }
 
 // The state wave's barrier after a chunk that is followed by another: its
 // last LDS accesses (the v_new hand-off, the next chunk's kg) need not be
@@ -165,6 +199,7 @@ struct Ctx {
     int rev;                    // backward: step c handles chunk NT - 1 - c
     float scale;
     int NT, T, lane, q4, vt;    // NT chunks over T tokens (this sequence's)
+    int ut;                     // split work-groups: this state wave's tile among the TPW
 };
 
 // State wave, chunk c in ring slot S (a template argument, so every LDS
@@ -186,12 +221,23 @@ struct Ctx {
 // op[S & 1] holds chunk c's operands.  op[(S + 1) & 1] holds chunk c - 1's
 // until its kg has fed the update products, then receives chunk c + 1's.
 // vn carries v_new from one step to the next.
-template <int S, bool HAS_PREV, bool HAS_NEXT>
+//
+// TPW > 1 (a split work-group): the slots and hand-offs of SplitLds<TPW>,
+// and the state wave also forms qg @ hc^T, the first term of o, behind each
+// w product (the output wave's order of products, so the same bits), and
+// hands it off with v_new instead of hc.
+template <int S, bool HAS_PREV, bool HAS_NEXT, int TPW = 1>
 __device__ __forceinline__ void state_step(const Ctx& cx, f32x4 (&St)[8], StateOps (&op)[2],
                                            i16x4& vn) {
+    constexpr bool QH = TPW > 1;
     const StateOps& cur = op[S & 1];
     StateOps& oth = op[(S + 1) & 1];
-    const uint8_t* ns = ring + ((S + 1) % RING) * SLOT;
+    const uint8_t* ns;
+    if constexpr (QH) {
+        ns = SplitLds<TPW>::ring() + ((S + 1) % RING) * SplitLds<TPW>::SLOT;
+    } else {
+        ns = ring + ((S + 1) % RING) * SLOT;
+    }
     uint8_t* hbuf = hc_buf[S % HANDOFF] + cx.lane * 16;
     const int lane = cx.lane;
 
@@ -212,6 +258,12 @@ __device__ __forceinline__ void state_step(const Ctx& cx, f32x4 (&St)[8], StateO
     auto read_dc = [&]() {
         if (HAS_NEXT) oth.dc = *reinterpret_cast<const f32x2*>(ns + decay_offset(lane));
     };
+    auto read_qg = [&](int j) {
+        if (QH && HAS_NEXT)
+            oth.qg[j] = *reinterpret_cast<const u32x4*>(ns + REC_QG + j * 1024 + lane * 16);
+    };
+    const f32x4 zq = {0.f, 0.f, 0.f, 0.f};
+    f32x4 qacc = zq;
     auto pack_hc = [&](int j) {  // bf16(S^T) of k-tiles 2j, 2j+1: a 16x16x32 B operand
         return u32x4{pack2(St[2 * j][0], St[2 * j][1]), pack2(St[2 * j][2], St[2 * j][3]),
                      pack2(St[2 * j + 1][0], St[2 * j + 1][1]),
@@ -234,6 +286,8 @@ __device__ __forceinline__ void state_step(const Ctx& cx, f32x4 (&St)[8], StateO
     update(1);
     read_w(2);
     read_w(3);
+    read_qg(0);
+    read_qg(1);
     // u as the fp32 accumulator the chain starts from
     const f32x4 u = {__builtin_bit_cast(float, cur.u.x << 16),
                      __builtin_bit_cast(float, cur.u.x & 0xffff0000u),
@@ -247,9 +301,10 @@ __device__ __forceinline__ void state_step(const Ctx& cx, f32x4 (&St)[8], StateO
     decay(std::integral_constant<int, 0>{});
     KDA_FENCE();
     f32x4 va = mfma_bf16_16x16x32(as_bf16x8(cur.w[0]), as_bf16x8(hc0), u);
+    if (QH) qacc = mfma_bf16_16x16x32(as_bf16x8(cur.qg[0]), as_bf16x8(hc0), zq);
     const u32x4 hc1 = pack_hc(1);
     if (HAS_NEXT)
-        oth.u = *reinterpret_cast<const u32x2*>(ns + REC_SHARED + (cx.vt & 1) * 512 + lane * 8);
+        oth.u = *reinterpret_cast<const u32x2*>(ns + REC_SHARED + (QH ? cx.ut : cx.vt & 1) * 512 + lane * 8);
     read_dc();
     KDA_FENCE();
     update(4);
@@ -258,8 +313,14 @@ __device__ __forceinline__ void state_step(const Ctx& cx, f32x4 (&St)[8], StateO
     update(5);
     KDA_FENCE();
     va = mfma_bf16_16x16x32(as_bf16x8(cur.w[1]), as_bf16x8(hc1), va);
-    *reinterpret_cast<u32x4*>(hbuf + 0 * 1024) = hc0;
-    *reinterpret_cast<u32x4*>(hbuf + 1 * 1024) = hc1;
+    if (QH) {
+        qacc = mfma_bf16_16x16x32(as_bf16x8(cur.qg[1]), as_bf16x8(hc1), qacc);
+        read_qg(2);
+        read_qg(3);
+    } else {
+        *reinterpret_cast<u32x4*>(hbuf + 0 * 1024) = hc0;
+        *reinterpret_cast<u32x4*>(hbuf + 1 * 1024) = hc1;
+    }
     KDA_FENCE();
     update(6);
     const u32x4 hc2 = pack_hc(2);
@@ -268,12 +329,16 @@ __device__ __forceinline__ void state_step(const Ctx& cx, f32x4 (&St)[8], StateO
     decay(std::integral_constant<int, 2>{});
     KDA_FENCE();
     va = mfma_bf16_16x16x32(as_bf16x8(cur.w[2]), as_bf16x8(hc2), va);
+    if (QH) qacc = mfma_bf16_16x16x32(as_bf16x8(cur.qg[2]), as_bf16x8(hc2), qacc);
     const u32x4 hc3 = pack_hc(3);
     KDA_FENCE();
     va = mfma_bf16_16x16x32(as_bf16x8(cur.w[3]), as_bf16x8(hc3), va);
+    if (QH) qacc = mfma_bf16_16x16x32(as_bf16x8(cur.qg[3]), as_bf16x8(hc3), qacc);
     decay(std::integral_constant<int, 3>{});
-    *reinterpret_cast<u32x4*>(hbuf + 2 * 1024) = hc2;
-    *reinterpret_cast<u32x4*>(hbuf + 3 * 1024) = hc3;
+    if (!QH) {
+        *reinterpret_cast<u32x4*>(hbuf + 2 * 1024) = hc2;
+        *reinterpret_cast<u32x4*>(hbuf + 3 * 1024) = hc3;
+    }
     read_kg(0);
     read_kg(1);
     read_kg(2);
@@ -281,7 +346,13 @@ __device__ __forceinline__ void state_step(const Ctx& cx, f32x4 (&St)[8], StateO
     KDA_FENCE();
 
     const u32x2 vnb = {pack2(va[0], va[1]), pack2(va[2], va[3])};
-    *reinterpret_cast<u32x2*>(vn_buf[S % HANDOFF] + lane * 8) = vnb;
+    if constexpr (QH) {
+        // (with the reads above, 16 LDS accesses a step: the barrier rule holds)
+        *reinterpret_cast<u32x2*>(SplitLds<TPW>::vn(S % HANDOFF, cx.ut) + lane * 8) = vnb;
+        *reinterpret_cast<f32x4*>(SplitLds<TPW>::qh(S % HANDOFF, cx.ut) + lane * 16) = qacc;
+    } else {
+        *reinterpret_cast<u32x2*>(vn_buf[S % HANDOFF] + lane * 8) = vnb;
+    }
     vn = as_i16x4(vnb);
     if (HAS_NEXT) {
         chunk_barrier_nodrain();
@@ -386,24 +457,24 @@ __device__ __forceinline__ void copy_step(const Ctx& cx, int c) {
 // with its slot as a compile-time constant.
 // N chunks from slot S on, each followed by another (so with a next
 // chunk to prefetch) and preceded by one.
-template <int S, int N>
+template <int S, int N, int TPW = 1>
 __device__ __forceinline__ void state_round_full(const Ctx& cx, f32x4 (&St)[8],
                                                  StateOps (&op)[2], i16x4& vn) {
-    state_step<S, true, true>(cx, St, op, vn);
-    if constexpr (N > 1) state_round_full<(S + 1) % RING, N - 1>(cx, St, op, vn);
+    state_step<S, true, true, TPW>(cx, St, op, vn);
+    if constexpr (N > 1) state_round_full<(S + 1) % RING, N - 1, TPW>(cx, St, op, vn);
 }
 
 // The remaining chunks c .. NT - 1 (at most N of them) from slot S on.
-template <int S, int N>
+template <int S, int N, int TPW = 1>
 __device__ __forceinline__ void state_round_tail(const Ctx& cx, int c, f32x4 (&St)[8],
                                                  StateOps (&op)[2], i16x4& vn) {
     if (c >= cx.NT) return;
     if (c + 1 < cx.NT) {
-        state_step<S, true, true>(cx, St, op, vn);
+        state_step<S, true, true, TPW>(cx, St, op, vn);
     } else {
-        state_step<S, true, false>(cx, St, op, vn);
+        state_step<S, true, false, TPW>(cx, St, op, vn);
     }
-    if constexpr (N > 1) state_round_tail<(S + 1) % RING, N - 1>(cx, c + 1, St, op, vn);
+    if constexpr (N > 1) state_round_tail<(S + 1) % RING, N - 1, TPW>(cx, c + 1, St, op, vn);
 }
 
 template <int S, bool TRAIN, int PART, bool WITH_O>
@@ -620,6 +691,7 @@ __device__ __forceinline__ void bwd_state_wave(const Params& p, const Ctx& cx, i
     store_state_to(p.dh0 ? p.dh0 + sbase : nullptr, p.h0_v_first != 0, v, q4, D);
 }
 
+template <int TPW = 1>
 __device__ __forceinline__ void state_wave(const Params& p, const Ctx& cx, int bh) {
     const int lane = cx.lane, q4 = cx.q4, vt = cx.vt;
     const int v = 16 * vt + (lane & 15);
@@ -628,18 +700,24 @@ __device__ __forceinline__ void state_wave(const Params& p, const Ctx& cx, int b
     load_state(p, sbase, v, q4, St);
     chunk_barrier();  // chunks 0 and 1 are in the ring
     StateOps op[2];
-    read_state_ops_a(ring, lane, vt, op[0]);
-    read_state_ops_b(ring, lane, op[0]);
+    const uint8_t* slot0;
+    if constexpr (TPW > 1) {
+        slot0 = SplitLds<TPW>::ring();
+    } else {
+        slot0 = ring;
+    }
+    read_state_ops_a<TPW>(slot0, lane, vt, op[0], cx.ut);
+    read_state_ops_b(slot0, lane, op[0]);
     __builtin_amdgcn_s_waitcnt(WAITCNT_LGKM0);
     i16x4 vn;
     if (cx.NT > 1) {
-        state_step<0, false, true>(cx, St, op, vn);
+        state_step<0, false, true, TPW>(cx, St, op, vn);
     } else {
-        state_step<0, false, false>(cx, St, op, vn);
+        state_step<0, false, false, TPW>(cx, St, op, vn);
     }
     int c = 1;
-    for (; c + RING < cx.NT; c += RING) state_round_full<1, RING>(cx, St, op, vn);
-    state_round_tail<1 % RING, RING>(cx, c, St, op, vn);
+    for (; c + RING < cx.NT; c += RING) state_round_full<1, RING, TPW>(cx, St, op, vn);
+    state_round_tail<1 % RING, RING, TPW>(cx, c, St, op, vn);
     chunk_barrier();  // the output wave's last chunk
     store_state(p, sbase, v, q4, St);
 }
@@ -867,6 +945,107 @@ __device__ __forceinline__ void copy_wave_ms(const Params& p, Ctx& cx, const MsC
     copy_barrier();  // the output wave's last chunk
 }
 
+// ---------------------------------------------------------------------------
+// Split work-groups (k2s_kernel): TPW = 2 value tiles of one (sequence,
+// head), one state wave per tile (state_step with its qg @ hc^T), one output
+// wave for both tiles, one copy wave streaming each record once (the shared
+// 13 KiB and the two u slices).  Where one-tile work-groups would outnumber
+// the CUs by up to twice, this shares the record stream between the tiles
+// as kda_k2w.hip does, while each tile's recurrence keeps a wave of its own
+// with little but the chain on it.  Same ring, lead, hand-off depth and
+// barrier per chunk as the one-tile kernel; o bit for bit that kernel's.
+// ---------------------------------------------------------------------------
+
+// Copy wave: one chunk's 13 shared KiB, then the TPW u slices (TPW / 2
+// loads of 1 KiB), at their places in the slot.
+template <int TPW>
+__device__ __forceinline__ void issue_chunk_split(__amdgpu_buffer_rsrc_t rs, uint32_t chunk_off,
+                                                  lds_u8* slot, uint32_t u_off, uint32_t voff16) {
+#pragma unroll
+    for (int i = 0; i < SHARED_LOADS; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_u8*)(slot + i * 1024), 16, voff16,
+                                                 chunk_off + i * 1024, 0, 0);
+#pragma unroll
+    for (int i = 0; i < TPW / 2; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_u8*)(slot + REC_SHARED + i * 1024), 16,
+                                                 voff16, chunk_off + u_off + i * 1024, 0, 0);
+}
+
+template <int S, int TPW>
+__device__ __forceinline__ void copy_round_split(const Ctx& cx, int c) {
+    using L = SplitLds<TPW>;
+    if (c + LEAD < cx.NT)
+        issue_chunk_split<TPW>(cx.rs, (uint32_t)(c + LEAD) * REC_BYTES,
+                               (lds_u8*)L::ring() + ((S + LEAD) % RING) * L::SLOT, cx.u_off, cx.voff16);
+    // chunk c + 2 is read by the state waves after this barrier
+    if (c + 2 < cx.NT) wait_chunk<L::NL>(min(LEAD - 2, cx.NT - 3 - c));
+    copy_barrier();
+    if constexpr (S + 1 < RING) {
+        if (c + 1 < cx.NT) copy_round_split<S + 1, TPW>(cx, c + 1);
+    }
+}
+
+template <int TPW>
+__device__ __forceinline__ void copy_wave_split(const Params& p, Ctx& cx, const SeqSpan& sp, int slice) {
+    using L = SplitLds<TPW>;
+    const int NT = cx.NT;
+    cx.rs = __builtin_amdgcn_make_buffer_rsrc(p.ws + sp.rec0 * REC_BYTES, (short)0, NT * REC_BYTES,
+                                              BUF_DWORD3);
+    cx.voff16 = cx.lane * 16;
+    cx.u_off = REC_U + 512 * TPW * slice;
+#pragma unroll
+    for (int d = 0; d < LEAD; ++d)
+        if (d < NT)
+            issue_chunk_split<TPW>(cx.rs, (uint32_t)d * REC_BYTES, (lds_u8*)L::ring() + d * L::SLOT,
+                                   cx.u_off, cx.voff16);
+    // chunks 0 and 1 (those that exist) before the first barrier
+    wait_chunk<L::NL>(NT >= 2 ? min(LEAD, NT) - 2 : 0);
+    copy_barrier();
+    for (int c = 0; c < NT; c += RING) copy_round_split<0, TPW>(cx, c);
+    copy_barrier();  // the output wave's last chunk
+}
+
+// Output wave, chunk c (slot S) after the barrier that ends chunk c + 1:
+// for each tile, o = scale * (qg @ hc^T) + Aqk @ v_new (kernels.py:268-279)
+// from the state wave's hand-off, as output_step forms it.
+template <int S, int TPW>
+__device__ __forceinline__ void output_step_split(const Ctx& cx, int c) {
+    using L = SplitLds<TPW>;
+    chunk_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    const uint8_t* slot = L::ring() + S * L::SLOT;
+    // Aqk 16 bytes at a time (this lane's 8 and its neighbour's), as in output_step
+    const u32x4 aq2 = *reinterpret_cast<const u32x4*>(slot + REC_AQK + (cx.lane >> 1) * 16);
+    const u32x2 aqk = (cx.lane & 1) ? u32x2{aq2.z, aq2.w} : u32x2{aq2.x, aq2.y};
+    const int t = c * BT + 4 * cx.q4 + (cx.lane & 3);
+    // every tile's hand-off read before the first store (no LDS read waits
+    // behind a store)
+    f32x4 qh[TPW];
+    u32x2 vn[TPW];
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+        qh[i] = *reinterpret_cast<const f32x4*>(L::qh(S % HANDOFF, i) + cx.lane * 16);
+        vn[i] = *reinterpret_cast<const u32x2*>(L::vn(S % HANDOFF, i) + cx.lane * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+        f32x4 oacc = qh[i] * cx.scale;
+        oacc = mfma_bf16_16x16x16(as_i16x4(aqk), as_i16x4(vn[i]), oacc);
+        const u32x2 ot = quad_transpose(pack2(oacc[0], oacc[1]), pack2(oacc[2], oacc[3]), cx.lane & 3);
+        if (t < cx.T)
+            __builtin_nontemporal_store(
+                ot, reinterpret_cast<u32x2*>(cx.obase + (int64_t)t * cx.orow_stride + 16 * i));
+    }
+}
+
+template <int S, int TPW>
+__device__ __forceinline__ void output_round_split(const Ctx& cx, int c) {
+    output_step_split<S, TPW>(cx, c);
+    if constexpr (S + 1 < RING) {
+        if (c + 1 < cx.NT) output_round_split<S + 1, TPW>(cx, c + 1);
+    }
+}
+
 enum Role { STATE = 0, OUTPUT = 1, COPY = 2, OUTPUT2 = 3 };
 
 // Every wave executes exactly NT + 2 barriers: one after the prologue, one
@@ -942,6 +1121,7 @@ __global__ __launch_bounds__(MODE == K2_FWD || MODE == K2_FWD_MS ? 192 : 256) vo
     cx.q4 = lane >> 4;
     cx.vt = lin & 7;
     cx.rev = MODE == K2_BWD;
+    cx.ut = 0;
 
     if (sp.nt == 0) {
         // An empty sequence: its final state is its initial state.  Every
@@ -984,6 +1164,65 @@ __global__ __launch_bounds__(MODE == K2_FWD || MODE == K2_FWD_MS ? 192 : 256) vo
     __builtin_amdgcn_endpgm();
 }
 
+// Work-group (sequence, value head, slice of TPW value tiles), XCD aware as
+// in kda_k2w.hip: the grid is padded to a multiple of 8 * (8 / TPW), and
+// the 8 / TPW slices of a head get consecutive ids of one residue class
+// mod 8, so they share an XCD and its L2 for the records.  Waves 0 .. TPW-1
+// are the state waves, TPW the output wave, TPW + 1 the copy wave.
+template <int TPW>
+__global__ __launch_bounds__(64 * (TPW + 2)) void k2s_kernel(Params p) {
+    constexpr int NSL = 8 / TPW;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nbh = (p.cu_seqlens ? p.N : p.B) * p.HV;
+    const int total = nbh * NSL;
+    const int padded = (total + 8 * NSL - 1) / (8 * NSL) * (8 * NSL);
+    const int wg = blockIdx.x;
+    const int lin = (wg & 7) * (padded >> 3) + (wg >> 3);
+    if (lin >= total) return;  // padding: the whole work-group leaves before any barrier
+    const int bh = lin / NSL;
+    const int slice = lin - bh * NSL;
+    const int hv = bh - (bh / p.HV) * p.HV;
+    const SeqSpan sp = seq_span(p, bh);
+
+    Ctx cx;
+    cx.scale = p.scale;
+    cx.NT = sp.nt;
+    cx.T = sp.len;
+    cx.lane = lane;
+    cx.q4 = lane >> 4;
+    cx.rev = 0;
+    cx.ut = wave < TPW ? wave : 0;
+    cx.vt = slice * TPW + cx.ut;
+
+    if (sp.nt == 0) {
+        // An empty sequence: its final state is its initial state, and no
+        // wave reaches a barrier.
+        if (wave < TPW) {
+            f32x4 St[8];
+            const int v = 16 * cx.vt + (lane & 15);
+            const int64_t sb = (int64_t)bh * DK * DK;
+            load_state(p, sb, v, cx.q4, St);
+            store_state(p, sb, v, cx.q4, St);
+        }
+        __builtin_amdgcn_endpgm();
+    }
+    if (wave < TPW) {
+        state_wave<TPW>(p, cx, bh);
+        __builtin_amdgcn_endpgm();
+    }
+    if (wave == TPW) {
+        cx.obase = p.o + (sp.tok0 * p.HV + hv) * DK + 16 * TPW * slice + 4 * ((lane & 15) >> 2);
+        cx.orow_stride = (int64_t)p.HV * DK;
+        chunk_barrier();
+        chunk_barrier();
+        for (int c = 0; c < cx.NT; c += RING) output_round_split<0, TPW>(cx, c);
+        __builtin_amdgcn_endpgm();
+    }
+    copy_wave_split<TPW>(p, cx, sp, slice);
+    __builtin_amdgcn_endpgm();
+}
+
 }  // namespace
 
 // CUs of the current device (cached per device).
@@ -1005,8 +1244,19 @@ hipError_t launch_k2(const Params& p, hipStream_t stream) {
     const int64_t tiles = (int64_t)p.HV * 8;
     const int ncu = cu_count();
     // More (sequence, head, value tile) triples than CUs: several tiles per
-    // work-group share one record stream (kda_k2w.hip).
-    if (const int tpw = k2_wide_tiles(p, ncu)) return launch_k2_wide(p, tpw, stream);
+    // work-group share one record stream.  Two tiles: a state wave per tile
+    // (k2s_kernel, above; B=1 T=4096 H=40 forward 148 against 166 us with
+    // kda_k2w.hip's compute waves, H=64 205 against 213 us).  Four or eight,
+    // or a caller's k2_wave_tiles: kda_k2w.hip.
+    if (const int tpw = k2_wide_tiles(p, ncu)) {
+        if (tpw == 2 && p.k2_wave_tiles == 0) {
+            const int64_t nbh = (int64_t)(p.cu_seqlens ? p.N : p.B) * p.HV;
+            const int64_t padded = (nbh * 4 + 31) / 32 * 32;  // 4 slices a head, 8 XCDs
+            hipLaunchKernelGGL(k2s_kernel<2>, dim3((unsigned)padded), dim3(64 * 4), 0, stream, p);
+            return hipGetLastError();
+        }
+        return launch_k2_wide(p, tpw, stream);
+    }
     if (nseq > 1 && nseq * tiles > ncu) {
         // several sequences per work-group, in as many groups as fill the
         // CUs once (at least one)

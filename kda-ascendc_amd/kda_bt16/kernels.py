@@ -81,7 +81,9 @@ def forward_choice(*, fused: bool | None = None, k2_tiles: int = 0, k2_wave_tile
       None (default) leaves it to the library; an explicit
       ``use_fused_kernel=True`` still wins;
     * ``k2_tiles``: stage-2 value tiles per work-group (1, 2, 4 or 8);
-    * ``k2_wave_tiles``: with 2-8 tiles, value tiles per compute wave (1, 2);
+    * ``k2_wave_tiles``: with 2-8 tiles, 1 or 2 forces compute waves that
+      each run that many whole tiles (0: the library's kernel, a state
+      wave per tile at 2 tiles);
 
     0 leaves the choice to the library.  They reach the C ABI as the
     ``KDA_BT16_FUSED_KERNEL`` / ``KDA_BT16_TWO_STAGE`` flags and the

@@ -1,13 +1,16 @@
-"""Stage 2 with several value tiles per work-group (csrc/kda_k2w.hip)
-against stage 2 with one tile per work-group (csrc/kda_k2.hip), bit for
-bit: the two run the same arithmetic in the same order (kernels.py:225-302),
-only the division of the work differs.
+"""Stage 2 with several value tiles per work-group against stage 2 with one
+tile per work-group (k2_kernel, csrc/kda_k2.hip), bit for bit: they run the
+same arithmetic in the same order (kernels.py:225-302), only the division of
+the work differs.
 
 ``forward_choice(k2_tiles=...)`` (the ``k2_tiles`` field of the C ABI's
-arguments) forces the tiles per work-group (1: kda_k2.hip; 2, 4, 8:
-kda_k2w.hip) over the launch heuristic, which picks several tiles only when
-(sequences x heads x 8) exceeds the CU count, and ``k2_wave_tiles`` the
-tiles per compute wave of kda_k2w.hip (1 or 2).
+arguments) forces the tiles per work-group (1, 2, 4, 8) over the launch
+heuristic, which picks several tiles only when (sequences x heads x 8)
+exceeds the CU count.  ``k2_wave_tiles`` picks the kernel for several tiles:
+0, the library's choice (a state wave per tile, k2s_kernel in
+csrc/kda_k2.hip, at 2 tiles; csrc/kda_k2w.hip's compute waves of one tile
+at 4 and of two at 8), or 1 / 2 for kda_k2w.hip's compute waves of that
+many tiles.
 """
 
 from __future__ import annotations
@@ -71,7 +74,7 @@ def test_wide_stage2_equals_one_tile_stage2(case, gpu_device):
     o1, ht1 = _run(c, gpu_device, cu, svf, h0, 1)
     assert torch.isfinite(o1.float()).all() and torch.isfinite(ht1).all()
     for tiles in (2, 4, 8):
-        for wt in (1, 2):
+        for wt in (0, 1, 2):
             o, ht = _run(c, gpu_device, cu, svf, h0, tiles, wt)
             what = f"{name}: {tiles} tiles, {wt} per wave"
             assert torch.equal(o.view(torch.int16), o1.view(torch.int16)), f"{what}: o"
