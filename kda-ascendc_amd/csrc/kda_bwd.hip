@@ -705,43 +705,77 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(GROUP ? 1 : 
 }
 
 // dA_log[hv] and ddt_bias[hv, :] summed over the chunk partials of value
-// head hv in a fixed order: thread group j (of RG) sums records j, j + RG,
-// ..., then the groups' sums are added in group order.
+// head hv (PART_STRIDE floats per record: DK bias sums, then the A_log
+// sum), in a fixed order, in two launches:
+//   1. the head's records (its batch rows' runs, or its varlen slots, in
+//      order) fall into segments of GR_SEG consecutive records, one
+//      work-group each: thread group j (of RG) sums records j, j + RG, ...
+//      of the segment, then the groups' sums are added in group order, and
+//      the segment's sum replaces its first record's partials (read by then);
+//   2. one work-group per head adds its segments' sums in segment order.
+// The order depends on the geometry only, so the sums are bit for bit
+// repeatable.
 constexpr int RG = 8;
+constexpr int GR_SEG = 32;
 
-__global__ __launch_bounds__(RG * DK) void gate_reduce_kernel(Params p) {
-    __shared__ float s_acc[RG][DK + 1];
-    const int hv = blockIdx.x, t = threadIdx.x & (DK - 1), grp = threadIdx.x / DK;
-    // records of value head hv: nb runs of nr consecutive records
-    const int nb = p.cu_seqlens ? 1 : p.B;
-    const int nr = p.cu_seqlens ? p.NS : p.NT;
-    float acc = 0.f, accA = 0.f;
-    for (int b = 0; b < nb; ++b) {
+// Records of value head hv: nb runs of nr, run b starting at first(b).
+struct GateRuns {
+    int nb, nr;
+    __device__ __forceinline__ GateRuns(const Params& p)
+        : nb(p.cu_seqlens ? 1 : p.B), nr(p.cu_seqlens ? p.NS : p.NT) {}
+    __device__ __forceinline__ float* rec(const Params& p, int hv, int i) const {
+        const int b = i / nr, x = i - b * nr;
         const int64_t first = p.cu_seqlens ? (int64_t)hv * p.NS : (int64_t)(b * p.HV + hv) * p.NT;
-        const float* base = p.tr_part + first * PART_STRIDE;
-        // sixteen records' loads in flight before the adds, which keep
-        // their order (the sums stay bit for bit those of a plain loop)
-#pragma unroll 16
-        for (int x = grp; x < nr; x += RG) {
-            acc += base[(int64_t)x * PART_STRIDE + t];
-            if (t == 0) accA += base[(int64_t)x * PART_STRIDE + DK];
-        }
+        return p.tr_part + (first + x) * PART_STRIDE;
+    }
+};
+
+__global__ __launch_bounds__(RG * DK) void gate_segment_kernel(Params p) {
+    __shared__ float s_acc[RG][DK + 1];
+    const GateRuns runs(p);
+    const int nrec = runs.nb * runs.nr;
+    const int nseg = (nrec + GR_SEG - 1) / GR_SEG;
+    const int hv = blockIdx.x / nseg, seg = blockIdx.x - hv * nseg;
+    const int t = threadIdx.x & (DK - 1), grp = threadIdx.x / DK;
+    const int i0 = seg * GR_SEG, i1 = min(i0 + GR_SEG, nrec);
+    float acc = 0.f, accA = 0.f;
+    // the segment's loads in flight before the adds, which keep their order
+#pragma unroll 4
+    for (int i = i0 + grp; i < i1; i += RG) {
+        const float* r = runs.rec(p, hv, i);
+        acc += r[t];
+        if (t == 0) accA += r[DK];
     }
     s_acc[grp][t] = acc;
     if (t == 0) s_acc[grp][DK] = accA;
-    __syncthreads();
+    __syncthreads();  // every read of the segment's records is done
     if (grp == 0) {
         float a = 0.f;
 #pragma unroll
         for (int j = 0; j < RG; ++j) a += s_acc[j][t];
-        if (p.ddt_bias) p.ddt_bias[hv * DK + t] = a;
-        if (t == 0 && p.dA_log) {
+        float* out = runs.rec(p, hv, i0);
+        out[t] = a;
+        if (t == 0) {
             float aa = 0.f;
 #pragma unroll
             for (int j = 0; j < RG; ++j) aa += s_acc[j][DK];
-            p.dA_log[hv] = aa;
+            out[DK] = aa;
         }
     }
+}
+
+__global__ __launch_bounds__(DK) void gate_reduce_kernel(Params p) {
+    const GateRuns runs(p);
+    const int nrec = runs.nb * runs.nr;
+    const int hv = blockIdx.x, t = threadIdx.x;
+    float a = 0.f, aa = 0.f;
+    for (int i0 = 0; i0 < nrec; i0 += GR_SEG) {
+        const float* r = runs.rec(p, hv, i0);
+        a += r[t];
+        if (t == 0) aa += r[DK];
+    }
+    if (p.ddt_bias) p.ddt_bias[hv * DK + t] = a;
+    if (t == 0 && p.dA_log) p.dA_log[hv] = aa;
 }
 
 }  // namespace
@@ -756,7 +790,14 @@ hipError_t launch_bwd_chunk(const Params& p, hipStream_t stream) {
 }
 
 hipError_t launch_bwd_gate_reduce(const Params& p, hipStream_t stream) {
-    hipLaunchKernelGGL(gate_reduce_kernel, dim3((unsigned)p.HV), dim3(RG * DK), 0, stream, p);
+    const int64_t nrec = p.cu_seqlens ? (int64_t)p.NS : (int64_t)p.B * p.NT;
+    const int64_t nseg = (nrec + GR_SEG - 1) / GR_SEG;
+    if (nseg > 0) {
+        hipLaunchKernelGGL(gate_segment_kernel, dim3((unsigned)(p.HV * nseg)), dim3(RG * DK), 0, stream, p);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(gate_reduce_kernel, dim3((unsigned)p.HV), dim3(DK), 0, stream, p);
     return hipGetLastError();
 }
 

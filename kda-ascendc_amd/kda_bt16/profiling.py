@@ -96,7 +96,7 @@ _K2_MODES = {"0": "k2", "3": "k2", "1": "k2_bwd_recompute", "2": "k2_bwd_chain",
              "4": "k2_train_fwd"}
 # The backward's kernels when it starts from the saved state (bench.py
 # --workload train reads their traffic).
-BACKWARD_ROLES = ["k1_dout", "k2_bwd_chain", "bwd_chunk", "gate_reduce"]
+BACKWARD_ROLES = ["k1_dout", "k2_bwd_chain", "bwd_chunk", "gate_segment", "gate_reduce"]
 
 
 def kernel_role(name: str) -> str | None:
@@ -112,8 +112,9 @@ def kernel_role(name: str) -> str | None:
     if m:
         return _K2_MODES.get(m.group(1), "k2_mode" + m.group(1))
     for key, role in (("fused_kernel", "fused"), ("k1_dout_kernel", "k1_dout"),
-                      ("k2w_kernel", "k2"), ("recurrent_kernel", "recurrent"),
-                      ("bwd_chunk_kernel", "bwd_chunk"), ("gate_reduce_kernel", "gate_reduce"),
+                      ("k2w_kernel", "k2"), ("k2s_kernel", "k2"), ("recurrent_kernel", "recurrent"),
+                      ("bwd_chunk_kernel", "bwd_chunk"), ("gate_segment_kernel", "gate_segment"),
+                      ("gate_reduce_kernel", "gate_reduce"),
                       ("copyBuffer", "copy")):
         if key in name:
             return role

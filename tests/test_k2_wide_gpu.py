@@ -94,3 +94,13 @@ def test_heuristic_takes_the_wide_kernel_for_many_heads(gpu_device):
         dt_bias=c["dt_bias"].to(gpu_device))
     torch.cuda.synchronize()
     assert torch.equal(o, o1) and torch.equal(ht, ht1)
+
+
+def test_heuristic_takes_two_tiles_for_forty_heads(gpu_device):
+    """B=1 T=200 H=40 (320 value tiles, 2 per work-group by default: the
+    state-wave-per-tile kernel) gives the one-tile result, partial last
+    chunk included."""
+    c = _inputs(1, 200, 40, 40, 1, seed=11)
+    o1, ht1 = _run(c, gpu_device, None, True, True, 1)
+    o, ht = _run(c, gpu_device, None, True, True, 0)
+    assert torch.equal(o, o1) and torch.equal(ht, ht1)

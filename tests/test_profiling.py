@@ -88,6 +88,9 @@ def test_kernel_roles():
     assert r(K1) == "k1" and r(K2) == "k2"
     assert r("void kda::(anonymous namespace)::k2_kernel<3>(kda::Params)") == "k2"
     assert r("void kda::(anonymous namespace)::k2w_kernel<4, 1>(kda::Params)") == "k2"
+    assert r("void kda::(anonymous namespace)::k2s_kernel<2>(kda::Params)") == "k2"
+    assert r("void kda::(anonymous namespace)::gate_segment_kernel(kda::Params)") == "gate_segment"
+    assert r("void kda::(anonymous namespace)::gate_reduce_kernel(kda::Params)") == "gate_reduce"
     assert r("void kda::(anonymous namespace)::k1_kernel<2, false, true>(kda::Params)") == "k1_train_fwd"
     assert r("void kda::(anonymous namespace)::k2_kernel<2>(kda::Params)") == "k2_bwd_chain"
     assert r("void kda::(anonymous namespace)::k2_kernel<4>(kda::Params)") == "k2_train_fwd"
