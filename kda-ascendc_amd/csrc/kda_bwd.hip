@@ -769,6 +769,8 @@ __global__ __launch_bounds__(DK) void gate_reduce_kernel(Params p) {
     const int nrec = runs.nb * runs.nr;
     const int hv = blockIdx.x, t = threadIdx.x;
     float a = 0.f, aa = 0.f;
+    // sixteen segments' loads in flight before their adds (in order)
+#pragma unroll 16
     for (int i0 = 0; i0 < nrec; i0 += GR_SEG) {
         const float* r = runs.rec(p, hv, i0);
         a += r[t];
