@@ -251,23 +251,26 @@ def varlen_offsets(seed: int = 7) -> list[int]:
 
 KERNEL_LABELS = {
     "k1": "stage 1 (k1_kernel)",
-    "k2": "stage 2 (k2_kernel, or k2w_kernel where one-tile work-groups would outnumber the CUs)",
+    "k2": "stage 2 (k2_kernel, or k2s_kernel / k2w_kernel where one-tile work-groups would "
+          "outnumber the CUs)",
     "fused": "fused_kernel (stage 1's records kept in LDS), the forward's one launch",
 }
 
 
-def _dominant_roofline(kern, traffic, alg_bytes, flops, fwd_ms, fused) -> dict:
+def _dominant_roofline(kern, traffic, alg_bytes, flops, fwd_ms, fused, launches: int = 1) -> dict:
     """The roofline of the forward's dominant (longest) kernel: the
-    forward's algorithmic bytes over that kernel's mean launch time, HIP
+    algorithmic bytes of one of its launches over its mean launch time, HIP
     events on the stream it runs on (stage launches timed on their own just
     before the timed region; a fused forward is its one launch), and its
     HBM bytes per launch from rocprof's FETCH_SIZE / WRITE_SIZE scaled by the
-    copy calibration.  The same figures for the whole forward (all its
-    launches over the timed region's mean forward time) are under
-    ``forward``."""
+    copy calibration.  A forward whose two stages run in `launches` chunk
+    ranges launches each stage that many times, each launch over 1/launches
+    of the chunks and of the algorithmic bytes; `kern` then holds one
+    launch's time.  The same figures for the whole forward (all its launches
+    over the timed region's mean forward time) are under ``forward``."""
     dom = max(kern, key=lambda n: kern[n]["ms"])
     dom_ms = kern[dom]["ms"]
-    achieved = alg_bytes / dom_ms / 1e6
+    achieved = alg_bytes / launches / dom_ms / 1e6
     fwd_achieved = alg_bytes / fwd_ms / 1e6
     have = traffic is not None and all(n in traffic for n in kern)
     return {
@@ -279,16 +282,19 @@ def _dominant_roofline(kern, traffic, alg_bytes, flops, fwd_ms, fused) -> dict:
         "frac": round(achieved / HBM_PEAK_GBS, 5),
         "traffic": traffic.get(dom) if traffic else None,
         "kernel_ms_events": round(dom_ms, 5),
+        "launches_per_forward": launches,
         "alg_bytes": alg_bytes,
-        "rule": "achieved = the forward's algorithmic bytes / the dominant kernel's mean launch "
-                "time (HIP events); traffic = that kernel's HBM bytes per launch (rocprof)",
+        "rule": "achieved = the forward's algorithmic bytes / launches per forward / the dominant "
+                "kernel's mean launch time (HIP events); traffic = that kernel's HBM bytes per "
+                "launch (rocprof)",
         "forward": {
             "kernels": (KERNEL_LABELS["fused"] if fused else
-                        "stage 1 then stage 2, one launch each"),
+                        "stage 1 then stage 2, one launch each" if launches == 1 else
+                        f"stage 1 then stage 2 on each of {launches} chunk ranges"),
             "ms_events": round(fwd_ms, 5),
             "achieved": round(fwd_achieved, 2),
             "frac": round(fwd_achieved / HBM_PEAK_GBS, 5),
-            "traffic": sum(traffic[n] for n in kern) if have else None,
+            "traffic": launches * sum(traffic[n] for n in kern) if have else None,
             "matmul_flops": flops,
             "alg_tflops": round(flops / fwd_ms / 1e9, 2),
             "alg_mfma_frac": round(flops / fwd_ms / 1e9 / BF16_PEAK_TFLOPS, 5),
@@ -688,6 +694,18 @@ def run_forward(args, dev, name: str, *, cpu: bool, inputs_cpu=None) -> dict:
     k1, k2, _, _ = kda_bt16_stage_launchers(q, k, v, g, beta, initial_state=h0,
                                             output_final_state=True, A_log=A_log,
                                             dt_bias=dt_bias, lower_bound=LOWER_BOUND)
+    fused = k1.forward_plan == "fused"
+    # A forward whose two stages run in chunk ranges launches each stage once
+    # per range: time the first range's launches (the ranges are equal when
+    # the chunks divide evenly), as the forward runs them.
+    launches = max(1, k1.forward_segments)
+    if launches > 1:
+        rows = 16 * (((t + 15) // 16) // launches)  # the first range's tokens (16 a chunk)
+        part = lambda x: x[:, :rows].contiguous()
+        k1, k2, _, _ = kda_bt16_stage_launchers(part(q), part(k), part(v), part(g), part(beta),
+                                                initial_state=h0, output_final_state=True,
+                                                A_log=A_log, dt_bias=dt_bias,
+                                                lower_bound=LOWER_BOUND)
     k1(); k2()
     # Each stage over at least 100 launches: a steadier figure than a few,
     # and ~30 ms of this work has run by the time the forward's own warmup
@@ -716,12 +734,12 @@ def run_forward(args, dev, name: str, *, cpu: bool, inputs_cpu=None) -> dict:
 
     by1, by2 = algorithmic_bytes(b, b, t, h, h0 is not None)
     fl1, fl2 = matmul_flops(None, b, t, h)
-    fused = k1.forward_plan == "fused"
+    # per launch (1/launches of the forward's chunks)
     stage_kern = {
-        "k1": {"ms": k1_ms, "alg_bytes": by1, "alg_gbs": by1 / k1_ms / 1e6,
-               "alg_tflops": fl1 / k1_ms / 1e9},
-        "k2": {"ms": k2_ms, "alg_bytes": by2, "alg_gbs": by2 / k2_ms / 1e6,
-               "alg_tflops": fl2 / k2_ms / 1e9},
+        "k1": {"ms": k1_ms, "alg_bytes": by1 / launches, "alg_gbs": by1 / launches / k1_ms / 1e6,
+               "alg_tflops": fl1 / launches / k1_ms / 1e9},
+        "k2": {"ms": k2_ms, "alg_bytes": by2 / launches, "alg_gbs": by2 / launches / k2_ms / 1e6,
+               "alg_tflops": fl2 / launches / k2_ms / 1e9},
     }
     # The forward's kernels: one fused launch, or the two stages.
     kern = ({"fused": {"ms": fwd_ms, "alg_bytes": by1 + by2, "alg_gbs": (by1 + by2) / fwd_ms / 1e6,
@@ -737,7 +755,8 @@ def run_forward(args, dev, name: str, *, cpu: bool, inputs_cpu=None) -> dict:
         for n, m in mfma.items():
             kern[n]["mfma"] = m
     tot_bytes = by1 + by2
-    roofline = _dominant_roofline(kern, traffic, tot_bytes, fl1 + fl2, fwd_ms, fused)
+    roofline = _dominant_roofline(kern, traffic, tot_bytes, fl1 + fl2, fwd_ms, fused,
+                                  1 if fused else launches)
     roofline["alg_bytes_rule"] = "B*T*H*1282 + 65536*B*H*(h0 passed + ht) + 516*H"
     if fused:
         # the two stages on the same inputs, each timed on its own (the

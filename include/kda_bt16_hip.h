@@ -189,6 +189,18 @@ int kda_bt16_fwd_hip(const KdaBt16Args* args, void* stream);
  * whose _run always launches its two stages (kernels.py:581-602). */
 int kda_bt16_fwd_plan(const KdaBt16Args* args);
 
+/* In how many segments of consecutive chunks kda_bt16_fwd_hip runs its two
+ * stages for these arguments on the current device: 0 when it runs fused,
+ * else 1 to 4, or a negative KDA_BT16_E* code for invalid arguments.  A
+ * fixed-length forward whose records would outgrow the GPU's last-level
+ * cache runs stage 1 then stage 2 on each range of chunks in turn, stage 2
+ * carrying the state across (results bit for bit those of one pass); every
+ * segment's records and the state between them fit the workspace of
+ * kda_bt16_workspace_bytes_args.  Reads no device memory.  No counterpart
+ * in the reference; for measurement (the stage-level entry points run one
+ * pass). */
+int kda_bt16_fwd_segments(const KdaBt16Args* args);
+
 /* Work-groups of the fused kernel that gave up a wait on the current
  * device since the library was loaded or the count last reset.  No
  * counterpart in the reference.  The fused kernel's waves meet through LDS

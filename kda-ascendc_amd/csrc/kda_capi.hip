@@ -64,6 +64,7 @@ int check_common(const KdaBt16Args* a, Params& p) {
     p.ht = a->ht;
     p.B = a->B;
     p.T = a->T;
+    p.tok_stride = a->T;
     p.H = a->H;
     p.HV = a->HV;
     p.NT = (int)chunks_of(a->T);
@@ -363,6 +364,13 @@ int kda_bt16_fwd_plan(const KdaBt16Args* args) {
     const int rc = to_params_core(args, p, true, true);
     if (rc != KDA_BT16_OK) return rc;
     return kda::fwd_plan(p);
+}
+
+int kda_bt16_fwd_segments(const KdaBt16Args* args) {
+    Params p;
+    const int rc = to_params_core(args, p, true, true);
+    if (rc != KDA_BT16_OK) return rc;
+    return kda::fwd_plan(p) == 1 ? 0 : kda::fwd_segments(p);
 }
 
 int kda_bt16_fused_aborts(uint32_t* count, int32_t reset) {

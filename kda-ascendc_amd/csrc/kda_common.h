@@ -127,6 +127,10 @@ struct Params {
     // q and k use H, HV a multiple of H (value head hv reads q/k head
     // hv / (HV / H), kernels.py:88).
     int B, T, H, HV, NT;
+    // Fixed length: tokens between the first tokens of consecutive batch
+    // rows, T for whole rows; a segment of the two-stage forward (launch_two_stage)
+    // views tokens [t0, t0 + T) of each row with the row stride kept.
+    int64_t tok_stride;
     float scale, lower_bound;
     int g_bf16, beta_bf16;
     int use_gate, use_l2norm, use_beta_sigmoid;
@@ -210,7 +214,7 @@ __device__ __forceinline__ SeqSpan seq_span(const Params& p, int bh) {
         s.nt = (s.len + BT - 1) / BT;
         s.rec0 = (int64_t)hv * p.NS + bos / BT + n;
     } else {
-        s.tok0 = (int64_t)(bh / p.HV) * p.T;
+        s.tok0 = (int64_t)(bh / p.HV) * p.tok_stride;
         s.len = p.T;
         s.nt = p.NT;
         s.rec0 = (int64_t)bh * p.NT;
@@ -418,8 +422,10 @@ bool fused_forward(const Params& p, int ncu);
 hipError_t launch_fused(const Params& p, hipStream_t stream);
 hipError_t fused_abort_count(uint32_t* count, bool reset);
 // The forward is fused or stage 1 then stage 2 (kda_k2.hip); fwd_plan says
-// which on the current device (1 fused, 0 two stages).
+// which on the current device (1 fused, 0 two stages), and fwd_segments in
+// how many segments of consecutive chunks the two stages run.
 int fwd_plan(const Params& p);
+int fwd_segments(const Params& p);
 hipError_t launch_two_stage(const Params& p, hipStream_t stream);
 hipError_t launch_recurrent(const Params& p, hipStream_t stream);
 // Backward (kda_bt16_bwd.hip, and the training variants of the stages).

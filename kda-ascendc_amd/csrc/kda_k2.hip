@@ -1273,9 +1273,73 @@ hipError_t launch_k2(const Params& p, hipStream_t stream) {
 
 int fwd_plan(const Params& p) { return fused_forward(p, cu_count()) ? 1 : 0; }
 
+// Segments of the two-stage forward.  A fixed-length forward whose records
+// outgrow the infinity cache runs stage 1 then stage 2 over consecutive
+// ranges of chunks, each range's records taking the workspace in turn and
+// stage 2 carrying the state from one range to the next: the same
+// arithmetic as one pass (stage 2 resumes from a state bit for bit), with
+// the records stage 2 reads written moments before.  About 150 MB of
+// records a segment, at most 4 segments of at least 64 chunks, where stage
+// 2 runs one or two value tiles per work-group (measured, forward µs for 1
+// / 2 / 4 segments: B=1 T=8192 H=32 261 / 249 / 269; T=16384 H=32 536 /
+// 523 / 499; T=8192 H=16, 143 MB of records, 186 / 190 / 215; T=8192 H=96,
+// four tiles per work-group, 612 / 607 / 625).  Not with packed sequences or
+// debug outputs.
+constexpr int64_t SEGMENT_RECORD_BYTES = 150000000;
+constexpr int MAX_SEGMENTS = 4;
+constexpr int MIN_SEGMENT_CHUNKS = 64;
+
+int fwd_segments(const Params& p) {
+    if (p.cu_seqlens || p.dbg_Aqk) return 1;
+    if (k2_wide_tiles(p, cu_count()) > 2) return 1;
+    const int64_t rec = (int64_t)p.B * p.HV * p.NT * REC_BYTES;
+    int64_t n = (rec + SEGMENT_RECORD_BYTES - 1) / SEGMENT_RECORD_BYTES;
+    n = std::min<int64_t>(n, MAX_SEGMENTS);
+    n = std::min<int64_t>(n, p.NT / MIN_SEGMENT_CHUNKS);
+    return (int)std::max<int64_t>(n, 1);
+}
+
 hipError_t launch_two_stage(const Params& p, hipStream_t stream) {
-    const hipError_t e = launch_k1(p, stream);
-    return e != hipSuccess ? e : launch_k2(p, stream);
+    const int nseg = fwd_segments(p);
+    if (nseg == 1) {
+        const hipError_t e = launch_k1(p, stream);
+        return e != hipSuccess ? e : launch_k2(p, stream);
+    }
+    // Segment s: chunks [NT*s/nseg, NT*(s+1)/nseg).  Its records take the
+    // front of the workspace; the state between segments (V-first) follows
+    // them, which the workspace of the whole forward always has room for
+    // (at least 64 chunks of records per (row, value head) are left over,
+    // against 64 KiB of state).
+    const int64_t pairs = (int64_t)p.B * p.HV;
+    const int64_t seg_chunks = (p.NT + nseg - 1) / nseg;
+    float* state = reinterpret_cast<float*>(
+        p.ws + ((pairs * seg_chunks * REC_BYTES + 255) / 256) * 256);
+    const int gb = p.g_bf16 ? 2 : 4, bb = p.beta_bf16 ? 2 : 4;
+    for (int s = 0; s < nseg; ++s) {
+        const int c0 = (int)((int64_t)p.NT * s / nseg), c1 = (int)((int64_t)p.NT * (s + 1) / nseg);
+        const int64_t t0 = (int64_t)c0 * BT;
+        Params q = p;
+        q.T = (int)std::min<int64_t>(p.T - t0, (int64_t)(c1 - c0) * BT);
+        q.NT = c1 - c0;
+        q.q = p.q + t0 * p.H * DK;
+        q.k = p.k + t0 * p.H * DK;
+        q.v = p.v + t0 * p.HV * DK;
+        q.g = static_cast<const uint8_t*>(p.g) + t0 * p.HV * DK * gb;
+        q.beta = static_cast<const uint8_t*>(p.beta) + t0 * p.HV * bb;
+        q.o = p.o + t0 * p.HV * DK;
+        if (s > 0) {
+            q.h0 = state;
+            q.h0_v_first = 1;
+        }
+        if (s + 1 < nseg) {
+            q.ht = state;
+            q.ht_v_first = 1;
+        }
+        hipError_t e = launch_k1(q, stream);
+        if (e == hipSuccess) e = launch_k2(q, stream);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 hipError_t launch_k2_train(const Params& p, hipStream_t stream) {

@@ -38,6 +38,7 @@ EXPORTED_SYMBOLS = (
     "kda_bt16_workspace_bytes_args",
     "kda_bt16_fwd_hip",
     "kda_bt16_fwd_plan",
+    "kda_bt16_fwd_segments",
     "kda_bt16_fwd_noalloc_hip",
     "kda_bt16_k1_hip",
     "kda_bt16_k2_hip",
@@ -166,6 +167,8 @@ def lib() -> ctypes.CDLL:
                                              ctypes.c_size_t, ctypes.c_void_p]
         h.kda_bt16_fwd_plan.restype = ctypes.c_int
         h.kda_bt16_fwd_plan.argtypes = [ctypes.POINTER(KdaBt16Args)]
+        h.kda_bt16_fwd_segments.restype = ctypes.c_int
+        h.kda_bt16_fwd_segments.argtypes = [ctypes.POINTER(KdaBt16Args)]
         h.kda_bt16_fused_aborts.restype = ctypes.c_int
         h.kda_bt16_fused_aborts.argtypes = [ctypes.POINTER(ctypes.c_uint32), ctypes.c_int32]
         h.kda_bt16_strerror.restype = ctypes.c_char_p
@@ -195,6 +198,16 @@ def fwd_plan(args: KdaBt16Args) -> int:
     rc = int(lib().kda_bt16_fwd_plan(ctypes.byref(args)))
     if rc < 0:
         raise RuntimeError(f"kda_bt16_fwd_plan: {lib().kda_bt16_strerror(rc).decode()}")
+    return rc
+
+
+def fwd_segments(args: KdaBt16Args) -> int:
+    """``kda_bt16_fwd_segments``: 0 if the forward runs fused, else the
+    number of chunk ranges its two stages run in turn (1-4); raises on
+    invalid arguments."""
+    rc = int(lib().kda_bt16_fwd_segments(ctypes.byref(args)))
+    if rc < 0:
+        raise RuntimeError(f"kda_bt16_fwd_segments: {lib().kda_bt16_strerror(rc).decode()}")
     return rc
 
 

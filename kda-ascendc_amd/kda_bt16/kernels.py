@@ -791,8 +791,11 @@ def kda_bt16_stage_launchers(
         _ = keep
         _hip.call("kda_bt16_k1_hip", args, torch.cuda.current_stream(dev).cuda_stream)
 
-    # which kernels kda_bt16_fwd runs for these arguments: "fused" or "two-stage"
+    # which kernels kda_bt16_fwd runs for these arguments: "fused" or
+    # "two-stage", and for the two stages in how many chunk ranges (these
+    # launchers run one pass over all chunks)
     k1.forward_plan = "fused" if _hip.fwd_plan(args) == 1 else "two-stage"
+    k1.forward_segments = _hip.fwd_segments(args)
 
     def k2():
         _ = keep

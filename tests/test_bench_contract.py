@@ -79,6 +79,16 @@ def test_roofline_is_the_dominant_kernels():
                                  124e9, 0.5, True)
     assert r["kernel"].startswith("fused_kernel") and r["traffic"] == 1_430_000_000
     assert r["achieved"] == r["forward"]["achieved"]
+    # two stages in two chunk ranges: times and traffic per launch, half the
+    # algorithmic bytes a launch; the forward's traffic both ranges'
+    kern = {"k1": {"ms": 0.060}, "k2": {"ms": 0.075}}
+    traffic = {"k1": 279_000_000, "k2": 181_000_000}
+    r = bench._dominant_roofline(kern, traffic, 340_000_000, 31e9, 0.25, False, 2)
+    assert r["kernel"].startswith("stage 2") and r["launches_per_forward"] == 2
+    assert r["achieved"] == pytest.approx(170e6 / 0.075 / 1e6, rel=1e-4)
+    assert r["traffic"] == 181_000_000 and r["kernel_ms_events"] == 0.075
+    assert r["forward"]["traffic"] == 920_000_000
+    assert r["forward"]["achieved"] == pytest.approx(340e6 / 0.25 / 1e6, rel=1e-4)
 
 
 def _run(*args):

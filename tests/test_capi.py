@@ -195,6 +195,42 @@ def test_forward_plan_thresholds():
     assert plan(B=5, H=32, HV=32, max_seqlen=16) == 1
 
 
+def test_forward_segments():
+    """kda_bt16_fwd_segments: 0 when the forward runs fused; for the two
+    stages, one chunk range per ~150 MB of records (at most 4, each of at
+    least 64 chunks) where stage 2 runs one or two value tiles per
+    work-group; one pass with packed sequences, debug outputs or wider
+    work-groups.  Without a GPU the library counts 256 CUs.  Pointers are
+    never dereferenced and nothing is launched."""
+    f = _hip.lib().kda_bt16_fwd_segments
+    fake = 1 << 40
+    ten = dict(q=fake, k=fake, v=fake, g=fake, beta=fake, o=fake)
+
+    def segs(**kw):
+        return f(ctypes.byref(_args(**ten, **kw)))
+
+    assert f(None) == -1
+    assert segs(K=64) == -2
+    assert segs(B=16, T=2048, H=32, HV=32) == 0                  # fused
+    assert segs(B=1, T=8192, H=32, HV=32) == 2                    # 285 MB of records
+    assert segs(B=2, T=8192, H=16, HV=16) == 2                    # the same records, two rows
+    assert segs(B=1, T=8192, H=16, HV=32) == 2                    # grouped value heads
+    assert segs(B=1, T=8192, H=16, HV=16) == 1                    # 143 MB
+    assert segs(B=2, T=4096, H=8, HV=8) == 1
+    assert segs(B=1, T=16384, H=32, HV=32) == 4                   # 570 MB
+    assert segs(B=1, T=8192, H=48, HV=48) == 3                    # 2 value tiles per work-group
+    assert segs(B=1, T=8192, H=96, HV=96) == 1                    # 4 value tiles per work-group
+    assert segs(B=1, T=8192, H=32, HV=32, k2_tiles=4) == 1        # forced wider work-groups
+    assert segs(B=1, T=1 << 20, H=1, HV=1) == 4
+    assert segs(B=1, T=4096, H=64, HV=64) == 2                    # 2 tiles, 285 MB
+    assert segs(B=1, T=2048, H=128, HV=128) == 1                  # 4 tiles
+    assert segs(B=1, T=8192, H=32, HV=32, flags=_hip.TWO_STAGE,
+                dbg_Aqk=fake, dbg_A_inv=fake, dbg_w=fake, dbg_u=fake, dbg_g=fake) == 1
+    cu = dict(N=8, T=8192, cu_seqlens=fake, cu_seqlens_dtype=_hip.DTYPE_I32)
+    assert segs(H=16, HV=16, **cu) == 1                           # packed: one pass
+    assert _hip.fwd_segments(_args(B=1, T=8192, H=32, HV=32, **ten)) == 2
+
+
 def test_forward_plan_with_max_seqlen():
     """With cu_seqlens and the longest sequence's length, the choice follows
     the estimated times: the fused kernel's is set by the longest sequence

@@ -1,0 +1,72 @@
+"""The two-stage forward in chunk ranges against one pass, bit for bit.
+
+A fixed-length forward whose stage-1 records would outgrow the GPU's
+last-level cache runs stage 1 then stage 2 on each of 2-4 consecutive chunk
+ranges, stage 2 carrying the state from one range to the next
+(``kda_bt16_fwd_segments``).  Stage 2 resuming from a state gives the bits of
+the uninterrupted recurrence (kernels.py:225-302 run over the chunks in
+order either way), so ``kda_bt16_fwd`` must equal the stage-level entry
+points run once over all chunks (``kda_bt16_stage_launchers``, one pass):
+batch rows (the row stride of a range), a partial last chunk, grouped value
+heads, both state layouts, with and without an initial and a final state,
+and stage 2 at one and at two value tiles per work-group.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from kda_bt16 import forward_choice, kda_bt16_fwd, kda_bt16_stage_launchers
+
+pytestmark = pytest.mark.gpu
+
+# name, B, T, H, HV, initial state, final state, state_v_first, ranges
+CASES = [
+    ("one_row", 1, 8192, 32, 32, False, True, True, 2),
+    ("two_rows_kfirst", 2, 8192, 16, 16, True, True, False, 2),
+    ("partial_last_chunk", 1, 8192 + 37, 32, 32, True, False, True, 2),
+    ("grouped_heads", 1, 8192, 16, 32, True, True, True, 2),
+    ("four_ranges", 1, 16384, 32, 32, False, True, True, 4),
+    ("two_tiles", 1, 4096, 64, 64, True, True, True, 2),
+]
+
+
+def _inputs(B, T, H, HV, seed, dev):
+    gen = torch.Generator().manual_seed(seed)
+    r = lambda *s: torch.randn(*s, generator=gen)
+    return dict(
+        q=r(B, T, H, 128).bfloat16().to(dev), k=r(B, T, H, 128).bfloat16().to(dev),
+        v=r(B, T, HV, 128).bfloat16().to(dev), g=r(B, T, HV, 128).bfloat16().to(dev),
+        beta=r(B, T, HV).bfloat16().to(dev),
+        A_log=torch.log(torch.rand(HV, generator=gen) * 15 + 1).to(dev),
+        dt_bias=(r(HV * 128) * 0.1).to(dev),
+        h0=(r(B, HV, 128, 128) * 0.05).to(dev),
+    )
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_ranges_equal_one_pass(case, gpu_device):
+    name, B, T, H, HV, with_h0, with_ht, svf, ranges = case
+    print(f"[segments] {name}: B={B} T={T} H={H} HV={HV}", flush=True)
+    x = _inputs(B, T, H, HV, seed=len(name), dev=gpu_device)
+    h0 = None
+    if with_h0:
+        h0 = x["h0"] if svf else x["h0"].transpose(-1, -2).contiguous()
+    kw = dict(scale=0.1, initial_state=h0, output_final_state=with_ht, use_qk_l2norm_in_kernel=True,
+              use_gate_in_kernel=True, use_beta_sigmoid_in_kernel=True, lower_bound=-5.0,
+              A_log=x["A_log"], dt_bias=x["dt_bias"], state_v_first=svf)
+    ins = [x[n] for n in ("q", "k", "v", "g", "beta")]
+    k1, k2, o1, ht1 = kda_bt16_stage_launchers(*ins, **kw)
+    assert k1.forward_plan == "two-stage" and k1.forward_segments == ranges, name
+    k1()
+    k2()
+    with forward_choice(fused=False):
+        o, ht = kda_bt16_fwd(*ins, **kw)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o.float()).all(), name
+    assert torch.equal(o.view(torch.int16), o1.view(torch.int16)), f"{name}: o"
+    if with_ht:
+        assert torch.equal(ht.view(torch.int32), ht1.view(torch.int32)), f"{name}: ht"
+    else:
+        assert ht is None and ht1 is None
