@@ -1278,13 +1278,16 @@ int fwd_plan(const Params& p) { return fused_forward(p, cu_count()) ? 1 : 0; }
 // ranges of chunks, each range's records taking the workspace in turn and
 // stage 2 carrying the state from one range to the next: the same
 // arithmetic as one pass (stage 2 resumes from a state bit for bit), with
-// the records stage 2 reads written moments before.  About 150 MB of
-// records a segment, at most 4 segments of at least 64 chunks, where stage
-// 2 runs one or two value tiles per work-group (measured, forward µs for 1
-// / 2 / 4 segments: B=1 T=8192 H=32 261 / 249 / 269; T=16384 H=32 536 /
-// 523 / 499; T=8192 H=16, 143 MB of records, 186 / 190 / 215; T=8192 H=96,
-// four tiles per work-group, 612 / 607 / 625).  Not with packed sequences or
-// debug outputs.
+// the records stage 2 reads written moments before.  Above 200 MB of
+// records, about 150 MB of records a segment, at most 4 segments of at
+// least 64 chunks, where stage 2 runs one or two value tiles per
+// work-group (measured, forward µs for 1 / 2 / 4 segments: B=1 T=8192 H=32
+// 261 / 249 / 269; T=16384 H=32 536 / 523 / 499; T=8192 H=16, 143 MB of
+// records, 186 / 190 / 215; T=8192 H=96, four tiles per work-group, 612 /
+// 607 / 625; for 1 / 2 segments at 178 MB, T=8192 H=20, 199 / 210, and at
+// 214 MB, T=8192 H=24, 221 / 221).  Not with packed sequences or debug
+// outputs.
+constexpr int64_t SEGMENT_MIN_RECORD_BYTES = 200000000;
 constexpr int64_t SEGMENT_RECORD_BYTES = 150000000;
 constexpr int MAX_SEGMENTS = 4;
 constexpr int MIN_SEGMENT_CHUNKS = 64;
@@ -1293,6 +1296,7 @@ int fwd_segments(const Params& p) {
     if (p.cu_seqlens || p.dbg_Aqk) return 1;
     if (k2_wide_tiles(p, cu_count()) > 2) return 1;
     const int64_t rec = (int64_t)p.B * p.HV * p.NT * REC_BYTES;
+    if (rec <= SEGMENT_MIN_RECORD_BYTES) return 1;
     int64_t n = (rec + SEGMENT_RECORD_BYTES - 1) / SEGMENT_RECORD_BYTES;
     n = std::min<int64_t>(n, MAX_SEGMENTS);
     n = std::min<int64_t>(n, p.NT / MIN_SEGMENT_CHUNKS);

@@ -197,10 +197,10 @@ def test_forward_plan_thresholds():
 
 def test_forward_segments():
     """kda_bt16_fwd_segments: 0 when the forward runs fused; for the two
-    stages, one chunk range per ~150 MB of records (at most 4, each of at
-    least 64 chunks) where stage 2 runs one or two value tiles per
-    work-group; one pass with packed sequences, debug outputs or wider
-    work-groups.  Without a GPU the library counts 256 CUs.  Pointers are
+    stages, one pass up to 200 MB of records, above that one chunk range
+    per ~150 MB of records (at most 4, each of at least 64 chunks) where
+    stage 2 runs one or two value tiles per work-group; one pass with packed
+    sequences, debug outputs or wider work-groups.  Without a GPU the library counts 256 CUs.  Pointers are
     never dereferenced and nothing is launched."""
     f = _hip.lib().kda_bt16_fwd_segments
     fake = 1 << 40
@@ -216,6 +216,9 @@ def test_forward_segments():
     assert segs(B=2, T=8192, H=16, HV=16) == 2                    # the same records, two rows
     assert segs(B=1, T=8192, H=16, HV=32) == 2                    # grouped value heads
     assert segs(B=1, T=8192, H=16, HV=16) == 1                    # 143 MB
+    assert segs(B=1, T=8192, H=20, HV=20) == 1                    # 178 MB
+    assert segs(B=1, T=4096, H=40, HV=40) == 1                    # 178 MB, 2 value tiles
+    assert segs(B=1, T=8192, H=24, HV=24) == 2                    # 214 MB
     assert segs(B=2, T=4096, H=8, HV=8) == 1
     assert segs(B=1, T=16384, H=32, HV=32) == 4                   # 570 MB
     assert segs(B=1, T=8192, H=48, HV=48) == 3                    # 2 value tiles per work-group
