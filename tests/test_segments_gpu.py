@@ -70,3 +70,38 @@ def test_ranges_equal_one_pass(case, gpu_device):
         assert torch.equal(ht.view(torch.int32), ht1.view(torch.int32)), f"{name}: ht"
     else:
         assert ht is None and ht1 is None
+
+
+def test_ranges_graph_replays_equal_eager(gpu_device):
+    """The forward in chunk ranges captured into a HIP graph
+    (torch.cuda.CUDAGraph): four launches, the state between ranges carried
+    in the captured workspace.  Each replay, on new inputs copied into the
+    captured buffers with eager work and a synchronisation between replays,
+    equals the eager call bit for bit."""
+    B, T, H, reps = 1, 8192, 32, 2
+    print(f"[segments] graph capture: B={B} T={T} H={H}", flush=True)
+    cases = [_inputs(B, T, H, H, seed=100 + i, dev=gpu_device) for i in range(reps)]
+    names = ("q", "k", "v", "g", "beta", "h0")
+    kw = dict(scale=0.1, output_final_state=True, use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True,
+              use_beta_sigmoid_in_kernel=True, lower_bound=-5.0,
+              A_log=cases[0]["A_log"], dt_bias=cases[0]["dt_bias"])
+    k1, *_ = kda_bt16_stage_launchers(*(cases[0][n] for n in names[:5]), **kw)
+    assert k1.forward_plan == "two-stage" and k1.forward_segments == 2
+    eager = []
+    for x in cases:
+        o, ht = kda_bt16_fwd(*(x[n] for n in names[:5]), initial_state=x["h0"], **kw)
+        eager.append((o.clone(), ht.clone()))
+    torch.cuda.synchronize()
+
+    static = [cases[0][n].clone() for n in names]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        o_static, ht_static = kda_bt16_fwd(*static[:5], initial_state=static[5], **kw)
+    for i, x in enumerate(cases):
+        for dst, n in zip(static, names):
+            dst.copy_(x[n])
+        graph.replay()
+        torch.cuda.synchronize()
+        float(torch.randn(4096, device=gpu_device).square().sum())  # unrelated eager work
+        assert torch.equal(o_static.view(torch.int16), eager[i][0].view(torch.int16)), f"replay {i}: o"
+        assert torch.equal(ht_static.view(torch.int32), eager[i][1].view(torch.int32)), f"replay {i}: ht"
