@@ -191,9 +191,9 @@ int kda_bt16_fwd_plan(const KdaBt16Args* args);
 
 /* In how many segments of consecutive chunks kda_bt16_fwd_hip runs its two
  * stages for these arguments on the current device: 0 when it runs fused,
- * else 1 to 4, or a negative KDA_BT16_E* code for invalid arguments.  A
- * fixed-length forward whose records would outgrow the GPU's last-level
- * cache runs stage 1 then stage 2 on each range of chunks in turn, stage 2
+ * else 1 to 64, or a negative KDA_BT16_E* code for invalid arguments.  A
+ * fixed-length forward with more than 200 MB of records runs stage 1 then
+ * stage 2 on each range of about 150 MB of records in turn, stage 2
  * carrying the state across (results bit for bit those of one pass); every
  * segment's records and the state between them fit the workspace of
  * kda_bt16_workspace_bytes_args.  Reads no device memory.  No counterpart

@@ -1279,22 +1279,23 @@ int fwd_plan(const Params& p) { return fused_forward(p, cu_count()) ? 1 : 0; }
 // stage 2 carrying the state from one range to the next: the same
 // arithmetic as one pass (stage 2 resumes from a state bit for bit), with
 // the records stage 2 reads written moments before.  Above 200 MB of
-// records, about 150 MB of records a segment, at most 4 segments of at
-// least 64 chunks, where stage 2 runs one or two value tiles per
-// work-group (measured, forward µs for 1 / 2 / 4 segments: B=1 T=8192 H=32
-// 261 / 249 / 269; T=16384 H=32 536 / 523 / 499; T=8192 H=16, 143 MB of
-// records, 186 / 190 / 215; T=8192 H=96, four tiles per work-group, 612 /
-// 607 / 625; for 1 / 2 segments at 178 MB, T=8192 H=20, 199 / 210, and at
-// 214 MB, T=8192 H=24, 221 / 221).  Not with packed sequences or debug
-// outputs.
+// records, about 150 MB of records a segment (each of at least 64 chunks;
+// at most 64 segments, a bound on the launches only), whatever stage 2's
+// value tiles per work-group.  Measured, forward µs: B=1 T=8192 H=32 for
+// 1 / 2 / 4 segments 261 / 249 / 269; T=8192 H=16, 143 MB of records, 186 /
+// 190 / 215; T=8192 H=20, 178 MB, 199 / 210 for 1 / 2; T=8192 H=24,
+// 214 MB, 221 / 221; ~100 MB segments lose to ~150 MB ones at every shape
+// tried (c2 263 against 247.5 µs); at four tiles per work-group, T=8192
+// H=96 607 / 597 for 1 / 6 segments (612 / 625 for 1 / 4, ~214 MB each),
+// T=8192 H=80 558 / 530 (1 / 5); at 2.28 GB of records (T=16384 H=128)
+// 1498 / 1431 for 8 / 16.  Not with packed sequences or debug outputs.
 constexpr int64_t SEGMENT_MIN_RECORD_BYTES = 200000000;
 constexpr int64_t SEGMENT_RECORD_BYTES = 150000000;
-constexpr int MAX_SEGMENTS = 4;
+constexpr int MAX_SEGMENTS = 64;
 constexpr int MIN_SEGMENT_CHUNKS = 64;
 
 int fwd_segments(const Params& p) {
     if (p.cu_seqlens || p.dbg_Aqk) return 1;
-    if (k2_wide_tiles(p, cu_count()) > 2) return 1;
     const int64_t rec = (int64_t)p.B * p.HV * p.NT * REC_BYTES;
     if (rec <= SEGMENT_MIN_RECORD_BYTES) return 1;
     int64_t n = (rec + SEGMENT_RECORD_BYTES - 1) / SEGMENT_RECORD_BYTES;

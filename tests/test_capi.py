@@ -198,9 +198,9 @@ def test_forward_plan_thresholds():
 def test_forward_segments():
     """kda_bt16_fwd_segments: 0 when the forward runs fused; for the two
     stages, one pass up to 200 MB of records, above that one chunk range
-    per ~150 MB of records (at most 4, each of at least 64 chunks) where
-    stage 2 runs one or two value tiles per work-group; one pass with packed
-    sequences, debug outputs or wider work-groups.  Without a GPU the library counts 256 CUs.  Pointers are
+    per ~150 MB of records (at most 64, each of at least 64 chunks), at any
+    number of stage-2 value tiles per work-group; one pass with packed
+    sequences or debug outputs.  Without a GPU the library counts 256 CUs.  Pointers are
     never dereferenced and nothing is launched."""
     f = _hip.lib().kda_bt16_fwd_segments
     fake = 1 << 40
@@ -222,11 +222,15 @@ def test_forward_segments():
     assert segs(B=2, T=4096, H=8, HV=8) == 1
     assert segs(B=1, T=16384, H=32, HV=32) == 4                   # 570 MB
     assert segs(B=1, T=8192, H=48, HV=48) == 3                    # 2 value tiles per work-group
-    assert segs(B=1, T=8192, H=96, HV=96) == 1                    # 4 value tiles per work-group
-    assert segs(B=1, T=8192, H=32, HV=32, k2_tiles=4) == 1        # forced wider work-groups
-    assert segs(B=1, T=1 << 20, H=1, HV=1) == 4
+    assert segs(B=1, T=8192, H=96, HV=96) == 6                    # 856 MB, 4 value tiles per work-group
+    assert segs(B=1, T=8192, H=32, HV=32, k2_tiles=4) == 2        # forced wider work-groups
+    assert segs(B=1, T=1 << 20, H=1, HV=1) == 8                   # 1.14 GB
+    assert segs(B=1, T=16384, H=128, HV=128) == 16                # 2.28 GB
+    assert segs(B=1, T=1 << 20, H=16, HV=16) == 64                # 18.3 GB: at most 64
+    assert segs(B=1, T=8192, H=1, HV=1) == 1                      # 8.9 MB
     assert segs(B=1, T=4096, H=64, HV=64) == 2                    # 2 tiles, 285 MB
-    assert segs(B=1, T=2048, H=128, HV=128) == 1                  # 4 tiles
+    assert segs(B=1, T=2048, H=128, HV=128) == 2                  # 285 MB, 4 tiles, 128 chunks
+    assert segs(B=1, T=1024, H=256, HV=256, flags=_hip.TWO_STAGE) == 1  # 64 chunks: no room for two ranges
     assert segs(B=1, T=8192, H=32, HV=32, flags=_hip.TWO_STAGE,
                 dbg_Aqk=fake, dbg_A_inv=fake, dbg_w=fake, dbg_u=fake, dbg_g=fake) == 1
     cu = dict(N=8, T=8192, cu_seqlens=fake, cu_seqlens_dtype=_hip.DTYPE_I32)

@@ -1,15 +1,16 @@
 """The two-stage forward in chunk ranges against one pass, bit for bit.
 
 A fixed-length forward whose stage-1 records would outgrow the GPU's
-last-level cache runs stage 1 then stage 2 on each of 2-4 consecutive chunk
-ranges, stage 2 carrying the state from one range to the next
+last-level cache runs stage 1 then stage 2 on each of 2 or more consecutive
+chunk ranges, stage 2 carrying the state from one range to the next
 (``kda_bt16_fwd_segments``).  Stage 2 resuming from a state gives the bits of
 the uninterrupted recurrence (kernels.py:225-302 run over the chunks in
 order either way), so ``kda_bt16_fwd`` must equal the stage-level entry
 points run once over all chunks (``kda_bt16_stage_launchers``, one pass):
 batch rows (the row stride of a range), a partial last chunk, grouped value
 heads, both state layouts, with and without an initial and a final state,
-and stage 2 at one and at two value tiles per work-group.
+stage 2 at one, two and four value tiles per work-group, and 2 to 16
+ranges.
 """
 
 from __future__ import annotations
@@ -29,19 +30,22 @@ CASES = [
     ("grouped_heads", 1, 8192, 16, 32, True, True, True, 2),
     ("four_ranges", 1, 16384, 32, 32, False, True, True, 4),
     ("two_tiles", 1, 4096, 64, 64, True, True, True, 2),
+    ("four_tiles", 1, 4096, 96, 96, True, True, True, 3),
+    ("c3_four_tiles", 1, 8192, 96, 96, False, True, True, 6),
+    ("sixteen_ranges_kfirst", 1, 16384, 128, 128, True, True, False, 16),
 ]
 
 
 def _inputs(B, T, H, HV, seed, dev):
-    gen = torch.Generator().manual_seed(seed)
-    r = lambda *s: torch.randn(*s, generator=gen)
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    r = lambda *s: torch.randn(*s, generator=gen, device=dev)
     return dict(
-        q=r(B, T, H, 128).bfloat16().to(dev), k=r(B, T, H, 128).bfloat16().to(dev),
-        v=r(B, T, HV, 128).bfloat16().to(dev), g=r(B, T, HV, 128).bfloat16().to(dev),
-        beta=r(B, T, HV).bfloat16().to(dev),
-        A_log=torch.log(torch.rand(HV, generator=gen) * 15 + 1).to(dev),
-        dt_bias=(r(HV * 128) * 0.1).to(dev),
-        h0=(r(B, HV, 128, 128) * 0.05).to(dev),
+        q=r(B, T, H, 128).bfloat16(), k=r(B, T, H, 128).bfloat16(),
+        v=r(B, T, HV, 128).bfloat16(), g=r(B, T, HV, 128).bfloat16(),
+        beta=r(B, T, HV).bfloat16(),
+        A_log=torch.log(torch.rand(HV, generator=gen, device=dev) * 15 + 1),
+        dt_bias=r(HV * 128) * 0.1,
+        h0=r(B, HV, 128, 128) * 0.05,
     )
 
 
