@@ -452,8 +452,7 @@ int kda_bt16_fwd_save_hip(const KdaBt16Args* args, void* saved, size_t saved_byt
     p.la = sv + L.la;
     p.la_stride = kda::LA_BYTES;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (kda::launch_k1_save(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
-    if (kda::launch_k2_train_o(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
+    if (kda::launch_fwd_save(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
     return KDA_BT16_OK;
 }
 

@@ -131,6 +131,12 @@ struct Params {
     // rows, T for whole rows; a segment of the two-stage forward (launch_two_stage)
     // views tokens [t0, t0 + T) of each row with the row stride kept.
     int64_t tok_stride;
+    // Fixed length: chunk c of (row, value head) bh has record slot
+    // bh * srec_stride + srec_off + c in the buffers a training forward
+    // saves (backward record, gram block, h, v_new), srec_stride 0 meaning
+    // NT: a segment of the training forward keeps the whole forward's slots
+    // there while its workspace records are the segment's own.
+    int srec_stride, srec_off;
     float scale, lower_bound;
     int g_bf16, beta_bf16;
     int use_gate, use_l2norm, use_beta_sigmoid;
@@ -199,7 +205,8 @@ __device__ __forceinline__ int cu_at(const Params& p, int i) {
 struct SeqSpan {
     int64_t tok0;
     int len, nt;
-    int64_t rec0;
+    int64_t rec0;   // first record slot in the workspace
+    int64_t srec0;  // first record slot in the saved-state buffers
 };
 
 // bh = (batch row or sequence) * HV + hv.
@@ -213,11 +220,13 @@ __device__ __forceinline__ SeqSpan seq_span(const Params& p, int bh) {
         s.len = eos - bos;
         s.nt = (s.len + BT - 1) / BT;
         s.rec0 = (int64_t)hv * p.NS + bos / BT + n;
+        s.srec0 = s.rec0;
     } else {
         s.tok0 = (int64_t)(bh / p.HV) * p.tok_stride;
         s.len = p.T;
         s.nt = p.NT;
         s.rec0 = (int64_t)bh * p.NT;
+        s.srec0 = (int64_t)bh * (p.srec_stride ? p.srec_stride : p.NT) + p.srec_off;
     }
     return s;
 }
@@ -427,6 +436,7 @@ hipError_t fused_abort_count(uint32_t* count, bool reset);
 int fwd_plan(const Params& p);
 int fwd_segments(const Params& p);
 hipError_t launch_two_stage(const Params& p, hipStream_t stream);
+hipError_t launch_fwd_save(const Params& p, hipStream_t stream);
 hipError_t launch_recurrent(const Params& p, hipStream_t stream);
 // Backward (kda_bt16_bwd.hip, and the training variants of the stages).
 hipError_t launch_k1_both_records(const Params& p, hipStream_t stream);

@@ -87,7 +87,7 @@ __global__ __launch_bounds__(64) void k1_dout_kernel(Params p) {
     Row32 dop;
     load_row(p.dout + (tok * p.HV + hv) * DK, valid, colbase, dop);
     const i16x4 eye = eye_operand(lane);
-    uint8_t* brec = p.ws_bwd + (sp.rec0 + c) * REC_BYTES;
+    uint8_t* brec = p.ws_bwd + (sp.srec0 + c) * REC_BYTES;
 #pragma unroll
     for (int vt = 0; vt < 8; ++vt)
         __builtin_nontemporal_store(__builtin_bit_cast(u32x2, tile_T(dop.v[vt], eye)),

@@ -347,7 +347,7 @@ __device__ __forceinline__ void k1_compute(const Params& p, int hv, int c, const
     const u32x2 ainv_bf = pack4(ainv);  // A = bf16(A_inv), kernels.py:170
     if constexpr (BOTH) {
         // the gram and the inverse for the per-chunk gradients (kda_common.h)
-        uint8_t* la = p.la + (sp.rec0 + c) * p.la_stride;
+        uint8_t* la = p.la + (sp.srec0 + c) * p.la_stride;
         __builtin_nontemporal_store(acc_kk, reinterpret_cast<f32x4*>(la + LA_LRAW + lane * 16));
         __builtin_nontemporal_store(ainv, reinterpret_cast<f32x4*>(la + LA_AINV + lane * 16));
     }
@@ -358,7 +358,7 @@ __device__ __forceinline__ void k1_compute(const Params& p, int hv, int c, const
 
     if constexpr (BOTH) {
         // ---- backward record ---------------------------------------------
-        uint8_t* brec = p.ws_bwd + (sp.rec0 + c) * REC_BYTES;
+        uint8_t* brec = p.ws_bwd + (sp.srec0 + c) * REC_BYTES;
         // Aqk^T as an A operand: lane (r, q4) takes Aqk[4*q4 + i][r], the
         // transpose of what it holds (bf16 rounding commutes with it).
         __builtin_nontemporal_store(__builtin_bit_cast(u32x2, tile_T(aqk_bf, eye)),

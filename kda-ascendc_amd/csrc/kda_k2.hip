@@ -496,7 +496,7 @@ __device__ __forceinline__ void copy_round(const Ctx& cx, int c) {
 template <int NL = LOADS_PER_CHUNK>
 __device__ __forceinline__ void copy_wave(const Params& p, Ctx& cx, const SeqSpan& sp) {
     const int NT = cx.NT;
-    uint8_t* recs = (cx.rev ? p.ws_bwd : p.ws) + sp.rec0 * REC_BYTES;
+    uint8_t* recs = cx.rev ? p.ws_bwd + sp.srec0 * REC_BYTES : p.ws + sp.rec0 * REC_BYTES;
     cx.rs = __builtin_amdgcn_make_buffer_rsrc(recs, (short)0, NT * REC_BYTES, BUF_DWORD3);
     cx.voff16 = cx.lane * 16;
     cx.u_off = REC_U + 512 * cx.vt;
@@ -521,8 +521,8 @@ __device__ __forceinline__ void output_wave(const Params& p, Ctx& cx, const SeqS
         // forward recompute: h and v_new; backward: dh' and dv_new
         uint16_t* bh = cx.rev ? p.tr_dh : p.tr_h;
         uint16_t* bv = cx.rev ? p.tr_dvn : p.tr_vn;
-        cx.trh = bh + sp.rec0 * TR_H_ELEMS + cx.vt * TR_H_TILE + 4 * (x >> 2);
-        cx.trvn = bv + sp.rec0 * TR_VN_ELEMS + cx.vt * TR_VN_TILE + 4 * (x >> 2);
+        cx.trh = bh + sp.srec0 * TR_H_ELEMS + cx.vt * TR_H_TILE + 4 * (x >> 2);
+        cx.trvn = bv + sp.srec0 * TR_VN_ELEMS + cx.vt * TR_VN_TILE + 4 * (x >> 2);
     }
     if constexpr (WITH_O) {
         cx.obase = p.o + (sp.tok0 * p.HV + hv) * DK + col;
@@ -1304,17 +1304,21 @@ int fwd_segments(const Params& p) {
     return (int)std::max<int64_t>(n, 1);
 }
 
-hipError_t launch_two_stage(const Params& p, hipStream_t stream) {
+namespace {
+// Stage 1 then stage 2 (the two launchers) over the forward's segments.
+template <typename K1, typename K2>
+hipError_t run_segments(const Params& p, hipStream_t stream, K1 stage1, K2 stage2) {
     const int nseg = fwd_segments(p);
     if (nseg == 1) {
-        const hipError_t e = launch_k1(p, stream);
-        return e != hipSuccess ? e : launch_k2(p, stream);
+        const hipError_t e = stage1(p, stream);
+        return e != hipSuccess ? e : stage2(p, stream);
     }
     // Segment s: chunks [NT*s/nseg, NT*(s+1)/nseg).  Its records take the
     // front of the workspace; the state between segments (V-first) follows
     // them, which the workspace of the whole forward always has room for
     // (at least 64 chunks of records per (row, value head) are left over,
-    // against 64 KiB of state).
+    // against 64 KiB of state).  A training forward's saved-state slots stay
+    // the whole forward's (srec_stride, srec_off).
     const int64_t pairs = (int64_t)p.B * p.HV;
     const int64_t seg_chunks = (p.NT + nseg - 1) / nseg;
     float* state = reinterpret_cast<float*>(
@@ -1326,6 +1330,8 @@ hipError_t launch_two_stage(const Params& p, hipStream_t stream) {
         Params q = p;
         q.T = (int)std::min<int64_t>(p.T - t0, (int64_t)(c1 - c0) * BT);
         q.NT = c1 - c0;
+        q.srec_stride = p.NT;
+        q.srec_off = c0;
         q.q = p.q + t0 * p.H * DK;
         q.k = p.k + t0 * p.H * DK;
         q.v = p.v + t0 * p.HV * DK;
@@ -1340,11 +1346,22 @@ hipError_t launch_two_stage(const Params& p, hipStream_t stream) {
             q.ht = state;
             q.ht_v_first = 1;
         }
-        hipError_t e = launch_k1(q, stream);
-        if (e == hipSuccess) e = launch_k2(q, stream);
+        hipError_t e = stage1(q, stream);
+        if (e == hipSuccess) e = stage2(q, stream);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
+}
+}  // namespace
+
+hipError_t launch_two_stage(const Params& p, hipStream_t stream) {
+    return run_segments(p, stream, launch_k1, launch_k2);
+}
+
+// The training forward (kda_bt16_fwd_save_hip): o and ht as launch_two_stage,
+// plus the state the backward starts from.
+hipError_t launch_fwd_save(const Params& p, hipStream_t stream) {
+    return run_segments(p, stream, launch_k1_save, launch_k2_train_o);
 }
 
 hipError_t launch_k2_train(const Params& p, hipStream_t stream) {

@@ -109,3 +109,49 @@ def test_ranges_graph_replays_equal_eager(gpu_device):
         float(torch.randn(4096, device=gpu_device).square().sum())  # unrelated eager work
         assert torch.equal(o_static.view(torch.int16), eager[i][0].view(torch.int16)), f"replay {i}: o"
         assert torch.equal(ht_static.view(torch.int32), eager[i][1].view(torch.int32)), f"replay {i}: ht"
+
+
+@pytest.mark.parametrize("B,T,H,HV,ranges", [(1, 8192, 32, 32, 2), (1, 4096, 48, 96, 3)],
+                         ids=["c2_two_ranges", "gva_three_ranges"])
+def test_training_forward_in_ranges(B, T, H, HV, ranges, gpu_device):
+    """The training forward that keeps its state (autograd's default,
+    kda_bt16_fwd_save_hip) runs in the same chunk ranges, its saved state in
+    the whole forward's record slots: o and ht equal the inference
+    forward's, and the gradients from that state equal the recompute
+    path's, which rebuilds the state in one pass, bit for bit."""
+    from kda_bt16 import set_backward_recompute
+
+    print(f"[segments] training forward: B={B} T={T} H={H} HV={HV}", flush=True)
+    x = _inputs(B, T, H, HV, seed=7, dev=gpu_device)
+    names = ("q", "k", "v", "g", "beta", "A_log", "dt_bias", "h0")
+    kw = dict(scale=0.1, output_final_state=True, use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True,
+              use_beta_sigmoid_in_kernel=True, lower_bound=-5.0)
+    k1, *_ = kda_bt16_stage_launchers(*(x[n] for n in names[:5]), initial_state=x["h0"],
+                                      A_log=x["A_log"], dt_bias=x["dt_bias"], **kw)
+    assert k1.forward_plan == "two-stage" and k1.forward_segments == ranges
+    gen = torch.Generator(device=gpu_device).manual_seed(3)
+    do = torch.randn(B, T, HV, 128, generator=gen, device=gpu_device).bfloat16()
+    dht = torch.randn(B, HV, 128, 128, generator=gen, device=gpu_device) * 0.1
+
+    def run(recompute):
+        set_backward_recompute(recompute)
+        lv = {n: x[n].detach().clone().requires_grad_(True) for n in names}
+        o, ht = kda_bt16_fwd(*(lv[n] for n in names[:5]), initial_state=lv["h0"],
+                             A_log=lv["A_log"], dt_bias=lv["dt_bias"], **kw)
+        loss = (o.float() * do.float()).sum() + (ht * dht).sum()
+        return o.detach(), ht.detach(), torch.autograd.grad(loss, [lv[n] for n in names])
+
+    try:
+        o_s, ht_s, g_s = run(False)
+        _, _, g_r = run(True)
+    finally:
+        set_backward_recompute(False)
+    with torch.no_grad():
+        o_i, ht_i = kda_bt16_fwd(*(x[n] for n in names[:5]), initial_state=x["h0"],
+                                 A_log=x["A_log"], dt_bias=x["dt_bias"], **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(o_s.view(torch.int16), o_i.view(torch.int16)), "o"
+    assert torch.equal(ht_s.view(torch.int32), ht_i.view(torch.int32)), "ht"
+    for n, a, b in zip(names, g_s, g_r):
+        assert torch.isfinite(a.float()).all(), n
+        assert torch.equal(a, b), f"d{n}"
