@@ -155,3 +155,53 @@ def test_training_forward_in_ranges(B, T, H, HV, ranges, gpu_device):
     for n, a, b in zip(names, g_s, g_r):
         assert torch.isfinite(a.float()).all(), n
         assert torch.equal(a, b), f"d{n}"
+
+
+def _random_range_cases(n=8, seed=2024):
+    """Seeded shapes whose records exceed 200 MB: batch rows 1-3, value
+    heads 16-64 in groups of 1, 2 or 4, ragged token counts."""
+    import random
+
+    rng = random.Random(seed)
+    cases = []
+    while len(cases) < n:
+        B = rng.choice([1, 1, 2, 3])
+        group = rng.choice([1, 1, 2, 4])
+        HV = rng.choice([16, 24, 32, 48, 64])
+        if HV % group:
+            continue
+        T = rng.randrange(2048, 12000)
+        if B * HV * ((T + 15) // 16) * 17408 <= 210e6:
+            continue
+        cases.append((B, T, HV // group, HV, rng.random() < 0.7, rng.random() < 0.7, rng.random() < 0.5))
+    return cases
+
+
+RANDOM_CASES = _random_range_cases()
+
+
+@pytest.mark.parametrize("case", RANDOM_CASES, ids=[f"B{c[0]}_T{c[1]}_H{c[2]}_HV{c[3]}" for c in RANDOM_CASES])
+def test_ranges_random_shapes(case, gpu_device):
+    """Seeded shapes above 200 MB of records: the forward in chunk ranges
+    equals one pass bit for bit."""
+    B, T, H, HV, with_h0, with_ht, svf = case
+    print(f"[segments] random: B={B} T={T} H={H} HV={HV} h0={with_h0} ht={with_ht} v_first={svf}", flush=True)
+    x = _inputs(B, T, H, HV, seed=T, dev=gpu_device)
+    h0 = None
+    if with_h0:
+        h0 = x["h0"] if svf else x["h0"].transpose(-1, -2).contiguous()
+    kw = dict(scale=0.1, initial_state=h0, output_final_state=with_ht, use_qk_l2norm_in_kernel=True,
+              use_gate_in_kernel=True, use_beta_sigmoid_in_kernel=True, lower_bound=-5.0,
+              A_log=x["A_log"], dt_bias=x["dt_bias"], state_v_first=svf)
+    ins = [x[n] for n in ("q", "k", "v", "g", "beta")]
+    with forward_choice(fused=False):
+        k1, k2, o1, ht1 = kda_bt16_stage_launchers(*ins, **kw)
+        assert k1.forward_segments >= 2
+        k1()
+        k2()
+        o, ht = kda_bt16_fwd(*ins, **kw)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o.float()).all()
+    assert torch.equal(o.view(torch.int16), o1.view(torch.int16)), "o"
+    if with_ht:
+        assert torch.equal(ht.view(torch.int32), ht1.view(torch.int32)), "ht"
