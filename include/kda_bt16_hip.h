@@ -103,7 +103,8 @@ extern "C" {
 #define KDA_BT16_EABI              -5 /* args->abi_version != KDA_BT16_ABI_VERSION */
 #define KDA_BT16_ERANGE            -6 /* lower_bound outside (-11, 0) with USE_GATE (kernels.py:733-744) */
 #define KDA_BT16_ESCRATCH          -7 /* kda_bt16_fwd_noalloc_hip: the geometry needs more than
-                                         KDA_BT16_NOALLOC_MAX_WORKSPACE bytes of records */
+                                         KDA_BT16_NOALLOC_MAX_WORKSPACE bytes of records,
+                                         even in chunk ranges */
 
 /* Size of the static device scratch of kda_bt16_fwd_noalloc_hip (96 MiB:
  * 5782 records of 17 KiB, e.g. B=2 T=4096 H=8, or 92.5k tokens of one
@@ -221,9 +222,13 @@ int kda_bt16_fused_aborts(uint32_t* count, int32_t reset);
  *   - When the forward runs fused (kda_bt16_fwd_plan) it uses no scratch
  *     and takes any size.
  *   - Otherwise the records stage 1 hands to stage 2 live in a file-scope
- *     device array of KDA_BT16_NOALLOC_MAX_WORKSPACE bytes; a geometry that
- *     needs more (kda_bt16_workspace_bytes_args) returns KDA_BT16_ESCRATCH
- *     before any launch.  The first such call on a device looks up the
+ *     device array of KDA_BT16_NOALLOC_MAX_WORKSPACE bytes.  A fixed-length
+ *     geometry whose records do not fit runs its two stages in consecutive
+ *     chunk ranges short enough to fit, with the state between them in the
+ *     array too (B=1 T=8192 H=32: 4 ranges of 128 chunks); packed
+ *     sequences, debug outputs, or so many (row, value head) pairs that not
+ *     even one-chunk ranges fit, return KDA_BT16_ESCRATCH before any
+ *     launch.  The first such call on a device looks up the
  *     array's device address (the runtime places the array on that device
  *     then, and the library holds it until the process ends): make that
  *     first call before capturing calls into a graph.

@@ -385,11 +385,17 @@ int kda_bt16_fwd_noalloc_hip(const KdaBt16Args* args, void* stream) {
     const hipStream_t s = static_cast<hipStream_t>(stream);
     // The fused forward keeps its records in LDS: no scratch, any size.
     if (kda::fwd_plan(p) == 1) return kda::launch_fused(p, s) == hipSuccess ? KDA_BT16_OK : KDA_BT16_ELAUNCH;
-    if (kda_bt16_workspace_bytes_args(args) > KDA_BT16_NOALLOC_MAX_WORKSPACE)
-        return KDA_BT16_ESCRATCH;
+    // The two stages in as many chunk ranges as the forward takes, or more,
+    // shorter ones when that many do not fit the scratch.
+    const int64_t cap = (int64_t)KDA_BT16_NOALLOC_MAX_WORKSPACE;
+    int nseg = kda::fwd_segments(p);
+    const bool fits = nseg == 1 ? kda_bt16_workspace_bytes_args(args) <= (size_t)cap
+                                : kda::segment_bytes(p, nseg) <= cap;
+    if (!fits) nseg = kda::segments_to_fit(p, cap);
+    if (nseg == 0) return KDA_BT16_ESCRATCH;
     rc = scratch_ptr(&p.ws);
     if (rc != KDA_BT16_OK) return rc;
-    if (kda::launch_two_stage(p, s) != hipSuccess) return KDA_BT16_ELAUNCH;
+    if (kda::launch_two_stage_in(p, nseg, s) != hipSuccess) return KDA_BT16_ELAUNCH;
     return KDA_BT16_OK;
 }
 
@@ -505,8 +511,9 @@ const char* kda_bt16_strerror(int code) {
         case KDA_BT16_ERANGE: return "lower_bound must be in (-11, 0) with the in-kernel gate";
         case KDA_BT16_ESCRATCH:
             return "kda_bt16_fwd_noalloc_hip: the geometry needs more records than its static "
-                   "scratch holds (kda_bt16_workspace_bytes_args() > KDA_BT16_NOALLOC_MAX_WORKSPACE, "
-                   "96 MiB); use kda_bt16_fwd_hip with a workspace";
+                   "scratch holds (KDA_BT16_NOALLOC_MAX_WORKSPACE, 96 MiB), even in chunk ranges "
+                   "(packed sequences and debug outputs run in one pass); use kda_bt16_fwd_hip "
+                   "with a workspace";
         default: return "unknown error";
     }
 }

@@ -437,6 +437,9 @@ int fwd_plan(const Params& p);
 int fwd_segments(const Params& p);
 hipError_t launch_two_stage(const Params& p, hipStream_t stream);
 hipError_t launch_fwd_save(const Params& p, hipStream_t stream);
+int64_t segment_bytes(const Params& p, int nseg);
+int segments_to_fit(const Params& p, int64_t max_bytes);
+hipError_t launch_two_stage_in(const Params& p, int nseg, hipStream_t stream);
 hipError_t launch_recurrent(const Params& p, hipStream_t stream);
 // Backward (kda_bt16_bwd.hip, and the training variants of the stages).
 hipError_t launch_k1_both_records(const Params& p, hipStream_t stream);

@@ -1307,8 +1307,7 @@ int fwd_segments(const Params& p) {
 namespace {
 // Stage 1 then stage 2 (the two launchers) over the forward's segments.
 template <typename K1, typename K2>
-hipError_t run_segments(const Params& p, hipStream_t stream, K1 stage1, K2 stage2) {
-    const int nseg = fwd_segments(p);
+hipError_t run_segments(const Params& p, int nseg, hipStream_t stream, K1 stage1, K2 stage2) {
     if (nseg == 1) {
         const hipError_t e = stage1(p, stream);
         return e != hipSuccess ? e : stage2(p, stream);
@@ -1322,7 +1321,7 @@ hipError_t run_segments(const Params& p, hipStream_t stream, K1 stage1, K2 stage
     const int64_t pairs = (int64_t)p.B * p.HV;
     const int64_t seg_chunks = (p.NT + nseg - 1) / nseg;
     float* state = reinterpret_cast<float*>(
-        p.ws + ((pairs * seg_chunks * REC_BYTES + 255) / 256) * 256);
+        p.ws + ((pairs * seg_chunks * REC_BYTES + 255) / 256) * 256);  // segment_bytes
     const int gb = p.g_bf16 ? 2 : 4, bb = p.beta_bf16 ? 2 : 4;
     for (int s = 0; s < nseg; ++s) {
         const int c0 = (int)((int64_t)p.NT * s / nseg), c1 = (int)((int64_t)p.NT * (s + 1) / nseg);
@@ -1355,13 +1354,35 @@ hipError_t run_segments(const Params& p, hipStream_t stream, K1 stage1, K2 stage
 }  // namespace
 
 hipError_t launch_two_stage(const Params& p, hipStream_t stream) {
-    return run_segments(p, stream, launch_k1, launch_k2);
+    return run_segments(p, fwd_segments(p), stream, launch_k1, launch_k2);
+}
+
+// Workspace bytes of a fixed-length forward in nseg > 1 segments: one
+// segment's records, then the state carried between segments.
+int64_t segment_bytes(const Params& p, int nseg) {
+    const int64_t pairs = (int64_t)p.B * p.HV;
+    const int64_t seg_chunks = (p.NT + nseg - 1) / nseg;
+    return (pairs * seg_chunks * REC_BYTES + 255) / 256 * 256 + pairs * DK * DK * 4;
+}
+
+// The fewest segments, at least fwd_segments' count, whose workspace fits
+// max_bytes (segments as short as one chunk), or 0 when none does or the
+// forward cannot run in segments (packed sequences, debug outputs).
+int segments_to_fit(const Params& p, int64_t max_bytes) {
+    if (p.cu_seqlens || p.dbg_Aqk) return 0;
+    for (int n = std::max(2, fwd_segments(p)); n <= p.NT; ++n)
+        if (segment_bytes(p, n) <= max_bytes) return n;
+    return 0;
+}
+
+hipError_t launch_two_stage_in(const Params& p, int nseg, hipStream_t stream) {
+    return run_segments(p, nseg, stream, launch_k1, launch_k2);
 }
 
 // The training forward (kda_bt16_fwd_save_hip): o and ht as launch_two_stage,
 // plus the state the backward starts from.
 hipError_t launch_fwd_save(const Params& p, hipStream_t stream) {
-    return run_segments(p, stream, launch_k1_save, launch_k2_train_o);
+    return run_segments(p, fwd_segments(p), stream, launch_k1_save, launch_k2_train_o);
 }
 
 hipError_t launch_k2_train(const Params& p, hipStream_t stream) {

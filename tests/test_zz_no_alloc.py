@@ -3,8 +3,9 @@ static device scratch instead of a workspace.  It must give what
 kda_bt16_fwd_hip gives, bit for bit, on consecutive calls that leave the
 scratch holding the previous call's records (each call here is smaller than
 the one before), take a fused geometry of any size (the fused forward keeps
-its records in LDS), and refuse a two-stage geometry that does not fit
-before any launch.
+its records in LDS), run a fixed-length two-stage geometry whose records
+outgrow the scratch in chunk ranges that fit, and refuse one that cannot
+fit even so before any launch.
 """
 
 from __future__ import annotations
@@ -36,12 +37,19 @@ def test_noalloc_refuses_oversized_geometry_without_launching():
     fake = 1 << 40  # never dereferenced: the size check fails before any launch
     full = dict(q=fake, k=fake, v=fake, g=fake, beta=fake, o=fake)
     f = _hip.lib().kda_bt16_fwd_noalloc_hip
-    # B=1 T=8192 HV=32 needs 272 MiB of records, on the two-stage path (a
-    # fused geometry would launch: checked first, and the call skipped)
-    a = _args(B=1, T=8192, H=32, HV=32, flags=_hip.TWO_STAGE, **full)
+    # on the two-stage path (a fused geometry would launch: checked first)
+    # 1280 (row, value head) pairs carry 80 MiB of state between chunk
+    # ranges: with one chunk's records it outgrows the scratch
+    a = _args(B=1, T=2048, H=1280, HV=1280, flags=_hip.TWO_STAGE, **full)
     assert _hip.workspace_bytes_args(a) > _hip.NOALLOC_MAX_WORKSPACE
+    assert 1280 * (17408 + 128 * 128 * 4) > _hip.NOALLOC_MAX_WORKSPACE
     assert _hip.fwd_plan(a) == 0
     assert f(ctypes.byref(a), None) == _hip.ESCRATCH
+    # packed sequences run in one pass: 272 MiB of records do not fit
+    v = _args(B=1, T=8192, H=32, HV=32, N=8, cu_seqlens=fake, cu_seqlens_dtype=_hip.DTYPE_I32,
+              flags=_hip.TWO_STAGE, **full)
+    assert _hip.workspace_bytes_args(v) > _hip.NOALLOC_MAX_WORKSPACE
+    assert f(ctypes.byref(v), None) == _hip.ESCRATCH
     assert b"static" in _hip.lib().kda_bt16_strerror(_hip.ESCRATCH)
     # the ordinary argument checks come first
     assert f(None, None) == -1
@@ -86,9 +94,10 @@ def _run_both(c, dev):
     ht = torch.full((S, HV, 128, 128), float("nan"), dtype=torch.float32, device=dev)
     args = _make_args(q, k, v, g, beta, 0.1, -5.0, A_log, dt_bias, h0, o, ht, None, 0,
                       _flags(True, True, True, c["svf"]), None, cu)
-    # a two-stage geometry fits the scratch; a fused one needs none
+    # a two-stage geometry fits the scratch, or runs in chunk ranges that
+    # do (fixed length); a fused one needs none
     assert (_hip.workspace_bytes_args(args) <= _hip.NOALLOC_MAX_WORKSPACE
-            or _hip.fwd_plan(args) == 1)
+            or _hip.fwd_plan(args) == 1 or cu is None)
     _hip.call("kda_bt16_fwd_noalloc_hip", args, torch.cuda.current_stream(dev).cuda_stream)
     torch.cuda.synchronize(dev)
     return (o_ref, ht_ref), (o, ht)
@@ -97,6 +106,9 @@ def _run_both(c, dev):
 @pytest.mark.gpu
 def test_noalloc_equals_fwd_on_consecutive_calls(gpu_device):
     cases = [
+        # two stages, 272 MiB of records: in chunk ranges that fit the
+        # scratch (3 of 171 chunks, 95 MB of records and the state)
+        ("B1_T8192_H32_ranges", _case(1, 8192, 32, 32, seed=8, h0=True, svf=True)),
         # fused (512 (sequence, head) pairs): 16384 records' worth (272 MiB),
         # more than the scratch holds, which the fused forward does not use
         ("B16_T512_H32_fused", _case(16, 512, 32, 32, seed=7, h0=True, svf=True)),
