@@ -225,7 +225,7 @@ int kda_bt16_fused_aborts(uint32_t* count, int32_t reset);
  *     device array of KDA_BT16_NOALLOC_MAX_WORKSPACE bytes.  A fixed-length
  *     geometry whose records do not fit runs its two stages in consecutive
  *     chunk ranges short enough to fit, with the state between them in the
- *     array too (B=1 T=8192 H=32: 4 ranges of 128 chunks); packed
+ *     array too (B=1 T=8192 H=32: 3 ranges of 170-171 chunks); packed
  *     sequences, debug outputs, or so many (row, value head) pairs that not
  *     even one-chunk ranges fit, return KDA_BT16_ESCRATCH before any
  *     launch.  The first such call on a device looks up the
