@@ -205,3 +205,33 @@ def test_ranges_random_shapes(case, gpu_device):
     assert torch.equal(o.view(torch.int16), o1.view(torch.int16)), "o"
     if with_ht:
         assert torch.equal(ht.view(torch.int32), ht1.view(torch.int32)), "ht"
+
+
+@pytest.mark.parametrize("mode", ["fp32_gate_beta", "precomputed_gate"])
+def test_ranges_gate_forms(mode, gpu_device):
+    """The range offsets of g and beta follow their element type (fp32 g and
+    beta here), and a precomputed gate (no in-kernel gate, kernels.py:116-124
+    with USE_GATE off) runs in ranges too: bit for bit against one pass."""
+    B, T, H = 1, 8192 + 5, 32
+    print(f"[segments] {mode}: B={B} T={T} H={H}", flush=True)
+    x = _inputs(B, T, H, H, seed=11, dev=gpu_device)
+    if mode == "fp32_gate_beta":
+        g, beta = x["g"].float(), x["beta"].float()
+        kw = dict(use_gate_in_kernel=True, lower_bound=-5.0, A_log=x["A_log"], dt_bias=x["dt_bias"])
+    else:
+        # a precomputed gate: small non-positive values, no in-kernel gate
+        g = (-torch.nn.functional.softplus(x["g"].float()) * 0.1).bfloat16()
+        beta = x["beta"]
+        kw = dict(use_gate_in_kernel=False)
+    kw.update(scale=0.1, initial_state=x["h0"], output_final_state=True, use_qk_l2norm_in_kernel=True,
+              use_beta_sigmoid_in_kernel=True)
+    ins = [x["q"], x["k"], x["v"], g, beta]
+    k1, k2, o1, ht1 = kda_bt16_stage_launchers(*ins, **kw)
+    assert k1.forward_plan == "two-stage" and k1.forward_segments == 2
+    k1()
+    k2()
+    o, ht = kda_bt16_fwd(*ins, **kw)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o.float()).all()
+    assert torch.equal(o.view(torch.int16), o1.view(torch.int16)), "o"
+    assert torch.equal(ht.view(torch.int32), ht1.view(torch.int32)), "ht"
